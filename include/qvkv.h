@@ -1,0 +1,264 @@
+/*
+ * qvkv: the paged KV-cache hot path on one MI355X (gfx950), as a C ABI.
+ *
+ * This header is the drop-in boundary.  In the reference (kentmarete/qubivex, Rust) the
+ * path sits behind `trait DiscreteDevice` (crates/qubivex-compute/src/discrete.rs:433-570),
+ * which the runtime's `OnDevice` (crates/qubivex-runtime/src/discrete.rs) drives.  Each
+ * entry point below names the trait method or reference function it replaces.
+ *
+ * Conventions
+ *  - Every call returns a status: QVKV_OK or one of the QVKV_E_* codes, which mirror the
+ *    `ComputeError` variants (crates/qubivex-compute/src/lib.rs:28-83).  The detail of
+ *    the last failure on the calling thread is returned by qvkv_last_error().
+ *  - Handles are opaque.  Host pointers are borrowed for the duration of the call.
+ *  - Functions without the `_async` suffix take HOST memory, run on the device's own
+ *    stream and complete before they return (the trait's "completes before return"
+ *    semantics, crates/qubivex-backend-vulkan/src/lib.rs:212-225).
+ *  - `_async` functions take DEVICE pointers and enqueue on `stream` (a hipStream_t, or
+ *    NULL for the device's own stream).  Index errors found by a kernel (a block id
+ *    past the pool, a table too short) are latched on the device and reported by the
+ *    next qvkv_check().  Kernels never touch memory outside the pool for such input.
+ *  - A pool position is `slot = block * layout.block + offset` (the reference's
+ *    `sync_to`, crates/qubivex-compute/src/discrete.rs:301-304).  Item t of a batch is
+ *    one (sequence, layer) pair: its blocks are blocks[table_at[t] ..], in position order
+ *    (crates/qubivex-compute/src/discrete.rs:257-266).
+ */
+#ifndef QVKV_H
+#define QVKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes: ComputeError (crates/qubivex-compute/src/lib.rs:28-83) ---- */
+#define QVKV_OK 0
+#define QVKV_E_SHAPE 1       /* ComputeError::Shape */
+#define QVKV_E_UNSUPPORTED 2 /* ComputeError::Unsupported */
+#define QVKV_E_OOM 3         /* ComputeError::OutOfDeviceMemory */
+#define QVKV_E_DEVICE 4      /* ComputeError::Device */
+
+/* ---- storage dtypes (crates/qubivex-core/src/dtype.rs:19-29: F32, F16, Q8_0) ---- */
+#define QVKV_F32 0
+#define QVKV_F16 1
+#define QVKV_Q8_0 2
+
+/* The pool's storage layout.  One block holds `block` positions of one layer: keys and
+ * values of every KV head.  Replaces the reference's fixed KV_BLOCK = 256 f32 layout
+ * (crates/qubivex-compute/src/discrete.rs:247-255).  block must be a multiple of 16;
+ * head_dim a multiple of 8 (f16) or of 32 (q8_0). */
+typedef struct qvkv_layout {
+    uint32_t dtype;    /* QVKV_F16 or QVKV_Q8_0 */
+    uint32_t kv_heads; /* G */
+    uint32_t head_dim; /* d */
+    uint32_t block;    /* B, positions per block */
+} qvkv_layout;
+
+typedef struct qvkv_dev qvkv_dev;
+typedef struct qvkv_buf qvkv_buf;
+
+/* Memory now: DiscreteDevice::usage (crates/qubivex-compute/src/discrete.rs:461). */
+typedef struct qvkv_usage_t {
+    uint64_t capacity, used, peak, refused;
+} qvkv_usage_t;
+
+/* Copies so far: TransferStats (crates/qubivex-compute/src/discrete.rs:376-427). */
+typedef struct qvkv_transfers_t {
+    uint64_t uploads, upload_bytes, downloads, download_bytes, submissions, wait_ns;
+} qvkv_transfers_t;
+
+/* Detail of the calling thread's last failure (ComputeError's Display). Returns the
+ * status of that failure. */
+int qvkv_last_error(char *buf, size_t len);
+
+/* ---- device and memory ---- */
+
+/* Opens HIP device `device` with its own stream (constructor of the backend;
+ * DiscreteDevice::name/describe: crates/qubivex-compute/src/discrete.rs:437-441). */
+int qvkv_open(int device, qvkv_dev **out);
+void qvkv_close(qvkv_dev *dev);
+int qvkv_describe(const qvkv_dev *dev, char *buf, size_t len);
+/* DiscreteDevice::usage (discrete.rs:461) */
+int qvkv_usage(const qvkv_dev *dev, qvkv_usage_t *out);
+/* DiscreteDevice::transfers (discrete.rs:464) */
+int qvkv_transfers(const qvkv_dev *dev, qvkv_transfers_t *out);
+/* The device's own stream (a hipStream_t). */
+void *qvkv_stream(const qvkv_dev *dev);
+
+/* DiscreteDevice::alloc (discrete.rs:500-508): `len` bytes, contents unspecified. */
+int qvkv_alloc(qvkv_dev *dev, size_t len, qvkv_buf **out);
+/* Drop of the last DeviceBuffer clone (discrete.rs:24-95). */
+void qvkv_free(qvkv_buf *buf);
+void *qvkv_buf_ptr(const qvkv_buf *buf);
+size_t qvkv_buf_len(const qvkv_buf *buf);
+/* DiscreteDevice::write (discrete.rs:510-523): host bytes into `buf` at `offset`. */
+int qvkv_write(qvkv_dev *dev, qvkv_buf *buf, size_t offset, const void *host, size_t len);
+/* Device bytes back to the host (the readback of k_new/v_new in the reference). */
+int qvkv_read(qvkv_dev *dev, const qvkv_buf *buf, size_t offset, void *host, size_t len);
+/* Waits for `stream` (NULL: the device's) and reports any index error a kernel latched
+ * since the last check (QVKV_E_SHAPE), clearing it. */
+int qvkv_check(qvkv_dev *dev, void *stream);
+
+/* ---- layout ---- */
+
+/* Bytes of one block: f16 2*B*G*d*2; q8_0 2*B*G*d*34/32.  Replaces kv_block_words
+ * (crates/qubivex-compute/src/discrete.rs:254-256). */
+int qvkv_block_bytes(const qvkv_layout *layout, uint64_t *out);
+
+/* ---- the hot path, device pointers ---- */
+
+/* Append: writes n rows (k[r], v[r]: G*d f32 each, [kv_head][d]) at pool positions
+ * slots[r], narrowing to the storage dtype (f16 RNE; q8_0 quantize-on-write over each
+ * head's 32-value groups).  Rows may belong to any sequence and layer.  Replaces the
+ * pool store of SimDevice::attention (crates/qubivex-backend-cpu/src/sim.rs:377-399),
+ * kv_sync.comp:40-50 and the store in attn_prelude.comp:166-173. */
+int qvkv_append_async(qvkv_dev *dev, const qvkv_layout *layout, void *pool,
+                      uint64_t pool_blocks, const float *k, const float *v,
+                      const uint32_t *slots, uint32_t n, void *stream);
+
+/* Gather: for each item t, positions 0..lens[t]-1 through its block table into
+ * out_k/out_v at position offset out_at[t] (elements out_at[t]*G*d), head-major
+ * [kv_head][lens[t]][d].  out_dtype QVKV_F16 (f16 pools only: a byte copy) or QVKV_F32
+ * (the logical values: widened f16 or dequantized q8_0).  out_positions bounds
+ * out_at[t] + lens[t].  Replaces the gather of SimDevice::attention (sim.rs:404-422)
+ * and KvCache::heads (crates/qubivex-arch/src/lib.rs:519-525). */
+int qvkv_gather_async(qvkv_dev *dev, const qvkv_layout *layout, const void *pool,
+                      uint64_t pool_blocks, const uint32_t *blocks, uint64_t n_table,
+                      const uint32_t *table_at, const uint32_t *lens, const uint64_t *out_at,
+                      uint32_t n_items, uint32_t max_len, uint32_t out_dtype,
+                      uint64_t out_positions, void *out_k, void *out_v, void *stream);
+
+/* Decode attention: for item t and query head h, softmax(q.K^T / sqrt(d)) V over
+ * positions 0..pos[t] of KV head h / (heads/G), read through the block table.
+ * q, out: [n_items][heads][d] f32.  max_pos bounds every pos[t] (it sizes the launch).
+ * fp32 accumulation; within 2e-3 max-abs and 1e-3 rel-L2 of math::attend.  Replaces
+ * the attention of SimDevice::attention (sim.rs:423-428 with math::attend,
+ * crates/qubivex-compute/src/math.rs:142-155) and attn_decode.comp. */
+int qvkv_attention_async(qvkv_dev *dev, const qvkv_layout *layout, const void *pool,
+                         uint64_t pool_blocks, const float *q, const uint32_t *blocks,
+                         uint64_t n_table, const uint32_t *table_at, const uint32_t *pos,
+                         uint32_t n_items, uint32_t heads, uint32_t max_pos, float *out,
+                         void *stream);
+
+/* Block copy: block src[i] -> block dst[i], i < n, byte for byte (copy-on-write of a
+ * shared block; compaction moves).  No dst may appear twice or also be a src in the
+ * same call.  No reference counterpart: the reference copies a whole prefix instead
+ * (KvCache::restore_from, crates/qubivex-arch/src/lib.rs:409-432). */
+int qvkv_block_copy_async(qvkv_dev *dev, const qvkv_layout *layout, void *pool,
+                          uint64_t pool_blocks, const uint32_t *src, const uint32_t *dst,
+                          uint32_t n, void *stream);
+
+/* ---- the hot path, host memory (synchronous; what the Rust backend binds) ---- */
+
+/* qvkv_append_async with host rows and slots. */
+int qvkv_append(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *pool, const float *k,
+                const float *v, const uint32_t *slots, uint32_t n);
+
+/* qvkv_gather_async with host tables and host outputs. */
+int qvkv_gather(qvkv_dev *dev, const qvkv_layout *layout, const qvkv_buf *pool,
+                const uint32_t *blocks, uint64_t n_table, const uint32_t *table_at,
+                const uint32_t *lens, const uint64_t *out_at, uint32_t n_items,
+                uint32_t out_dtype, uint64_t out_positions, void *out_k, void *out_v);
+
+/* qvkv_block_copy_async with host id lists. */
+int qvkv_block_copy(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *pool,
+                    const uint32_t *src, const uint32_t *dst, uint32_t n);
+
+/* The KV part of one DeviceMoeAttention submission
+ * (crates/qubivex-compute/src/discrete.rs:257-307; SimDevice::attention, sim.rs:301-436):
+ * first the n_sync host rows (`sync`: n_sync * 2*G*d f32, key row then value row) to
+ * `sync_to`, then token t's k_new/v_new row at its own position pos[t], then attention
+ * of q over positions 0..=pos[t].  q, out: [s][heads][d]; k_new, v_new: [s][G*d].
+ * blocks/table_at/pos as AttnPlan (crates/qubivex-runtime/src/discrete.rs:284-290). */
+int qvkv_decode_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *pool,
+                          const float *q, uint32_t heads, const uint32_t *pos, uint32_t s,
+                          const uint32_t *blocks, uint64_t n_table, const uint32_t *table_at,
+                          const float *sync, const uint32_t *sync_to, uint32_t n_sync,
+                          const float *k_new, const float *v_new, float *out);
+
+/* ---- host pool manager: block pool, block tables, sharing, eviction, compaction ----
+ *
+ * The host side of the path, above the kernels: the reference's KvPool / KvFree /
+ * Mirror / attention_plan (crates/qubivex-runtime/src/discrete.rs:209-290,951-1009),
+ * generalised with per-block reference counts (prefix sharing with copy-on-write),
+ * last-use ticks (LRU eviction) and compaction.  A pool owns one device allocation of
+ * n_blocks blocks.  Sequences are small integer handles; each holds, per layer, a block
+ * table and the number of positions written.  Not thread-safe per pool: the caller
+ * serialises calls on one pool (the reference holds its free-list mutex likewise). */
+
+typedef struct qvkv_pool qvkv_pool;
+
+/* Counters: KvPoolStats (crates/qubivex-runtime/src/discrete.rs:92-108) plus the
+ * sharing and compaction counters this path adds. */
+typedef struct qvkv_pool_stats_t {
+    uint64_t bytes, blocks, free, layers, synced_rows, full;
+    uint64_t shared_blocks, cow_copies, evicted_blocks, moved_blocks;
+} qvkv_pool_stats_t;
+
+/* A pool of n_blocks blocks (OnDevice::new pool sizing, discrete.rs:429-455; the free
+ * list starts (0..n).rev() so the first pop is block 0, :448).  Allocates the device
+ * memory now.  dev == NULL makes a host-only pool: the same bookkeeping with no device
+ * memory, whose block copies are recorded for qvkv_pool_take_copies instead of run
+ * (a planner, and the CPU-side test double of the runtime's SimDevice). */
+int qvkv_pool_create(qvkv_dev *dev, const qvkv_layout *layout, uint64_t n_blocks,
+                     uint32_t n_layers, qvkv_pool **out);
+/* Host-only pools: the block copies (src, dst) issued since the last call, in issue
+ * order (each batch's pairs are independent).  *n receives the count pending; at most
+ * cap pairs are returned and removed. */
+int qvkv_pool_take_copies(qvkv_pool *pool, uint32_t *src, uint32_t *dst, uint64_t cap,
+                          uint64_t *n);
+void qvkv_pool_destroy(qvkv_pool *pool);
+void *qvkv_pool_ptr(const qvkv_pool *pool);
+int qvkv_pool_stats(const qvkv_pool *pool, qvkv_pool_stats_t *out);
+
+/* A new empty sequence (a KvCache's mirror, discrete.rs:247-280). */
+int qvkv_seq_create(qvkv_pool *pool, uint32_t *seq);
+/* Gives every block of `seq` back (Mirror::release / Drop, discrete.rs:267-280). */
+int qvkv_seq_release(qvkv_pool *pool, uint32_t seq);
+/* A new sequence sharing the first `positions` positions of `parent` on every layer:
+ * the blocks holding them gain a reference (no copy).  A later write into a shared
+ * block copies it first.  Replaces KvCache::restore_from's copy
+ * (crates/qubivex-arch/src/lib.rs:409-432) as ADR-016 describes. */
+int qvkv_seq_fork(qvkv_pool *pool, uint32_t parent, uint32_t positions, uint32_t *child);
+/* Positions held by `seq` on `layer`. */
+int qvkv_seq_len(const qvkv_pool *pool, uint32_t seq, uint32_t layer, uint32_t *out);
+/* Marks the sequence used now (LRU clock; PrefixCache `used`,
+ * crates/qubivex-kv-cache/src/lib.rs:30-31). */
+int qvkv_seq_touch(qvkv_pool *pool, uint32_t seq);
+
+/* Plans writes of `count[i]` new positions for seqs[i] on `layer` (the positions
+ * len..len+count-1): grows each table from the free list, and copies-on-write a shared
+ * block that a write lands in (the COW pairs are copied on the device before this
+ * returns).  slots_out receives sum(count) pool positions, seq-major.  Returns
+ * QVKV_E_OOM with nothing changed for the failing sequence (`pool.full` counts it;
+ * discrete.rs:882-891) when the free list runs dry.  attention_plan's growth step
+ * (discrete.rs:988-994). */
+int qvkv_pool_plan_append(qvkv_pool *pool, const uint32_t *seqs, const uint32_t *count,
+                          uint32_t n_seqs, uint32_t layer, uint32_t *slots_out);
+/* Flattened block tables of seqs[i] on `layer` (AttnPlan.blocks/table_at/pos,
+ * discrete.rs:995-997).  blocks_cap bounds blocks_out; *n_table_out receives the
+ * entries written; pos_out[i] = len-1 (the newest position). */
+int qvkv_pool_tables(const qvkv_pool *pool, const uint32_t *seqs, uint32_t n_seqs,
+                     uint32_t layer, uint32_t *blocks_out, uint64_t blocks_cap,
+                     uint64_t *n_table_out, uint32_t *table_at_out, uint32_t *pos_out);
+/* Releases least-recently-used sequences (PrefixCache::evict_oldest,
+ * crates/qubivex-kv-cache/src/lib.rs:197-213; ties: the lower handle) until at least
+ * `target_blocks` blocks have returned to the free list or none is left; writes the
+ * released handles to released_out (cap entries) and their count. */
+int qvkv_pool_evict_lru(qvkv_pool *pool, uint64_t target_blocks, uint32_t *released_out,
+                        uint32_t cap, uint32_t *n_released);
+/* Moves every live block into the ids 0..live-1 in the order of a permutation drawn
+ * from `seed` (seed 0: ascending by current id), rewriting every table and the free
+ * list, with cycle-safe batches of the block-copy kernel.  *moved receives the blocks
+ * moved. */
+int qvkv_pool_compact(qvkv_pool *pool, uint64_t seed, uint64_t *moved);
+/* Reference count of one block (0 = free). */
+int qvkv_pool_refcount(const qvkv_pool *pool, uint32_t block, uint32_t *out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QVKV_H */

@@ -1,0 +1,61 @@
+"""Builds libqvkv.so (HIP kernels + C ABI + host pool manager) for gfx950, in-tree.
+
+hipcc cross-compiles without a GPU.  All HIP code is built with packed-fp32 code
+generation turned off (-packed-fp32-ops), and with the default IEEE float semantics
+(correctly rounded f32 division, no fast-math): the append path must be bit-exact.
+"""
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+OUT_DIR = os.path.join(HERE, "lib")
+LIB = os.path.join(OUT_DIR, "libqvkv.so")
+ARCH = os.environ.get("QVKV_ARCH", "gfx950")
+
+HIP_SOURCES = ["kernels.hip", "abi.hip"]
+CXX_SOURCES = ["pool.cpp"]
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+
+
+def build(verbose: bool = False, jobs: int = 4) -> str:
+    os.makedirs(OUT_DIR, exist_ok=True)
+    obj_dir = os.path.join(OUT_DIR, "obj")
+    os.makedirs(obj_dir, exist_ok=True)
+    inc = ["-I", os.path.join(ROOT, "include"), "-I", CSRC]
+    common = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function"]
+    procs, objs = [], []
+    for src in HIP_SOURCES:
+        obj = os.path.join(obj_dir, src + ".o")
+        objs.append(obj)
+        cmd = ["hipcc", f"--offload-arch={ARCH}", "-c", *common, *inc,
+               "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+               "-fno-gpu-rdc", os.path.join(CSRC, src), "-o", obj]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append(subprocess.Popen(cmd))
+    for src in CXX_SOURCES:
+        obj = os.path.join(obj_dir, src + ".o")
+        objs.append(obj)
+        cmd = ["hipcc", "-c", *common, *inc, "-I", "/opt/rocm/include", "-D__HIP_PLATFORM_AMD__", "-x", "c++", os.path.join(CSRC, src), "-o", obj]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append(subprocess.Popen(cmd))
+    failed = [p.args for p in procs if p.wait() != 0]
+    if failed:
+        raise RuntimeError(f"build failed: {failed[0]}")
+    tmp = LIB + ".tmp"
+    _run(["hipcc", f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp], verbose)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

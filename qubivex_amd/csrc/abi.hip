@@ -1,0 +1,627 @@
+// The C ABI of include/qvkv.h: device handle, memory, staging of host arguments, and
+// the kernel entry points (device-pointer `_async` forms and host-memory forms).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "internal.h"
+#include "qvkv.h"
+
+using qvkv::Geometry;
+
+namespace {
+
+thread_local std::string g_err;
+thread_local int g_err_code = QVKV_OK;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    g_err_code = code;
+    return code;
+}
+
+}  // namespace
+
+int qvkv::set_error(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    g_err_code = code;
+    return code;
+}
+
+namespace {
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(QVKV_E_DEVICE, "hip device error: %s: %s", what, hipGetErrorString(e));
+}
+
+}  // namespace
+
+struct qvkv_dev {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int *d_err = nullptr;        // latched kernel index errors (bit set)
+    void *ws = nullptr;          // attention workspace (partials of context chunks)
+    uint64_t ws_bytes = 0;
+    void *stage = nullptr;       // device staging for the host-memory entry points
+    uint64_t stage_bytes = 0;
+    std::mutex mu;               // serialises host-memory entry points and workspace growth
+    std::atomic<uint64_t> used{0}, peak{0}, refused{0};
+    std::atomic<uint64_t> uploads{0}, upload_bytes{0}, downloads{0}, download_bytes{0};
+    std::atomic<uint64_t> submissions{0}, wait_ns{0};
+    char name[256] = {0};
+};
+
+struct qvkv_buf {
+    qvkv_dev *dev;
+    void *ptr;
+    size_t len;
+};
+
+namespace {
+
+int set_device(qvkv_dev *dev) {
+    hipError_t e = hipSetDevice(dev->device);
+    return e == hipSuccess ? QVKV_OK : hip_fail(e, "hipSetDevice");
+}
+
+hipStream_t pick(qvkv_dev *dev, void *stream) {
+    return stream ? (hipStream_t)stream : dev->stream;
+}
+
+void account_alloc(qvkv_dev *dev, uint64_t n) {
+    uint64_t u = dev->used.fetch_add(n) + n;
+    uint64_t p = dev->peak.load();
+    while (u > p && !dev->peak.compare_exchange_weak(p, u)) {
+    }
+}
+
+int dev_malloc(qvkv_dev *dev, void **p, uint64_t n) {
+    hipError_t e = hipMalloc(p, n ? n : 1);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        dev->refused.fetch_add(1);
+        size_t fr = 0, tot = 0;
+        (void)hipMemGetInfo(&fr, &tot);
+        return fail(QVKV_E_OOM,
+                    "hip device is out of memory: %llu bytes requested, %llu of %llu in use",
+                    (unsigned long long)n, (unsigned long long)(tot - fr),
+                    (unsigned long long)tot);
+    }
+    account_alloc(dev, n);
+    return QVKV_OK;
+}
+
+void dev_free(qvkv_dev *dev, void *p, uint64_t n) {
+    if (!p) return;
+    (void)hipFree(p);
+    dev->used.fetch_sub(n);
+}
+
+// Grows a device buffer to at least `need` bytes (contents not kept).  Waits for the
+// device first, so no enqueued work still reads the old buffer.
+int ensure(qvkv_dev *dev, void **buf, uint64_t *have, uint64_t need) {
+    if (*have >= need) return QVKV_OK;
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
+    dev_free(dev, *buf, *have);
+    *buf = nullptr;
+    *have = 0;
+    uint64_t sz = std::max<uint64_t>(need, 1 << 20);
+    sz = (sz + 4095) & ~4095ull;
+    int rc = dev_malloc(dev, buf, sz);
+    if (rc) return rc;
+    *have = sz;
+    return QVKV_OK;
+}
+
+int geometry(const qvkv_layout *l, Geometry *g) {
+    const char *why = "";
+    int rc = qvkv::make_geometry(l, g, &why);
+    return rc ? fail(rc, "shape mismatch in kv layout: %s", why) : QVKV_OK;
+}
+
+// Stages host arrays into the device staging buffer (16-byte aligned pieces).
+struct Stager {
+    struct Piece {
+        const void *src;
+        uint64_t len;
+        uint64_t off;
+    };
+    std::vector<Piece> pieces;
+    uint64_t total = 0;
+    uint64_t add(const void *src, uint64_t len) {
+        uint64_t off = total;
+        pieces.push_back({src, len, off});
+        total += (len + 255) & ~255ull;
+        return off;
+    }
+    uint64_t reserve(uint64_t len) { return add(nullptr, len); }
+    int upload(qvkv_dev *dev) {
+        int rc = ensure(dev, &dev->stage, &dev->stage_bytes, total);
+        if (rc) return rc;
+        for (auto &p : pieces) {
+            if (!p.src || !p.len) continue;
+            hipError_t e = hipMemcpyAsync((char *)dev->stage + p.off, p.src, p.len,
+                                          hipMemcpyHostToDevice, dev->stream);
+            if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync (upload)");
+            dev->uploads.fetch_add(1);
+            dev->upload_bytes.fetch_add(p.len);
+        }
+        return QVKV_OK;
+    }
+    template <class T>
+    T *at(qvkv_dev *dev, uint64_t off) {
+        return (T *)((char *)dev->stage + off);
+    }
+};
+
+int download(qvkv_dev *dev, void *host, const void *devp, uint64_t len) {
+    if (!len) return QVKV_OK;
+    hipError_t e = hipMemcpyAsync(host, devp, len, hipMemcpyDeviceToHost, dev->stream);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync (download)");
+    dev->downloads.fetch_add(1);
+    dev->download_bytes.fetch_add(len);
+    return QVKV_OK;
+}
+
+// Waits for the stream and turns a latched kernel index error into QVKV_E_SHAPE.
+int finish(qvkv_dev *dev, hipStream_t s) {
+    auto t0 = std::chrono::steady_clock::now();
+    hipError_t e = hipStreamSynchronize(s);
+    dev->wait_ns.fetch_add((uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
+                               std::chrono::steady_clock::now() - t0)
+                               .count());
+    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+    int bits = 0;
+    e = hipMemcpy(&bits, dev->d_err, sizeof bits, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpy (error flag)");
+    if (bits) {
+        int zero = 0;
+        e = hipMemcpy(dev->d_err, &zero, sizeof zero, hipMemcpyHostToDevice);
+        if (e != hipSuccess) return hip_fail(e, "hipMemcpy (error flag reset)");
+        return fail(QVKV_E_SHAPE,
+                    "shape mismatch in kv kernel: %s%s%s%s",
+                    (bits & 1) ? "a block id past the pool; " : "",
+                    (bits & 2) ? "a block table shorter than its positions; " : "",
+                    (bits & 4) ? "a position past max_pos; " : "",
+                    (bits & 8) ? "an output range past out_positions; " : "");
+    }
+    return QVKV_OK;
+}
+
+int launched(qvkv_dev *dev, hipError_t e, const char *what) {
+    if (e != hipSuccess) return hip_fail(e, what);
+    dev->submissions.fetch_add(1);
+    return QVKV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qvkv_last_error(char *buf, size_t len) {
+    if (buf && len) {
+        size_t n = std::min(len - 1, g_err.size());
+        memcpy(buf, g_err.data(), n);
+        buf[n] = 0;
+    }
+    return g_err_code;
+}
+
+int qvkv_open(int device, qvkv_dev **out) {
+    if (!out) return fail(QVKV_E_SHAPE, "null output handle");
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count <= device || device < 0)
+        return fail(QVKV_E_DEVICE, "hip device error: no device %d (%d present)", device, count);
+    auto *d = new qvkv_dev();
+    d->device = device;
+    if (int rc = set_device(d)) { delete d; return rc; }
+    hipDeviceProp_t prop;
+    if ((e = hipGetDeviceProperties(&prop, device)) != hipSuccess) {
+        delete d;
+        return hip_fail(e, "hipGetDeviceProperties");
+    }
+    snprintf(d->name, sizeof d->name, "hip:%d %s (%s, %d CUs, %.1f GiB)", device, prop.name,
+             prop.gcnArchName, prop.multiProcessorCount, prop.totalGlobalMem / 1073741824.0);
+    if ((e = hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking)) != hipSuccess) {
+        delete d;
+        return hip_fail(e, "hipStreamCreate");
+    }
+    if (int rc = dev_malloc(d, (void **)&d->d_err, 256)) {
+        (void)hipStreamDestroy(d->stream);
+        delete d;
+        return rc;
+    }
+    int zero = 0;
+    (void)hipMemcpy(d->d_err, &zero, sizeof zero, hipMemcpyHostToDevice);
+    *out = d;
+    return QVKV_OK;
+}
+
+void qvkv_close(qvkv_dev *dev) {
+    if (!dev) return;
+    (void)hipSetDevice(dev->device);
+    (void)hipStreamSynchronize(dev->stream);
+    dev_free(dev, dev->ws, dev->ws_bytes);
+    dev_free(dev, dev->stage, dev->stage_bytes);
+    dev_free(dev, dev->d_err, 256);
+    (void)hipStreamDestroy(dev->stream);
+    delete dev;
+}
+
+int qvkv_describe(const qvkv_dev *dev, char *buf, size_t len) {
+    if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    if (buf && len) snprintf(buf, len, "%s", dev->name);
+    return QVKV_OK;
+}
+
+int qvkv_usage(const qvkv_dev *dev, qvkv_usage_t *out) {
+    if (!dev || !out) return fail(QVKV_E_SHAPE, "null argument");
+    size_t fr = 0, tot = 0;
+    (void)hipSetDevice(dev->device);
+    hipError_t e = hipMemGetInfo(&fr, &tot);
+    if (e != hipSuccess) return hip_fail(e, "hipMemGetInfo");
+    out->capacity = tot;
+    out->used = dev->used.load();
+    out->peak = dev->peak.load();
+    out->refused = dev->refused.load();
+    return QVKV_OK;
+}
+
+int qvkv_transfers(const qvkv_dev *dev, qvkv_transfers_t *out) {
+    if (!dev || !out) return fail(QVKV_E_SHAPE, "null argument");
+    out->uploads = dev->uploads.load();
+    out->upload_bytes = dev->upload_bytes.load();
+    out->downloads = dev->downloads.load();
+    out->download_bytes = dev->download_bytes.load();
+    out->submissions = dev->submissions.load();
+    out->wait_ns = dev->wait_ns.load();
+    return QVKV_OK;
+}
+
+void *qvkv_stream(const qvkv_dev *dev) { return dev ? (void *)dev->stream : nullptr; }
+
+int qvkv_alloc(qvkv_dev *dev, size_t len, qvkv_buf **out) {
+    if (!dev || !out) return fail(QVKV_E_SHAPE, "null argument");
+    if (int rc = set_device(dev)) return rc;
+    void *p = nullptr;
+    if (int rc = dev_malloc(dev, &p, len)) return rc;
+    *out = new qvkv_buf{dev, p, len};
+    return QVKV_OK;
+}
+
+void qvkv_free(qvkv_buf *buf) {
+    if (!buf) return;
+    (void)hipSetDevice(buf->dev->device);
+    // In-flight work on the device's stream may still read the buffer.
+    (void)hipStreamSynchronize(buf->dev->stream);
+    dev_free(buf->dev, buf->ptr, buf->len);
+    delete buf;
+}
+
+void *qvkv_buf_ptr(const qvkv_buf *buf) { return buf ? buf->ptr : nullptr; }
+size_t qvkv_buf_len(const qvkv_buf *buf) { return buf ? buf->len : 0; }
+
+int qvkv_write(qvkv_dev *dev, qvkv_buf *buf, size_t offset, const void *host, size_t len) {
+    if (!dev || !buf || (!host && len)) return fail(QVKV_E_SHAPE, "null argument");
+    if (buf->dev != dev) return fail(QVKV_E_DEVICE, "hip device error: a buffer of another device");
+    if (offset > buf->len || len > buf->len - offset)
+        return fail(QVKV_E_DEVICE, "hip device error: write of %zu bytes at %zu past a %zu-byte buffer",
+                    len, offset, buf->len);
+    std::lock_guard<std::mutex> lk(dev->mu);
+    if (int rc = set_device(dev)) return rc;
+    hipError_t e = hipMemcpyAsync((char *)buf->ptr + offset, host, len, hipMemcpyHostToDevice,
+                                  dev->stream);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync (write)");
+    dev->uploads.fetch_add(1);
+    dev->upload_bytes.fetch_add(len);
+    e = hipStreamSynchronize(dev->stream);
+    return e == hipSuccess ? QVKV_OK : hip_fail(e, "hipStreamSynchronize");
+}
+
+int qvkv_read(qvkv_dev *dev, const qvkv_buf *buf, size_t offset, void *host, size_t len) {
+    if (!dev || !buf || (!host && len)) return fail(QVKV_E_SHAPE, "null argument");
+    if (buf->dev != dev) return fail(QVKV_E_DEVICE, "hip device error: a buffer of another device");
+    if (offset > buf->len || len > buf->len - offset)
+        return fail(QVKV_E_DEVICE, "hip device error: read of %zu bytes at %zu past a %zu-byte buffer",
+                    len, offset, buf->len);
+    std::lock_guard<std::mutex> lk(dev->mu);
+    if (int rc = set_device(dev)) return rc;
+    if (int rc = download(dev, host, (const char *)buf->ptr + offset, len)) return rc;
+    hipError_t e = hipStreamSynchronize(dev->stream);
+    return e == hipSuccess ? QVKV_OK : hip_fail(e, "hipStreamSynchronize");
+}
+
+int qvkv_check(qvkv_dev *dev, void *stream) {
+    if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    if (int rc = set_device(dev)) return rc;
+    return finish(dev, pick(dev, stream));
+}
+
+int qvkv_block_bytes(const qvkv_layout *layout, uint64_t *out) {
+    Geometry g;
+    if (int rc = geometry(layout, &g)) return rc;
+    if (out) *out = g.block_bytes;
+    return QVKV_OK;
+}
+
+// ---------------------------------------------------------------------------------
+// device-pointer forms
+// ---------------------------------------------------------------------------------
+
+int qvkv_append_async(qvkv_dev *dev, const qvkv_layout *layout, void *pool,
+                      uint64_t pool_blocks, const float *k, const float *v,
+                      const uint32_t *slots, uint32_t n, void *stream) {
+    if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    Geometry g;
+    if (int rc = geometry(layout, &g)) return rc;
+    if (n == 0) return QVKV_OK;
+    if (!pool || !k || !v || !slots) return fail(QVKV_E_SHAPE, "shape mismatch in append: null pointer");
+    if (int rc = set_device(dev)) return rc;
+    return launched(dev, qvkv::launch_append(g, pool, pool_blocks, k, v, slots, n, dev->d_err,
+                                             pick(dev, stream)),
+                    "append launch");
+}
+
+int qvkv_gather_async(qvkv_dev *dev, const qvkv_layout *layout, const void *pool,
+                      uint64_t pool_blocks, const uint32_t *blocks, uint64_t n_table,
+                      const uint32_t *table_at, const uint32_t *lens, const uint64_t *out_at,
+                      uint32_t n_items, uint32_t max_len, uint32_t out_dtype,
+                      uint64_t out_positions, void *out_k, void *out_v, void *stream) {
+    if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    Geometry g;
+    if (int rc = geometry(layout, &g)) return rc;
+    if (out_dtype != QVKV_F32 && !(out_dtype == QVKV_F16 && g.dtype == QVKV_F16))
+        return fail(QVKV_E_UNSUPPORTED, "hip backend has no gather kernel for this output dtype");
+    if (n_items == 0 || max_len == 0) return QVKV_OK;
+    if (!pool || !blocks || !table_at || !lens || !out_at || !out_k || !out_v)
+        return fail(QVKV_E_SHAPE, "shape mismatch in gather: null pointer");
+    if (int rc = set_device(dev)) return rc;
+    return launched(dev, qvkv::launch_gather(g, pool, pool_blocks, blocks, n_table, table_at,
+                                             lens, out_at, n_items, max_len, (int)out_dtype,
+                                             out_positions, out_k, out_v, dev->d_err,
+                                             pick(dev, stream)),
+                    "gather launch");
+}
+
+int qvkv_attention_async(qvkv_dev *dev, const qvkv_layout *layout, const void *pool,
+                         uint64_t pool_blocks, const float *q, const uint32_t *blocks,
+                         uint64_t n_table, const uint32_t *table_at, const uint32_t *pos,
+                         uint32_t n_items, uint32_t heads, uint32_t max_pos, float *out,
+                         void *stream) {
+    if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    Geometry g;
+    if (int rc = geometry(layout, &g)) return rc;
+    qvkv::AttnPlan p;
+    const char *why = "";
+    if (int rc = qvkv::plan_attention(g, n_items, heads, max_pos, &p, &why))
+        return fail(rc, "shape mismatch in attention: %s", why);
+    if (n_items == 0) return QVKV_OK;
+    if (!pool || !q || !blocks || !table_at || !pos || !out)
+        return fail(QVKV_E_SHAPE, "shape mismatch in attention: null pointer");
+    if (int rc = set_device(dev)) return rc;
+    if (p.ws_bytes) {
+        std::lock_guard<std::mutex> lk(dev->mu);
+        if (int rc = ensure(dev, &dev->ws, &dev->ws_bytes, p.ws_bytes)) return rc;
+    }
+    return launched(dev, qvkv::launch_attention(g, p, pool, pool_blocks, q, blocks, n_table,
+                                                table_at, pos, n_items, heads, max_pos, out,
+                                                dev->ws, dev->d_err, pick(dev, stream)),
+                    "attention launch");
+}
+
+int qvkv_block_copy_async(qvkv_dev *dev, const qvkv_layout *layout, void *pool,
+                          uint64_t pool_blocks, const uint32_t *src, const uint32_t *dst,
+                          uint32_t n, void *stream) {
+    if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    Geometry g;
+    if (int rc = geometry(layout, &g)) return rc;
+    if (n == 0) return QVKV_OK;
+    if (!pool || !src || !dst) return fail(QVKV_E_SHAPE, "shape mismatch in block copy: null pointer");
+    if (int rc = set_device(dev)) return rc;
+    return launched(dev, qvkv::launch_block_copy(g, pool, pool_blocks, src, dst, n, dev->d_err,
+                                                 pick(dev, stream)),
+                    "block copy launch");
+}
+
+// ---------------------------------------------------------------------------------
+// host-memory forms (synchronous)
+// ---------------------------------------------------------------------------------
+
+static int pool_of(const qvkv_dev *dev, const qvkv_buf *pool, const Geometry &g, uint64_t *blocks) {
+    if (!pool) return fail(QVKV_E_SHAPE, "shape mismatch: null pool");
+    if (pool->dev != dev) return fail(QVKV_E_DEVICE, "hip device error: a pool of another device");
+    *blocks = pool->len / g.block_bytes;
+    return QVKV_OK;
+}
+
+int qvkv_append(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *pool, const float *k,
+                const float *v, const uint32_t *slots, uint32_t n) {
+    if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    Geometry g;
+    if (int rc = geometry(layout, &g)) return rc;
+    uint64_t held;
+    if (int rc = pool_of(dev, pool, g, &held)) return rc;
+    if (n == 0) return QVKV_OK;
+    for (uint32_t r = 0; r < n; r++)
+        if (slots[r] / g.B >= held)
+            return fail(QVKV_E_SHAPE, "shape mismatch in append: slot %u is in a block past the pool's %llu",
+                        slots[r], (unsigned long long)held);
+    std::lock_guard<std::mutex> lk(dev->mu);
+    if (int rc = set_device(dev)) return rc;
+    Stager st;
+    const uint64_t rowb = g.kv_out * 4;
+    uint64_t ko = st.add(k, n * rowb), vo = st.add(v, n * rowb), so = st.add(slots, n * 4ull);
+    if (int rc = st.upload(dev)) return rc;
+    if (int rc = launched(dev, qvkv::launch_append(g, pool->ptr, held, st.at<float>(dev, ko),
+                                                   st.at<float>(dev, vo),
+                                                   st.at<uint32_t>(dev, so), n, dev->d_err,
+                                                   dev->stream),
+                          "append launch"))
+        return rc;
+    return finish(dev, dev->stream);
+}
+
+int qvkv_gather(qvkv_dev *dev, const qvkv_layout *layout, const qvkv_buf *pool,
+                const uint32_t *blocks, uint64_t n_table, const uint32_t *table_at,
+                const uint32_t *lens, const uint64_t *out_at, uint32_t n_items,
+                uint32_t out_dtype, uint64_t out_positions, void *out_k, void *out_v) {
+    if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    Geometry g;
+    if (int rc = geometry(layout, &g)) return rc;
+    uint64_t held;
+    if (int rc = pool_of(dev, pool, g, &held)) return rc;
+    if (out_dtype != QVKV_F32 && !(out_dtype == QVKV_F16 && g.dtype == QVKV_F16))
+        return fail(QVKV_E_UNSUPPORTED, "hip backend has no gather kernel for this output dtype");
+    if (n_items == 0) return QVKV_OK;
+    uint32_t max_len = 0;
+    for (uint32_t t = 0; t < n_items; t++) {
+        max_len = std::max(max_len, lens[t]);
+        const uint64_t nb = ((uint64_t)lens[t] + g.B - 1) / g.B;
+        if ((uint64_t)table_at[t] + nb > n_table)
+            return fail(QVKV_E_SHAPE, "shape mismatch in gather: item %u has no block for its positions", t);
+        for (uint64_t b = 0; b < nb; b++)
+            if (blocks[table_at[t] + b] >= held)
+                return fail(QVKV_E_SHAPE, "shape mismatch in gather: a block past the pool's %llu",
+                            (unsigned long long)held);
+        if (out_at[t] + lens[t] > out_positions)
+            return fail(QVKV_E_SHAPE, "shape mismatch in gather: item %u past out_positions", t);
+    }
+    std::lock_guard<std::mutex> lk(dev->mu);
+    if (int rc = set_device(dev)) return rc;
+    const uint64_t esz = out_dtype == QVKV_F16 ? 2 : 4;
+    const uint64_t ob = out_positions * g.kv_out * esz;
+    Stager st;
+    uint64_t bo = st.add(blocks, n_table * 4), to = st.add(table_at, n_items * 4ull),
+             lo = st.add(lens, n_items * 4ull), oo = st.add(out_at, n_items * 8ull);
+    uint64_t ko = st.reserve(ob), vo = st.reserve(ob);
+    if (int rc = st.upload(dev)) return rc;
+    if (int rc = launched(dev, qvkv::launch_gather(g, pool->ptr, held, st.at<uint32_t>(dev, bo),
+                                                   n_table, st.at<uint32_t>(dev, to),
+                                                   st.at<uint32_t>(dev, lo),
+                                                   st.at<uint64_t>(dev, oo), n_items, max_len,
+                                                   (int)out_dtype, out_positions,
+                                                   st.at<void>(dev, ko), st.at<void>(dev, vo),
+                                                   dev->d_err, dev->stream),
+                          "gather launch"))
+        return rc;
+    if (int rc = download(dev, out_k, st.at<void>(dev, ko), ob)) return rc;
+    if (int rc = download(dev, out_v, st.at<void>(dev, vo), ob)) return rc;
+    return finish(dev, dev->stream);
+}
+
+int qvkv_block_copy(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *pool,
+                    const uint32_t *src, const uint32_t *dst, uint32_t n) {
+    if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    Geometry g;
+    if (int rc = geometry(layout, &g)) return rc;
+    uint64_t held;
+    if (int rc = pool_of(dev, pool, g, &held)) return rc;
+    for (uint32_t i = 0; i < n; i++)
+        if (src[i] >= held || dst[i] >= held)
+            return fail(QVKV_E_SHAPE, "shape mismatch in block copy: a block past the pool's %llu",
+                        (unsigned long long)held);
+    if (n == 0) return QVKV_OK;
+    std::lock_guard<std::mutex> lk(dev->mu);
+    if (int rc = set_device(dev)) return rc;
+    Stager st;
+    uint64_t so = st.add(src, n * 4ull), dd = st.add(dst, n * 4ull);
+    if (int rc = st.upload(dev)) return rc;
+    if (int rc = launched(dev, qvkv::launch_block_copy(g, pool->ptr, held, st.at<uint32_t>(dev, so),
+                                                       st.at<uint32_t>(dev, dd), n, dev->d_err,
+                                                       dev->stream),
+                          "block copy launch"))
+        return rc;
+    return finish(dev, dev->stream);
+}
+
+int qvkv_decode_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *pool,
+                          const float *q, uint32_t heads, const uint32_t *pos, uint32_t s,
+                          const uint32_t *blocks, uint64_t n_table, const uint32_t *table_at,
+                          const float *sync, const uint32_t *sync_to, uint32_t n_sync,
+                          const float *k_new, const float *v_new, float *out) {
+    if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    Geometry g;
+    if (int rc = geometry(layout, &g)) return rc;
+    uint64_t held;
+    if (int rc = pool_of(dev, pool, g, &held)) return rc;
+    qvkv::AttnPlan p;
+    const char *why = "";
+    uint32_t max_pos = 0;
+    for (uint32_t t = 0; t < s; t++) max_pos = std::max(max_pos, pos[t]);
+    if (int rc = qvkv::plan_attention(g, s, heads, max_pos, &p, &why))
+        return fail(rc, "shape mismatch in routed moe attention: %s", why);
+    if (s == 0) return QVKV_OK;
+    // The checks of SimDevice::attention (sim.rs:377-381): every block and sync target
+    // inside the pool, every token with a block for each of its positions.
+    for (uint64_t i = 0; i < n_table; i++)
+        if (blocks[i] >= held)
+            return fail(QVKV_E_SHAPE, "shape mismatch in routed moe attention: a block past the pool's %llu",
+                        (unsigned long long)held);
+    for (uint32_t i = 0; i < n_sync; i++)
+        if (sync_to[i] / g.B >= held)
+            return fail(QVKV_E_SHAPE, "shape mismatch in routed moe attention: a block past the pool's %llu",
+                        (unsigned long long)held);
+    std::vector<uint32_t> slots(s);
+    for (uint32_t t = 0; t < s; t++) {
+        const uint64_t i = (uint64_t)table_at[t] + pos[t] / g.B;
+        if ((uint64_t)table_at[t] + pos[t] / g.B + 1 > n_table)
+            return fail(QVKV_E_SHAPE, "shape mismatch in routed moe attention: token %u has no block for position %u",
+                        t, pos[t]);
+        slots[t] = blocks[i] * g.B + pos[t] % g.B;
+    }
+    // sync rows are [key row | value row]; the append takes separate key and value rows
+    std::vector<float> sk((uint64_t)n_sync * g.kv_out), sv((uint64_t)n_sync * g.kv_out);
+    for (uint32_t r = 0; r < n_sync; r++) {
+        memcpy(&sk[(uint64_t)r * g.kv_out], sync + (uint64_t)r * 2 * g.kv_out, g.kv_out * 4);
+        memcpy(&sv[(uint64_t)r * g.kv_out], sync + ((uint64_t)r * 2 + 1) * g.kv_out, g.kv_out * 4);
+    }
+    std::lock_guard<std::mutex> lk(dev->mu);
+    if (int rc = set_device(dev)) return rc;
+    if (p.ws_bytes)
+        if (int rc = ensure(dev, &dev->ws, &dev->ws_bytes, p.ws_bytes)) return rc;
+    const uint64_t rowb = g.kv_out * 4, qb = (uint64_t)s * heads * g.D * 4;
+    Stager st;
+    uint64_t sko = st.add(sk.data(), n_sync * rowb), svo = st.add(sv.data(), n_sync * rowb),
+             sto = st.add(sync_to, n_sync * 4ull), kno = st.add(k_new, s * rowb),
+             vno = st.add(v_new, s * rowb), slo = st.add(slots.data(), s * 4ull),
+             qo = st.add(q, qb), po = st.add(pos, s * 4ull), bo = st.add(blocks, n_table * 4),
+             tao = st.add(table_at, s * 4ull), oo = st.reserve(qb);
+    if (int rc = st.upload(dev)) return rc;
+    hipError_t e = hipSuccess;
+    if (n_sync)
+        e = qvkv::launch_append(g, pool->ptr, held, st.at<float>(dev, sko), st.at<float>(dev, svo),
+                                st.at<uint32_t>(dev, sto), n_sync, dev->d_err, dev->stream);
+    if (int rc = launched(dev, e, "append launch (sync rows)")) return rc;
+    e = qvkv::launch_append(g, pool->ptr, held, st.at<float>(dev, kno), st.at<float>(dev, vno),
+                            st.at<uint32_t>(dev, slo), s, dev->d_err, dev->stream);
+    if (int rc = launched(dev, e, "append launch (new rows)")) return rc;
+    e = qvkv::launch_attention(g, p, pool->ptr, held, st.at<float>(dev, qo),
+                               st.at<uint32_t>(dev, bo), n_table, st.at<uint32_t>(dev, tao),
+                               st.at<uint32_t>(dev, po), s, heads, max_pos,
+                               st.at<float>(dev, oo), dev->ws, dev->d_err, dev->stream);
+    if (int rc = launched(dev, e, "attention launch")) return rc;
+    if (int rc = download(dev, out, st.at<void>(dev, oo), qb)) return rc;
+    return finish(dev, dev->stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,57 @@
+// Internal interface between the C ABI (abi.hip, pool.cpp) and the kernels (kernels.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "qvkv.h"
+
+namespace qvkv {
+
+// Byte offsets inside one block.  f16: K [G][B][d] f16, then V [G][B][d] f16.
+// q8_0: K int8 [G][B][d] (row bytes permuted, see kernels.hip), K scales [G][B][d/32]
+// f16, V int8 [G][B][d] (permuted), V scales [G][B][d/32] f16.
+struct Geometry {
+    int dtype, G, D, B;
+    uint64_t kv_out;
+    uint64_t block_bytes;
+    uint64_t k_off, ks_off, v_off, vs_off;
+};
+
+// Records the calling thread's last error (returned by qvkv_last_error); returns code.
+int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Validates a layout and fills the geometry; returns a QVKV_* status and a message.
+int make_geometry(const qvkv_layout *l, Geometry *g, const char **why);
+
+// Kernel launchers; all enqueue on `stream` and return hipError_t of the launch.
+hipError_t launch_append(const Geometry &g, void *pool, uint64_t pool_blocks, const float *k,
+                         const float *v, const uint32_t *slots, uint32_t n, int *err,
+                         hipStream_t s);
+hipError_t launch_gather(const Geometry &g, const void *pool, uint64_t pool_blocks,
+                         const uint32_t *blocks, uint64_t n_table, const uint32_t *table_at,
+                         const uint32_t *lens, const uint64_t *out_at, uint32_t n_items,
+                         uint32_t max_len, int out_dtype, uint64_t out_positions, void *out_k,
+                         void *out_v, int *err, hipStream_t s);
+hipError_t launch_block_copy(const Geometry &g, void *pool, uint64_t pool_blocks,
+                             const uint32_t *src, const uint32_t *dst, uint32_t n, int *err,
+                             hipStream_t s);
+
+// Attention: the launch plan decides the split over the context and the workspace.
+struct AttnPlan {
+    int kind;           // 0: MFMA kernel, 1: generic kernel
+    uint32_t hc;        // head chunks of <= 8 query heads per KV head
+    uint32_t n_chunks;  // context chunks per (item, kv head, head chunk)
+    uint32_t tpc;       // 16-position tiles per chunk
+    uint64_t ws_bytes;  // workspace for partial results (0 when n_chunks == 1)
+};
+int plan_attention(const Geometry &g, uint32_t n_items, uint32_t heads, uint32_t max_pos,
+                   AttnPlan *p, const char **why);
+hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *pool,
+                            uint64_t pool_blocks, const float *q, const uint32_t *blocks,
+                            uint64_t n_table, const uint32_t *table_at, const uint32_t *pos,
+                            uint32_t n_items, uint32_t heads, uint32_t max_pos, float *out,
+                            void *ws, int *err, hipStream_t s);
+
+}  // namespace qvkv

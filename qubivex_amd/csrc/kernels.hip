@@ -1,0 +1,894 @@
+// HIP kernels of the paged KV-cache hot path, written for gfx950 (CDNA4, wave64).
+//
+// Pool layout in HBM (one block = `B` positions of one layer, all KV heads):
+//   f16 : K [G][B][d] f16 | V [G][B][d] f16
+//   q8_0: K int8 [G][B][d] | K scales [G][B][d/32] f16 | V int8 [G][B][d] | V scales
+// Each (head, position) row of d values is contiguous, so appending one position
+// writes G short contiguous runs, and a 16-position tile of one head is one
+// contiguous 16*d-element run (the gather's unit and the attention's MFMA tile).
+//
+// q8_0 rows are stored with their bytes permuted so that each MFMA lane reads its
+// operand with one contiguous load (the 32-value quantization groups are the logical
+// ones, along d, as in the reference's q8_0 format):
+//   K: logical d = 32*i + 8*q + t  is stored at byte  q*(d/4) + 8*i + t
+//   V: logical d = 32*g + 2*c + u  is stored at byte  c*(d/16) + 2*g + u
+//
+// Decode attention uses v_mfma_f32_16x16x16_f16 for the GQA group contraction: a
+// 16-position K tile against the group's query heads (8 columns for the heads' f16
+// high parts, 8 for their f16 residuals, so q keeps ~22 significant bits), and the
+// probabilities (again high part + residual) against the V tile.  Accumulation is f32.
+// The score tile produced by the first MFMA is, lane for lane, the A operand of the
+// second, so probabilities never leave registers.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "internal.h"
+
+namespace qvkv {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+enum : int { ERR_BLOCK = 1, ERR_TABLE = 2, ERR_POS = 4, ERR_OUT = 8 };
+
+struct Geo {  // kernel-side copy of Geometry
+    int dtype, G, D, B;
+    uint32_t kv_out;
+    uint64_t bb, k_off, ks_off, v_off, vs_off;
+};
+
+static Geo to_geo(const Geometry &g) {
+    return Geo{g.dtype, g.G, g.D, g.B, (uint32_t)g.kv_out, g.block_bytes,
+               g.k_off, g.ks_off, g.v_off, g.vs_off};
+}
+
+__device__ __forceinline__ void flag(int *err, int bit) { atomicOr(err, bit); }
+
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+    h2 v = {(_Float16)a, (_Float16)b};  // v_cvt_f16_f32: IEEE round to nearest even
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// Position of logical value d inside a stored q8_0 row.
+__device__ __forceinline__ uint32_t kperm(uint32_t d, uint32_t D) {
+    return ((d & 31u) >> 3) * (D >> 2) + (d >> 5) * 8u + (d & 7u);
+}
+__device__ __forceinline__ uint32_t vperm(uint32_t d, uint32_t D) {
+    return ((d & 31u) >> 1) * (D >> 4) + 2u * (d >> 5) + (d & 1u);
+}
+
+// ---------------------------------------------------------------------------------
+// Append.  Thread = 8 consecutive values of one row of K or V (two 16-byte loads).
+// f16: one 16-byte store.  q8_0: the 4 threads of a 32-value group share the group's
+// absolute maximum through two lane swaps, then quantize exactly as the reference
+// quantizer: d = amax/127 (f32), scale = f16(d) RNE, inv = d > 0 ? 1/d : 0 from the
+// f32 d, q = clamp(round_half_away(x*inv), -127, 127), NaN -> 0.
+// ---------------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(256) void k_append(uint8_t *__restrict__ pool, uint64_t pool_blocks,
+                                                const float *__restrict__ k,
+                                                const float *__restrict__ v,
+                                                const uint32_t *__restrict__ slots, uint32_t n,
+                                                Geo geo, int *err) {
+    const uint32_t cpr = geo.kv_out >> 3;  // 8-value chunks per K (or V) row
+    const uint32_t total = n * 2u * cpr;
+    const uint32_t D = (uint32_t)geo.D, B = (uint32_t)geo.B;
+    for (uint32_t w = blockIdx.x * 256u + threadIdx.x; w < total; w += gridDim.x * 256u) {
+        const uint32_t row = w / (2u * cpr);
+        uint32_t rem = w - row * 2u * cpr;
+        const bool isv = rem >= cpr;
+        const uint32_t e = (isv ? rem - cpr : rem) * 8u;
+        const uint32_t g = e / D, i = e - g * D;
+        const uint32_t slot = slots[row];
+        const uint64_t blk = slot / B;
+        const uint32_t off = slot - (uint32_t)blk * B;
+        if (blk >= pool_blocks) {  // whole rows: every lane of a q8_0 group agrees
+            flag(err, ERR_BLOCK);
+            continue;
+        }
+        const float *src = (isv ? v : k) + (uint64_t)row * geo.kv_out + e;
+        const float4 x0 = *(const float4 *)src;
+        const float4 x1 = *(const float4 *)(src + 4);
+        uint8_t *base = pool + blk * geo.bb;
+        const uint64_t rowidx = (uint64_t)g * B + off;  // (head, position) row in its region
+        if (DT == QVKV_F16) {
+            uint4 o;
+            o.x = pack_h2(x0.x, x0.y);
+            o.y = pack_h2(x0.z, x0.w);
+            o.z = pack_h2(x1.x, x1.y);
+            o.w = pack_h2(x1.z, x1.w);
+            *(uint4 *)(base + (isv ? geo.v_off : geo.k_off) + (rowidx * D + i) * 2u) = o;
+        } else {
+            float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            float amax = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 8; t++) amax = fmaxf(amax, fabsf(xs[t]));
+            amax = fmaxf(amax, __shfl_xor(amax, 1));
+            amax = fmaxf(amax, __shfl_xor(amax, 2));
+            const float d = amax / 127.0f;
+            const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+            uint32_t qb[2] = {0, 0};
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                float r = roundf(xs[t] * inv);
+                r = (r != r) ? 0.0f : fminf(fmaxf(r, -127.0f), 127.0f);
+                const uint32_t b = (uint32_t)(uint8_t)(int8_t)(int)r;
+                qb[t >> 2] |= b << (8 * (t & 3));
+            }
+            const uint32_t grp = i >> 5;
+            if (!isv) {
+                uint8_t *dst = base + geo.k_off + rowidx * D + kperm(i, D);
+                *(uint2 *)dst = make_uint2(qb[0], qb[1]);
+                if ((i & 31u) == 0) {
+                    _Float16 sh = (_Float16)d;
+                    *(_Float16 *)(base + geo.ks_off + (rowidx * (D >> 5) + grp) * 2u) = sh;
+                }
+            } else {
+                uint8_t *dst = base + geo.v_off + rowidx * D;
+#pragma unroll
+                for (int t = 0; t < 8; t += 2) {
+                    const uint32_t pair = (qb[t >> 2] >> (8 * (t & 3))) & 0xffffu;
+                    *(uint16_t *)(dst + vperm(i + t, D)) = (uint16_t)pair;
+                }
+                if ((i & 31u) == 0) {
+                    _Float16 sh = (_Float16)d;
+                    *(_Float16 *)(base + geo.vs_off + (rowidx * (D >> 5) + grp) * 2u) = sh;
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// Gather.  Workgroup = one 16-position tile of one item, every head, K and V.
+// ---------------------------------------------------------------------------------
+template <int DT, int OUT>
+__global__ __launch_bounds__(256) void k_gather(const uint8_t *__restrict__ pool,
+                                                uint64_t pool_blocks,
+                                                const uint32_t *__restrict__ blocks,
+                                                uint64_t n_table,
+                                                const uint32_t *__restrict__ table_at,
+                                                const uint32_t *__restrict__ lens,
+                                                const uint64_t *__restrict__ out_at,
+                                                uint32_t n_items, uint32_t tiles_max,
+                                                uint64_t out_positions, void *out_k,
+                                                void *out_v, Geo geo, int *err) {
+    const uint32_t item = blockIdx.x / tiles_max;
+    const uint32_t tile = blockIdx.x - item * tiles_max;
+    if (item >= n_items) return;
+    const uint32_t len = lens[item];
+    const uint32_t p0 = tile * 16u;
+    if (p0 >= len) return;
+    const uint32_t D = (uint32_t)geo.D, B = (uint32_t)geo.B, G = (uint32_t)geo.G;
+    const uint32_t tab = table_at[item];
+    const uint32_t nblk = (len + B - 1) / B;
+    if ((uint64_t)tab + nblk > n_table) {
+        if (threadIdx.x == 0) flag(err, ERR_TABLE);
+        return;
+    }
+    const uint64_t oat = out_at[item];
+    if (oat + len > out_positions) {
+        if (threadIdx.x == 0) flag(err, ERR_OUT);
+        return;
+    }
+    const uint32_t blk = blocks[tab + p0 / B];
+    if (blk >= pool_blocks) {
+        if (threadIdx.x == 0) flag(err, ERR_BLOCK);
+        return;
+    }
+    const uint32_t r0 = p0 % B;
+    const uint8_t *base = pool + (uint64_t)blk * geo.bb;
+    const uint32_t c8 = D >> 3;                 // 8-value chunks per row
+    const uint32_t per_kv = G * 16u * c8;       // chunks per tile for K (or V)
+    for (uint32_t idx = threadIdx.x; idx < 2u * per_kv; idx += 256u) {
+        const bool isv = idx >= per_kv;
+        uint32_t r = isv ? idx - per_kv : idx;
+        const uint32_t e = (r % c8) * 8u;
+        r /= c8;
+        const uint32_t row = r & 15u;
+        const uint32_t g = r >> 4;
+        const uint32_t p = p0 + row;
+        if (p >= len) continue;
+        const uint64_t rowidx = (uint64_t)g * B + r0 + row;
+        // out element offset: out_at*G*d + (g*len + p)*d + e
+        const uint64_t o = oat * (uint64_t)G * D + ((uint64_t)g * len + p) * D + e;
+        if (DT == QVKV_F16) {
+            const uint4 x = *(const uint4 *)(base + (isv ? geo.v_off : geo.k_off) +
+                                              (rowidx * D + e) * 2u);
+            if (OUT == QVKV_F16) {
+                *(uint4 *)((uint16_t *)(isv ? out_v : out_k) + o) = x;
+            } else {
+                h2 a = __builtin_bit_cast(h2, x.x), b = __builtin_bit_cast(h2, x.y);
+                h2 c = __builtin_bit_cast(h2, x.z), d2 = __builtin_bit_cast(h2, x.w);
+                float *dst = (float *)(isv ? out_v : out_k) + o;
+                *(float4 *)dst = make_float4((float)a.x, (float)a.y, (float)b.x, (float)b.y);
+                *(float4 *)(dst + 4) = make_float4((float)c.x, (float)c.y, (float)d2.x, (float)d2.y);
+            }
+        } else {  // q8_0 -> f32: y = f32(q) * f32(scale), one multiply (the reference dequant)
+            const uint8_t *rowp = base + (isv ? geo.v_off : geo.k_off) + rowidx * D;
+            const _Float16 sh = *(const _Float16 *)(base + (isv ? geo.vs_off : geo.ks_off) +
+                                                    (rowidx * (D >> 5) + (e >> 5)) * 2u);
+            const float sc = (float)sh;
+            float y[8];
+            if (!isv) {
+                const uint2 qb = *(const uint2 *)(rowp + kperm(e, D));
+#pragma unroll
+                for (int t = 0; t < 8; t++) {
+                    const uint32_t w = t < 4 ? qb.x : qb.y;
+                    y[t] = (float)(int8_t)(w >> (8 * (t & 3))) * sc;
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < 8; t += 2) {
+                    const uint16_t pr = *(const uint16_t *)(rowp + vperm(e + t, D));
+                    y[t] = (float)(int8_t)(pr & 0xff) * sc;
+                    y[t + 1] = (float)(int8_t)(pr >> 8) * sc;
+                }
+            }
+            float *dst = (float *)(isv ? out_v : out_k) + o;
+            *(float4 *)dst = make_float4(y[0], y[1], y[2], y[3]);
+            *(float4 *)(dst + 4) = make_float4(y[4], y[5], y[6], y[7]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// Block copy: workgroup = 16 KiB of one (src, dst) pair.
+// ---------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_block_copy(uint8_t *__restrict__ pool,
+                                                    uint64_t pool_blocks,
+                                                    const uint32_t *__restrict__ src,
+                                                    const uint32_t *__restrict__ dst,
+                                                    uint32_t n, uint32_t wgs_per_block,
+                                                    uint64_t bb, int *err) {
+    const uint32_t pair = blockIdx.x / wgs_per_block;
+    const uint32_t part = blockIdx.x - pair * wgs_per_block;
+    if (pair >= n) return;
+    const uint32_t s = src[pair], d = dst[pair];
+    if (s >= pool_blocks || d >= pool_blocks) {
+        if (threadIdx.x == 0 && part == 0) flag(err, ERR_BLOCK);
+        return;
+    }
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    const u4 *from = (const u4 *)(pool + (uint64_t)s * bb);
+    u4 *to = (u4 *)(pool + (uint64_t)d * bb);
+    const uint64_t words = bb >> 4;
+    const uint64_t begin = (uint64_t)part * 1024u;  // 1024 x 16 B per workgroup
+    u4 r[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const uint64_t i = begin + threadIdx.x + u * 256u;
+        if (i < words) r[u] = __builtin_nontemporal_load(from + i);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const uint64_t i = begin + threadIdx.x + u * 256u;
+        if (i < words) __builtin_nontemporal_store(r[u], to + i);
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// Decode attention, MFMA form.  Workgroup = 4 waves on one (item, KV head, head chunk
+// of <= 8 query heads, context chunk); wave w takes the chunk's tiles w, w+4, ...
+// Lane l: c = l % 16 (MFMA column / K row), q = l / 16.
+// ---------------------------------------------------------------------------------
+static constexpr float LOG2E_F = 1.4426950408889634f;
+
+__device__ __forceinline__ h4 h4_of(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(h4, make_uint2(a, b));
+}
+
+// 4 int8 (one word) -> 4 f16, exactly: (0x6400 | (x ^ 0x80)) is 1024 + x + 128 in f16.
+__device__ __forceinline__ h4 i8x4_to_h4(uint32_t w) {
+    const uint32_t u = w ^ 0x80808080u;
+    const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const h2 a = __builtin_bit_cast(h2, lo) - bias;
+    const h2 b = __builtin_bit_cast(h2, hi) - bias;
+    return h4{a.x, a.y, b.x, b.y};
+}
+
+// f32 -> (high f16, residual f16); lane columns < 8 take the high part.
+__device__ __forceinline__ _Float16 split_part(float x, bool hi_part) {
+    const _Float16 hi = (_Float16)x;
+    const _Float16 lo = (_Float16)(x - (float)hi);
+    return hi_part ? hi : lo;
+}
+
+template <int NB>
+__device__ __forceinline__ void load_bytes(const uint8_t *p, uint32_t *w) {
+    if constexpr (NB == 4) {
+        w[0] = *(const uint32_t *)p;
+    } else if constexpr (NB == 8) {
+        const uint2 x = *(const uint2 *)p;
+        w[0] = x.x; w[1] = x.y;
+    } else {
+#pragma unroll
+        for (int i = 0; i < NB / 16; i++) {
+            const uint4 x = *(const uint4 *)(p + 16 * i);
+            w[4 * i] = x.x; w[4 * i + 1] = x.y; w[4 * i + 2] = x.z; w[4 * i + 3] = x.w;
+        }
+    }
+}
+
+template <int D, bool Q8>
+__global__ __launch_bounds__(256) void k_attn_mfma(
+    const uint8_t *__restrict__ pool, uint64_t pool_blocks, const float *__restrict__ q,
+    const uint32_t *__restrict__ blocks, uint64_t n_table, const uint32_t *__restrict__ table_at,
+    const uint32_t *__restrict__ pos, uint32_t n_items, uint32_t H, uint32_t max_pos,
+    float *__restrict__ out, float *__restrict__ ws, uint32_t hc_n, uint32_t n_chunks,
+    uint32_t tpc, Geo geo, int *err) {
+    constexpr int NJ = D / 16;  // MFMA steps over d
+    constexpr int NG = D / 32;  // 32-value groups per row
+    __shared__ float sm[4][8], sl[4][8];
+    __shared__ float so[4][8][D];
+
+    const uint32_t G = (uint32_t)geo.G, B = (uint32_t)geo.B;
+    const uint32_t GS = H / G;
+    const uint32_t chunk = blockIdx.x % n_chunks;
+    const uint32_t unit = blockIdx.x / n_chunks;
+    const uint32_t hc = unit % hc_n;
+    const uint32_t ug = unit / hc_n;
+    const uint32_t g = ug % G;
+    const uint32_t item = ug / G;
+    if (item >= n_items) return;
+    const uint32_t plast = pos[item];
+    if (plast > max_pos) {
+        if (threadIdx.x == 0) flag(err, ERR_POS);
+        return;
+    }
+    const uint32_t n = plast + 1;
+    const uint32_t ntiles = (n + 15) / 16;
+    const uint32_t tab = table_at[item];
+    if ((uint64_t)tab + (n + B - 1) / B > n_table) {
+        if (threadIdx.x == 0) flag(err, ERR_TABLE);
+        return;
+    }
+    const uint32_t t_begin = chunk * tpc;
+    const uint32_t t_end = min(ntiles, t_begin + tpc);
+    if (t_begin >= t_end) return;
+
+    const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+    const uint32_t c = lane & 15u, qg = lane >> 4;
+    const bool hi_col = c < 8;
+    const uint32_t hidx = hc * 8 + (c & 7u);
+    const bool hvalid = hidx < GS;
+
+    // Query fragments (B operand of QK^T): column c, k-step j holds d = dset(qg, j).
+    h4 qf[NJ];
+    {
+        const float qs = (1.0f / sqrtf((float)D)) * LOG2E_F;
+        const float *qrow = q + ((uint64_t)item * H + (uint64_t)g * GS + hidx) * D;
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const int d0 = 32 * (j >> 1) + 8 * (int)qg + 4 * (j & 1);
+            float4 x = hvalid ? *(const float4 *)(qrow + d0) : make_float4(0.f, 0.f, 0.f, 0.f);
+            qf[j] = h4{split_part(x.x * qs, hi_col), split_part(x.y * qs, hi_col),
+                       split_part(x.z * qs, hi_col), split_part(x.w * qs, hi_col)};
+        }
+    }
+
+    float m = -INFINITY, l = 0.0f;
+    f4 acc[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) acc[j] = f4{0.f, 0.f, 0.f, 0.f};
+
+    for (uint32_t tt = t_begin + w; tt < t_end; tt += 4) {
+        const uint32_t p0 = tt * 16u;
+        const uint32_t blk = blocks[tab + p0 / B];
+        if (blk >= pool_blocks) {
+            if (lane == 0) flag(err, ERR_BLOCK);
+            continue;
+        }
+        const uint32_t r0 = p0 % B;
+        const uint8_t *base = pool + (uint64_t)blk * geo.bb;
+        const uint64_t rows = (uint64_t)g * B + r0;  // first (head, position) row of the tile
+
+        // ---- scores S^T[position][column] = K . Q^T
+        f4 s = f4{0.f, 0.f, 0.f, 0.f};
+        float vsc[4][NG];
+        uint32_t vw[4][Q8 ? D / 64 > 0 ? D / 64 : 1 : D / 32];
+        if constexpr (!Q8) {
+            const _Float16 *kr = (const _Float16 *)(base + geo.k_off) + (rows + c) * D;
+            uint4 kv[NG];
+#pragma unroll
+            for (int i = 0; i < NG; i++) kv[i] = *(const uint4 *)(kr + 32 * i + 8 * qg);
+            // V rows 4qg..4qg+3, columns c*D/16 .. +D/16 (issued early: independent of S)
+            const uint8_t *vr = base + geo.v_off + ((rows + 4 * qg) * D + c * (D / 16)) * 2u;
+#pragma unroll
+            for (int i = 0; i < 4; i++) load_bytes<D / 8>(vr + (uint64_t)i * D * 2u, vw[i]);
+#pragma unroll
+            for (int i = 0; i < NG; i++) {
+                s = __builtin_amdgcn_mfma_f32_16x16x16f16(h4_of(kv[i].x, kv[i].y), qf[2 * i], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_16x16x16f16(h4_of(kv[i].z, kv[i].w), qf[2 * i + 1], s, 0, 0, 0);
+            }
+        } else {
+            const uint8_t *kr = base + geo.k_off + (rows + c) * D + qg * (D / 4);
+            uint32_t kw[D / 16];
+            load_bytes<D / 4>(kr, kw);
+            // scales of rows 4qg..4qg+3: 4*NG f16, contiguous
+            const _Float16 *ksp = (const _Float16 *)(base + geo.ks_off) + (rows + 4 * qg) * NG;
+            const _Float16 *vsp = (const _Float16 *)(base + geo.vs_off) + (rows + 4 * qg) * NG;
+            _Float16 ksh[4 * NG], vsh[4 * NG];
+            load_bytes<8 * NG>((const uint8_t *)ksp, (uint32_t *)ksh);
+            load_bytes<8 * NG>((const uint8_t *)vsp, (uint32_t *)vsh);
+            const uint8_t *vr = base + geo.v_off + (rows + 4 * qg) * D + c * (D / 16);
+#pragma unroll
+            for (int i = 0; i < 4; i++) load_bytes<D / 16>(vr + (uint64_t)i * D, vw[i]);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int gi = 0; gi < NG; gi++) vsc[i][gi] = (float)vsh[i * NG + gi];
+#pragma unroll
+            for (int gi = 0; gi < NG; gi++) {
+                f4 sg = f4{0.f, 0.f, 0.f, 0.f};
+                sg = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4(kw[2 * gi]), qf[2 * gi], sg, 0, 0, 0);
+                sg = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4(kw[2 * gi + 1]), qf[2 * gi + 1], sg, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) s[i] = fmaf(sg[i], (float)ksh[i * NG + gi], s[i]);
+            }
+        }
+
+        // ---- high + residual columns, mask, online softmax (log2 domain)
+        float sc[4];
+        const bool partial = p0 + 16u > n;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float v2 = s[i] + __shfl_xor(s[i], 8);
+            if (partial && p0 + 4 * qg + i >= n) v2 = -INFINITY;
+            sc[i] = v2;
+        }
+        float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float mnew = fmaxf(m, tmax);
+        const float msafe = mnew == -INFINITY ? 0.0f : mnew;
+        const float alpha = __builtin_amdgcn_exp2f(m - msafe);
+        float pr[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) pr[i] = __builtin_amdgcn_exp2f(sc[i] - msafe);
+        l = l * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
+        if (__any(mnew > m)) {
+            float ar[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) ar[i] = __shfl(alpha, 4 * qg + i);
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[j][i] *= ar[i];
+        }
+        m = mnew;
+
+        // ---- O += P . V
+        if constexpr (!Q8) {
+            if (partial) {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (p0 + 4 * qg + i >= n)
+#pragma unroll
+                        for (int x = 0; x < D / 32; x++) vw[i][x] = 0u;
+            }
+            const h4 pa = h4{split_part(pr[0], hi_col), split_part(pr[1], hi_col),
+                             split_part(pr[2], hi_col), split_part(pr[3], hi_col)};
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+                const uint32_t w0 = __builtin_amdgcn_perm(vw[1][j >> 1], vw[0][j >> 1], sel);
+                const uint32_t w1 = __builtin_amdgcn_perm(vw[3][j >> 1], vw[2][j >> 1], sel);
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, h4_of(w0, w1), acc[j], 0, 0, 0);
+            }
+        } else {
+            if (partial) {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (p0 + 4 * qg + i >= n) {
+#pragma unroll
+                        for (int x = 0; x < (D / 64 > 0 ? D / 64 : 1); x++) vw[i][x] = 0u;
+#pragma unroll
+                        for (int gi = 0; gi < NG; gi++) vsc[i][gi] = 0.0f;
+                    }
+            }
+#pragma unroll
+            for (int gi = 0; gi < NG; gi++) {
+                const h4 pa = h4{split_part(pr[0] * vsc[0][gi], hi_col),
+                                 split_part(pr[1] * vsc[1][gi], hi_col),
+                                 split_part(pr[2] * vsc[2][gi], hi_col),
+                                 split_part(pr[3] * vsc[3][gi], hi_col)};
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    const int j = 2 * gi + u;
+                    const uint32_t bsel = (uint32_t)(j & 3);
+                    const uint32_t sel = 0x0c000c00u | ((4u + bsel) << 16) | bsel;
+                    const uint32_t a01 = __builtin_amdgcn_perm(vw[1][j >> 2] ^ 0x80808080u,
+                                                               vw[0][j >> 2] ^ 0x80808080u, sel) | 0x64006400u;
+                    const uint32_t a23 = __builtin_amdgcn_perm(vw[3][j >> 2] ^ 0x80808080u,
+                                                               vw[2][j >> 2] ^ 0x80808080u, sel) | 0x64006400u;
+                    const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+                    const h2 x01 = __builtin_bit_cast(h2, a01) - bias;
+                    const h2 x23 = __builtin_bit_cast(h2, a23) - bias;
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, h4{x01.x, x01.y, x23.x, x23.y},
+                                                                   acc[j], 0, 0, 0);
+                }
+            }
+        }
+    }
+
+    // ---- wave totals: l over the 4 row groups; O high rows + residual rows
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+#pragma unroll
+    for (int j = 0; j < NJ; j++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[j][i] += __shfl_xor(acc[j][i], 32);
+    if (qg == 0 && c < 8) {
+        sm[w][c] = m;
+        sl[w][c] = l;
+    }
+    if (qg < 2) {
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const int d = Q8 ? 32 * (j >> 1) + 2 * (int)c + (j & 1) : (int)c * (D / 16) + j;
+#pragma unroll
+            for (int i = 0; i < 4; i++) so[w][4 * qg + i][d] = acc[j][i];
+        }
+    }
+    __syncthreads();
+
+    // ---- merge the 4 waves; write the result or this chunk's partial
+    for (uint32_t idx = threadIdx.x; idx < 8u * D; idx += 256u) {
+        const uint32_t hh = idx / D, d = idx - hh * D;
+        const uint32_t hi2 = hc * 8 + hh;
+        if (hi2 >= GS) continue;
+        float M = sm[0][hh];
+#pragma unroll
+        for (int x = 1; x < 4; x++) M = fmaxf(M, sm[x][hh]);
+        const float Ms = M == -INFINITY ? 0.0f : M;
+        float L = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int x = 0; x < 4; x++) {
+            const float f = sm[x][hh] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sm[x][hh] - Ms);
+            L = fmaf(sl[x][hh], f, L);
+            O = fmaf(so[x][hh][d], f, O);
+        }
+        const uint64_t oh = (uint64_t)item * H + (uint64_t)g * GS + hi2;
+        if (n_chunks == 1) {
+            out[oh * D + d] = O / L;
+        } else {
+            ws[(oh * n_chunks + chunk) * D + d] = O;
+            if (d == 0) {
+                float *ml = ws + (uint64_t)n_items * H * n_chunks * D;
+                ml[(oh * n_chunks + chunk) * 2] = M;
+                ml[(oh * n_chunks + chunk) * 2 + 1] = L;
+            }
+        }
+    }
+}
+
+// Merge of context-chunk partials: block = one (item, query head), D threads.
+__global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ ws,
+                                                    const uint32_t *__restrict__ pos,
+                                                    uint32_t n_items, uint32_t H,
+                                                    uint32_t max_pos, uint32_t n_chunks,
+                                                    uint32_t tpc, uint32_t D,
+                                                    float *__restrict__ out) {
+    const uint32_t oh = blockIdx.x;
+    const uint32_t item = oh / H;
+    if (item >= n_items) return;
+    const uint32_t plast = pos[item];
+    if (plast > max_pos) return;
+    const uint32_t ntiles = (plast + 1 + 15) / 16;
+    const uint32_t nch = (ntiles + tpc - 1) / tpc;
+    const float *ml = ws + (uint64_t)n_items * H * n_chunks * D;
+    float M = -INFINITY;
+    for (uint32_t cidx = 0; cidx < nch; cidx++) M = fmaxf(M, ml[((uint64_t)oh * n_chunks + cidx) * 2]);
+    const float Ms = M == -INFINITY ? 0.0f : M;
+    for (uint32_t d = threadIdx.x; d < D; d += blockDim.x) {
+        float L = 0.0f, O = 0.0f;
+        for (uint32_t cidx = 0; cidx < nch; cidx++) {
+            const uint64_t at = (uint64_t)oh * n_chunks + cidx;
+            const float mc = ml[at * 2];
+            const float f = mc == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mc - Ms);
+            L = fmaf(ml[at * 2 + 1], f, L);
+            O = fmaf(ws[at * D + d], f, O);
+        }
+        out[(uint64_t)oh * D + d] = O / L;
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// Decode attention, generic form (any d that is a multiple of 8 up to 512, any group):
+// one wave per (item, query head); lanes take 64 positions at a time for the scores,
+// then d-columns for P.V.  Used where the MFMA form has no instance.
+// ---------------------------------------------------------------------------------
+template <bool Q8>
+__device__ __forceinline__ float kv_elem(const uint8_t *base, const Geo &geo, bool isv,
+                                         uint64_t row, uint32_t d) {
+    const uint32_t D = (uint32_t)geo.D;
+    if constexpr (!Q8) {
+        return (float)((const _Float16 *)(base + (isv ? geo.v_off : geo.k_off)))[row * D + d];
+    } else {
+        const int8_t qv = (int8_t)base[(isv ? geo.v_off : geo.k_off) + row * D +
+                                       (isv ? vperm(d, D) : kperm(d, D))];
+        const float sc = (float)((const _Float16 *)(base + (isv ? geo.vs_off : geo.ks_off)))
+            [row * (D >> 5) + (d >> 5)];
+        return (float)qv * sc;
+    }
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+    return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+    return x;
+}
+
+template <bool Q8>
+__global__ __launch_bounds__(64) void k_attn_generic(
+    const uint8_t *__restrict__ pool, uint64_t pool_blocks, const float *__restrict__ q,
+    const uint32_t *__restrict__ blocks, uint64_t n_table, const uint32_t *__restrict__ table_at,
+    const uint32_t *__restrict__ pos, uint32_t n_items, uint32_t H, uint32_t max_pos,
+    float *__restrict__ out, Geo geo, int *err) {
+    __shared__ float qs[512];
+    __shared__ float ps[64];
+    const uint32_t item = blockIdx.x / H, h = blockIdx.x - item * H;
+    if (item >= n_items) return;
+    const uint32_t D = (uint32_t)geo.D, B = (uint32_t)geo.B, G = (uint32_t)geo.G;
+    const uint32_t g = h / (H / G);
+    const uint32_t lane = threadIdx.x;
+    const uint32_t plast = pos[item];
+    if (plast > max_pos) {
+        if (lane == 0) flag(err, ERR_POS);
+        return;
+    }
+    const uint32_t n = plast + 1;
+    const uint32_t tab = table_at[item];
+    if ((uint64_t)tab + (n + B - 1) / B > n_table) {
+        if (lane == 0) flag(err, ERR_TABLE);
+        return;
+    }
+    const float scale = (1.0f / sqrtf((float)D)) * LOG2E_F;
+    const float *qrow = q + ((uint64_t)item * H + h) * D;
+    for (uint32_t i = lane; i < D; i += 64) qs[i] = qrow[i] * scale;
+    __syncthreads();
+    float m = -INFINITY, l = 0.0f, acc[8];
+#pragma unroll
+    for (int x = 0; x < 8; x++) acc[x] = 0.0f;
+    for (uint32_t b0 = 0; b0 < n; b0 += 64) {
+        const uint32_t p = b0 + lane;
+        float s = -INFINITY;
+        if (p < n) {
+            const uint32_t blk = blocks[tab + p / B];
+            if (blk < pool_blocks) {
+                const uint8_t *base = pool + (uint64_t)blk * geo.bb;
+                const uint64_t row = (uint64_t)g * B + p % B;
+                float t = 0.0f;
+                for (uint32_t d = 0; d < D; d++) t = fmaf(qs[d], kv_elem<Q8>(base, geo, false, row, d), t);
+                s = t;
+            } else {
+                flag(err, ERR_BLOCK);
+            }
+        }
+        const float mnew = fmaxf(m, wave_max(s));
+        const float msafe = mnew == -INFINITY ? 0.0f : mnew;
+        const float alpha = __builtin_amdgcn_exp2f(m - msafe);
+        const float e = p < n ? __builtin_amdgcn_exp2f(s - msafe) : 0.0f;
+        l = l * alpha + wave_sum(e);
+#pragma unroll
+        for (int x = 0; x < 8; x++) acc[x] *= alpha;
+        m = mnew;
+        ps[lane] = e;
+        __syncthreads();
+        const uint32_t cnt = min(64u, n - b0);
+        for (uint32_t pp = 0; pp < cnt; pp++) {
+            const uint32_t p2 = b0 + pp;
+            const uint32_t blk = blocks[tab + p2 / B];
+            if (blk >= pool_blocks) continue;
+            const uint8_t *base = pool + (uint64_t)blk * geo.bb;
+            const uint64_t row = (uint64_t)g * B + p2 % B;
+            const float wgt = ps[pp];
+#pragma unroll
+            for (int x = 0; x < 8; x++) {
+                const uint32_t d = lane + 64u * x;
+                if (d < D) acc[x] = fmaf(wgt, kv_elem<Q8>(base, geo, true, row, d), acc[x]);
+            }
+        }
+        __syncthreads();
+    }
+    float *orow = out + ((uint64_t)item * H + h) * D;
+#pragma unroll
+    for (int x = 0; x < 8; x++) {
+        const uint32_t d = lane + 64u * x;
+        if (d < D) orow[d] = acc[x] / l;
+    }
+}
+
+// =================================================================================
+// Host side: geometry and launchers.
+// =================================================================================
+
+int make_geometry(const qvkv_layout *l, Geometry *g, const char **why) {
+    if (!l) { *why = "null layout"; return QVKV_E_SHAPE; }
+    if (l->dtype != QVKV_F16 && l->dtype != QVKV_Q8_0) {
+        *why = "pool dtype must be F16 or Q8_0";
+        return QVKV_E_UNSUPPORTED;
+    }
+    if (l->kv_heads == 0 || l->head_dim == 0 || l->block == 0) {
+        *why = "kv_heads, head_dim and block must be positive";
+        return QVKV_E_SHAPE;
+    }
+    if (l->block % 16 != 0 || l->block > 4096) {
+        *why = "block must be a multiple of 16 positions (at most 4096)";
+        return QVKV_E_SHAPE;
+    }
+    if (l->head_dim > 512 || l->head_dim % (l->dtype == QVKV_Q8_0 ? 32 : 8) != 0) {
+        *why = "head_dim must be a multiple of 8 (f16) or 32 (q8_0), at most 512";
+        return QVKV_E_SHAPE;
+    }
+    if ((uint64_t)l->kv_heads * l->head_dim > (1u << 20)) {
+        *why = "kv_heads * head_dim too large";
+        return QVKV_E_SHAPE;
+    }
+    g->dtype = (int)l->dtype;
+    g->G = (int)l->kv_heads;
+    g->D = (int)l->head_dim;
+    g->B = (int)l->block;
+    g->kv_out = (uint64_t)l->kv_heads * l->head_dim;
+    const uint64_t rows = (uint64_t)l->kv_heads * l->block;  // (head, position) rows per block
+    if (l->dtype == QVKV_F16) {
+        g->k_off = 0;
+        g->ks_off = 0;
+        g->v_off = rows * l->head_dim * 2;
+        g->vs_off = 0;
+        g->block_bytes = 2 * rows * l->head_dim * 2;
+    } else {
+        const uint64_t q = rows * l->head_dim, s = rows * (l->head_dim / 32) * 2;
+        g->k_off = 0;
+        g->ks_off = q;
+        g->v_off = q + s;
+        g->vs_off = 2 * q + s;
+        g->block_bytes = 2 * (q + s);
+    }
+    return QVKV_OK;
+}
+
+static unsigned grid_for(uint64_t threads) {
+    uint64_t wgs = (threads + 255) / 256;
+    const uint64_t cap = 256ull * 64ull;  // 64 workgroups per CU, grid-stride beyond
+    return (unsigned)(wgs < 1 ? 1 : (wgs > cap ? cap : wgs));
+}
+
+hipError_t launch_append(const Geometry &g, void *pool, uint64_t pool_blocks, const float *k,
+                         const float *v, const uint32_t *slots, uint32_t n, int *err,
+                         hipStream_t s) {
+    const Geo geo = to_geo(g);
+    const uint64_t per_row = 2 * (g.kv_out / 8);
+    // keep the flat index inside 32 bits: launch in row batches
+    const uint32_t max_rows = (uint32_t)((0x7fffffffull / per_row));
+    for (uint32_t r0 = 0; r0 < n; r0 += max_rows) {
+        const uint32_t nr = n - r0 < max_rows ? n - r0 : max_rows;
+        const unsigned grid = grid_for((uint64_t)nr * per_row);
+        const float *kk = k + (uint64_t)r0 * g.kv_out, *vv = v + (uint64_t)r0 * g.kv_out;
+        if (g.dtype == QVKV_F16)
+            hipLaunchKernelGGL(k_append<QVKV_F16>, dim3(grid), dim3(256), 0, s, (uint8_t *)pool,
+                               pool_blocks, kk, vv, slots + r0, nr, geo, err);
+        else
+            hipLaunchKernelGGL(k_append<QVKV_Q8_0>, dim3(grid), dim3(256), 0, s, (uint8_t *)pool,
+                               pool_blocks, kk, vv, slots + r0, nr, geo, err);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_gather(const Geometry &g, const void *pool, uint64_t pool_blocks,
+                         const uint32_t *blocks, uint64_t n_table, const uint32_t *table_at,
+                         const uint32_t *lens, const uint64_t *out_at, uint32_t n_items,
+                         uint32_t max_len, int out_dtype, uint64_t out_positions, void *out_k,
+                         void *out_v, int *err, hipStream_t s) {
+    const Geo geo = to_geo(g);
+    const uint32_t tiles = (max_len + 15) / 16;
+    if (tiles == 0 || n_items == 0) return hipSuccess;
+    const uint64_t grid = (uint64_t)tiles * n_items;
+    if (grid > 0x7fffffffull) return hipErrorInvalidValue;
+    const uint8_t *p = (const uint8_t *)pool;
+#define QV_GATHER(DT, OT)                                                                      \
+    hipLaunchKernelGGL((k_gather<DT, OT>), dim3((unsigned)grid), dim3(256), 0, s, p,           \
+                       pool_blocks, blocks, n_table, table_at, lens, out_at, n_items, tiles,   \
+                       out_positions, out_k, out_v, geo, err)
+    if (g.dtype == QVKV_F16 && out_dtype == QVKV_F16) QV_GATHER(QVKV_F16, QVKV_F16);
+    else if (g.dtype == QVKV_F16) QV_GATHER(QVKV_F16, QVKV_F32);
+    else QV_GATHER(QVKV_Q8_0, QVKV_F32);
+#undef QV_GATHER
+    return hipGetLastError();
+}
+
+hipError_t launch_block_copy(const Geometry &g, void *pool, uint64_t pool_blocks,
+                             const uint32_t *src, const uint32_t *dst, uint32_t n, int *err,
+                             hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    const uint32_t per = (uint32_t)((g.block_bytes / 16 + 1023) / 1024);
+    const uint64_t grid = (uint64_t)per * n;
+    if (grid > 0x7fffffffull) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_block_copy, dim3((unsigned)grid), dim3(256), 0, s, (uint8_t *)pool,
+                       pool_blocks, src, dst, n, per, g.block_bytes, err);
+    return hipGetLastError();
+}
+
+int plan_attention(const Geometry &g, uint32_t n_items, uint32_t heads, uint32_t max_pos,
+                   AttnPlan *p, const char **why) {
+    if (heads == 0 || heads % (uint32_t)g.G != 0) {
+        *why = "query heads must be a positive multiple of kv_heads";
+        return QVKV_E_SHAPE;
+    }
+    const uint32_t GS = heads / (uint32_t)g.G;
+    const bool mfma = g.D == 64 || g.D == 128 || g.D == 256;
+    p->kind = mfma ? 0 : 1;
+    p->hc = (GS + 7) / 8;
+    p->n_chunks = 1;
+    p->tpc = 0;
+    p->ws_bytes = 0;
+    if (!mfma) {
+        if ((uint64_t)n_items * heads > 0x7fffffffull) { *why = "batch too large"; return QVKV_E_SHAPE; }
+        return QVKV_OK;
+    }
+    const uint64_t units = (uint64_t)n_items * g.G * p->hc;
+    const uint64_t max_tiles = ((uint64_t)max_pos + 1 + 15) / 16;
+    const uint64_t target = 2048;  // workgroups: 8 per CU keeps all 256 CUs busy
+    uint64_t nch = units >= target ? 1 : (target + units - 1) / units;
+    const uint64_t cap = (max_tiles + 3) / 4;  // at least one tile per wave
+    if (nch > cap) nch = cap;
+    if (nch < 1) nch = 1;
+    uint64_t tpc = (max_tiles + nch - 1) / nch;
+    nch = (max_tiles + tpc - 1) / tpc;
+    if (units * nch > 0x7fffffffull) { *why = "batch too large"; return QVKV_E_SHAPE; }
+    p->n_chunks = (uint32_t)nch;
+    p->tpc = (uint32_t)tpc;
+    p->ws_bytes = nch > 1 ? (uint64_t)n_items * heads * nch * (g.D + 2) * 4 : 0;
+    return QVKV_OK;
+}
+
+hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *pool,
+                            uint64_t pool_blocks, const float *q, const uint32_t *blocks,
+                            uint64_t n_table, const uint32_t *table_at, const uint32_t *pos,
+                            uint32_t n_items, uint32_t heads, uint32_t max_pos, float *out,
+                            void *ws, int *err, hipStream_t s) {
+    if (n_items == 0) return hipSuccess;
+    const Geo geo = to_geo(g);
+    const uint8_t *pp = (const uint8_t *)pool;
+    if (p.kind == 1) {
+        if (g.dtype == QVKV_F16)
+            hipLaunchKernelGGL(k_attn_generic<false>, dim3(n_items * heads), dim3(64), 0, s, pp,
+                               pool_blocks, q, blocks, n_table, table_at, pos, n_items, heads,
+                               max_pos, out, geo, err);
+        else
+            hipLaunchKernelGGL(k_attn_generic<true>, dim3(n_items * heads), dim3(64), 0, s, pp,
+                               pool_blocks, q, blocks, n_table, table_at, pos, n_items, heads,
+                               max_pos, out, geo, err);
+        return hipGetLastError();
+    }
+    const uint64_t grid = (uint64_t)n_items * g.G * p.hc * p.n_chunks;
+    float *wsf = (float *)ws;
+#define QV_ATTN(DD, QQ)                                                                         \
+    hipLaunchKernelGGL((k_attn_mfma<DD, QQ>), dim3((unsigned)grid), dim3(256), 0, s, pp,        \
+                       pool_blocks, q, blocks, n_table, table_at, pos, n_items, heads, max_pos, \
+                       out, wsf, p.hc, p.n_chunks, p.tpc, geo, err)
+    const bool q8 = g.dtype == QVKV_Q8_0;
+    if (g.D == 64) { if (q8) QV_ATTN(64, true); else QV_ATTN(64, false); }
+    else if (g.D == 128) { if (q8) QV_ATTN(128, true); else QV_ATTN(128, false); }
+    else { if (q8) QV_ATTN(256, true); else QV_ATTN(256, false); }
+#undef QV_ATTN
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || p.n_chunks == 1) return e;
+    hipLaunchKernelGGL(k_attn_merge, dim3(n_items * heads), dim3(g.D), 0, s, (const float *)ws,
+                       pos, n_items, heads, max_pos, p.n_chunks, p.tpc, (uint32_t)g.D, out);
+    return hipGetLastError();
+}
+
+}  // namespace qvkv

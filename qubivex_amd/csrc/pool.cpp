@@ -1,0 +1,460 @@
+// Host pool manager: the block pool, per-sequence per-layer block tables, prefix
+// sharing with copy-on-write, LRU eviction and compaction (include/qvkv.h, qvkv_pool_*).
+//
+// Reference behaviour restated here (kentmarete/qubivex):
+//  - the free list is a LIFO of block ids that starts as (0..n).rev(), so the first
+//    pop is block 0 (crates/qubivex-runtime/src/discrete.rs:215-225, 446-449);
+//  - a sequence's table grows, layer by layer, to pos/B + 1 blocks by popping the free
+//    list; a dry free list declines the whole layer (`full`)
+//    (crates/qubivex-runtime/src/discrete.rs:988-994, 882-891);
+//  - releasing a sequence gives every block back (Mirror::release,
+//    crates/qubivex-runtime/src/discrete.rs:267-280);
+//  - eviction takes the least recently used first (PrefixCache::evict_oldest,
+//    crates/qubivex-kv-cache/src/lib.rs:197-213).
+// Added for paged sharing (ADR-016's "Paged KV later",
+// docs/decisions/ADR-016-KV-SUBSYSTEM.md:82-89): per-block reference counts, fork
+// (a prefix hit becomes shared blocks instead of restore_from's copy), copy-on-write of
+// a shared partially filled block before a write lands in it, and compaction of live
+// blocks to the front of the pool in cycle-safe batches of the block-copy kernel.
+#include <algorithm>
+#include <mutex>
+#include <numeric>
+#include <unordered_map>
+#include <vector>
+
+#include "internal.h"
+#include "qvkv.h"
+
+struct Seq {
+    bool live = false;
+    uint64_t used = 0;
+    std::vector<std::vector<uint32_t>> blocks;  // per layer, in position order
+    std::vector<uint32_t> len;                  // per layer, positions written
+};
+
+struct qvkv_pool {
+    qvkv_dev *dev = nullptr;
+    qvkv_layout layout{};
+    qvkv::Geometry g{};
+    uint64_t n_blocks = 0;
+    uint32_t n_layers = 0;
+    qvkv_buf *buf = nullptr;
+    std::vector<uint32_t> free;  // LIFO: back() is the next block handed out
+    std::vector<uint32_t> refs;  // per block; 0 = free
+    std::vector<Seq> seqs;
+    std::vector<uint32_t> free_handles;
+    std::vector<uint32_t> log_src, log_dst;  // host-only pools: copies issued, in order
+    uint64_t clock = 0;
+    uint64_t layers = 0, rows = 0, full = 0, cow = 0, evicted = 0, moved = 0;
+    mutable std::mutex mu;
+};
+
+namespace {
+
+int err(int code, const char *msg) { return qvkv::set_error(code, "%s", msg); }
+
+Seq *seq_of(qvkv_pool *p, uint32_t s) {
+    return (s < p->seqs.size() && p->seqs[s].live) ? &p->seqs[s] : nullptr;
+}
+const Seq *seq_of(const qvkv_pool *p, uint32_t s) {
+    return (s < p->seqs.size() && p->seqs[s].live) ? &p->seqs[s] : nullptr;
+}
+
+uint32_t new_handle(qvkv_pool *p) {
+    uint32_t h;
+    if (!p->free_handles.empty()) {
+        h = p->free_handles.back();
+        p->free_handles.pop_back();
+    } else {
+        h = (uint32_t)p->seqs.size();
+        p->seqs.emplace_back();
+    }
+    Seq &s = p->seqs[h];
+    s.live = true;
+    s.used = ++p->clock;
+    s.blocks.assign(p->n_layers, {});
+    s.len.assign(p->n_layers, 0);
+    return h;
+}
+
+void unref(qvkv_pool *p, uint32_t b, uint64_t *returned) {
+    if (--p->refs[b] == 0) {
+        p->free.push_back(b);
+        if (returned) ++*returned;
+    }
+}
+
+uint64_t release(qvkv_pool *p, uint32_t h) {
+    Seq &s = p->seqs[h];
+    uint64_t returned = 0;
+    for (auto &l : s.blocks) {
+        for (uint32_t b : l) unref(p, b, &returned);
+        l.clear();
+    }
+    s.live = false;
+    s.len.clear();
+    p->free_handles.push_back(h);
+    return returned;
+}
+
+// Copies block pairs on the device, in one launch, before returning.
+int copy_blocks(qvkv_pool *p, const std::vector<uint32_t> &src, const std::vector<uint32_t> &dst) {
+    if (src.empty()) return QVKV_OK;
+    if (!p->dev) {
+        p->log_src.insert(p->log_src.end(), src.begin(), src.end());
+        p->log_dst.insert(p->log_dst.end(), dst.begin(), dst.end());
+        return QVKV_OK;
+    }
+    return qvkv_block_copy(p->dev, &p->layout, p->buf, src.data(), dst.data(), (uint32_t)src.size());
+}
+
+uint64_t splitmix(uint64_t &x) {
+    uint64_t z = (x += 0x9e3779b97f4a7c15ull);
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+}  // namespace
+
+extern "C" {
+
+int qvkv_pool_create(qvkv_dev *dev, const qvkv_layout *layout, uint64_t n_blocks,
+                     uint32_t n_layers, qvkv_pool **out) {
+    if (!layout || !out) return err(QVKV_E_SHAPE, "shape mismatch in pool: null argument");
+    qvkv::Geometry g;
+    const char *why = "";
+    if (int rc = qvkv::make_geometry(layout, &g, &why)) return err(rc, why);
+    if (n_blocks == 0 || n_blocks > 0xffffffffull || n_layers == 0)
+        return err(QVKV_E_SHAPE, "shape mismatch in pool: block count must be in 1..2^32-1, layers >= 1");
+    if (n_blocks * g.block_bytes / g.block_bytes != n_blocks)
+        return err(QVKV_E_SHAPE, "shape mismatch in pool: size overflows");
+    auto *p = new qvkv_pool();
+    p->dev = dev;
+    p->layout = *layout;
+    p->g = g;
+    p->n_blocks = n_blocks;
+    p->n_layers = n_layers;
+    if (dev) {
+        if (int rc = qvkv_alloc(dev, n_blocks * g.block_bytes, &p->buf)) {
+            delete p;
+            return rc;
+        }
+    }
+    p->refs.assign(n_blocks, 0);
+    p->free.resize(n_blocks);
+    for (uint64_t i = 0; i < n_blocks; i++) p->free[i] = (uint32_t)(n_blocks - 1 - i);
+    *out = p;
+    return QVKV_OK;
+}
+
+void qvkv_pool_destroy(qvkv_pool *pool) {
+    if (!pool) return;
+    if (pool->buf) qvkv_free(pool->buf);
+    delete pool;
+}
+
+int qvkv_pool_take_copies(qvkv_pool *p, uint32_t *src, uint32_t *dst, uint64_t cap, uint64_t *n) {
+    if (!p || !n || (cap && (!src || !dst))) return err(QVKV_E_SHAPE, "shape mismatch in pool: null argument");
+    std::lock_guard<std::mutex> lk(p->mu);
+    const uint64_t have = p->log_src.size();
+    *n = have;
+    const uint64_t take = std::min<uint64_t>(cap, have);
+    std::copy(p->log_src.begin(), p->log_src.begin() + take, src);
+    std::copy(p->log_dst.begin(), p->log_dst.begin() + take, dst);
+    p->log_src.erase(p->log_src.begin(), p->log_src.begin() + take);
+    p->log_dst.erase(p->log_dst.begin(), p->log_dst.begin() + take);
+    return QVKV_OK;
+}
+
+void *qvkv_pool_ptr(const qvkv_pool *pool) { return pool && pool->buf ? qvkv_buf_ptr(pool->buf) : nullptr; }
+
+int qvkv_pool_stats(const qvkv_pool *p, qvkv_pool_stats_t *out) {
+    if (!p || !out) return err(QVKV_E_SHAPE, "shape mismatch in pool: null argument");
+    std::lock_guard<std::mutex> lk(p->mu);
+    out->bytes = p->n_blocks * p->g.block_bytes;
+    out->blocks = p->n_blocks;
+    out->free = p->free.size();
+    out->layers = p->layers;
+    out->synced_rows = p->rows;
+    out->full = p->full;
+    out->shared_blocks = (uint64_t)std::count_if(p->refs.begin(), p->refs.end(),
+                                                 [](uint32_t r) { return r > 1; });
+    out->cow_copies = p->cow;
+    out->evicted_blocks = p->evicted;
+    out->moved_blocks = p->moved;
+    return QVKV_OK;
+}
+
+int qvkv_seq_create(qvkv_pool *p, uint32_t *seq) {
+    if (!p || !seq) return err(QVKV_E_SHAPE, "shape mismatch in pool: null argument");
+    std::lock_guard<std::mutex> lk(p->mu);
+    *seq = new_handle(p);
+    return QVKV_OK;
+}
+
+int qvkv_seq_release(qvkv_pool *p, uint32_t seq) {
+    if (!p) return err(QVKV_E_SHAPE, "shape mismatch in pool: null argument");
+    std::lock_guard<std::mutex> lk(p->mu);
+    if (!seq_of(p, seq)) return err(QVKV_E_SHAPE, "shape mismatch in pool: no such sequence");
+    release(p, seq);
+    return QVKV_OK;
+}
+
+int qvkv_seq_fork(qvkv_pool *p, uint32_t parent, uint32_t positions, uint32_t *child) {
+    if (!p || !child) return err(QVKV_E_SHAPE, "shape mismatch in pool: null argument");
+    std::lock_guard<std::mutex> lk(p->mu);
+    const Seq *ps = seq_of(p, parent);
+    if (!ps) return err(QVKV_E_SHAPE, "shape mismatch in pool: no such sequence");
+    for (uint32_t l = 0; l < p->n_layers; l++)
+        if (ps->len[l] < positions)
+            return err(QVKV_E_SHAPE, "shape mismatch in pool: the parent holds fewer positions");
+    const uint32_t h = new_handle(p);  // may reallocate seqs: re-take the parent
+    Seq &c = p->seqs[h];
+    const Seq &pp = p->seqs[parent];
+    const uint32_t B = p->layout.block;
+    const uint32_t nb = (positions + B - 1) / B;
+    for (uint32_t l = 0; l < p->n_layers; l++) {
+        c.blocks[l].assign(pp.blocks[l].begin(), pp.blocks[l].begin() + nb);
+        for (uint32_t b : c.blocks[l]) p->refs[b]++;
+        c.len[l] = positions;
+    }
+    *child = h;
+    return QVKV_OK;
+}
+
+int qvkv_seq_len(const qvkv_pool *p, uint32_t seq, uint32_t layer, uint32_t *out) {
+    if (!p || !out) return err(QVKV_E_SHAPE, "shape mismatch in pool: null argument");
+    std::lock_guard<std::mutex> lk(p->mu);
+    const Seq *s = seq_of(p, seq);
+    if (!s || layer >= p->n_layers) return err(QVKV_E_SHAPE, "shape mismatch in pool: no such sequence or layer");
+    *out = s->len[layer];
+    return QVKV_OK;
+}
+
+int qvkv_seq_touch(qvkv_pool *p, uint32_t seq) {
+    if (!p) return err(QVKV_E_SHAPE, "shape mismatch in pool: null argument");
+    std::lock_guard<std::mutex> lk(p->mu);
+    Seq *s = seq_of(p, seq);
+    if (!s) return err(QVKV_E_SHAPE, "shape mismatch in pool: no such sequence");
+    s->used = ++p->clock;
+    return QVKV_OK;
+}
+
+int qvkv_pool_plan_append(qvkv_pool *p, const uint32_t *seqs, const uint32_t *count,
+                          uint32_t n_seqs, uint32_t layer, uint32_t *slots_out) {
+    if (!p || (n_seqs && (!seqs || !count || !slots_out)))
+        return err(QVKV_E_SHAPE, "shape mismatch in pool: null argument");
+    std::lock_guard<std::mutex> lk(p->mu);
+    if (layer >= p->n_layers) return err(QVKV_E_SHAPE, "shape mismatch in pool: no such layer");
+    const uint32_t B = p->layout.block;
+    // Dry run: blocks this call takes (growth + copies of shared partial blocks), with
+    // the reference counts as they will be when each sequence's turn comes.
+    std::unordered_map<uint32_t, uint32_t> drops;
+    uint64_t need = 0;
+    for (uint32_t i = 0; i < n_seqs; i++) {
+        const Seq *s = seq_of(p, seqs[i]);
+        if (!s) return err(QVKV_E_SHAPE, "shape mismatch in pool: no such sequence");
+        for (uint32_t j = 0; j < i; j++)
+            if (seqs[j] == seqs[i]) return err(QVKV_E_SHAPE, "shape mismatch in pool: a sequence twice in one plan");
+        const uint64_t len = s->len[layer];
+        if (len + count[i] > 0xffffffffull) return err(QVKV_E_SHAPE, "shape mismatch in pool: too many positions");
+        const uint64_t want = (len + count[i] + B - 1) / B;
+        if (want > s->blocks[layer].size()) need += want - s->blocks[layer].size();
+        if (count[i] && len % B != 0) {
+            const uint32_t b = s->blocks[layer][len / B];
+            const uint32_t live = p->refs[b] - drops[b];
+            if (live > 1) {
+                need++;
+                drops[b]++;
+            }
+        }
+    }
+    if (need > p->free.size()) {
+        p->full++;
+        return err(QVKV_E_OOM, "hip device is out of memory: the KV pool has no free block");
+    }
+    std::vector<uint32_t> src, dst;
+    uint64_t o = 0;
+    for (uint32_t i = 0; i < n_seqs; i++) {
+        Seq &s = p->seqs[seqs[i]];
+        auto &tab = s.blocks[layer];
+        const uint32_t len = s.len[layer];
+        if (count[i] && len % B != 0 && p->refs[tab[len / B]] > 1) {
+            const uint32_t old = tab[len / B];
+            const uint32_t nb = p->free.back();
+            p->free.pop_back();
+            p->refs[nb] = 1;
+            p->refs[old]--;
+            tab[len / B] = nb;
+            src.push_back(old);
+            dst.push_back(nb);
+            p->cow++;
+        }
+        const uint64_t want = ((uint64_t)len + count[i] + B - 1) / B;
+        while (tab.size() < want) {
+            const uint32_t nb = p->free.back();
+            p->free.pop_back();
+            p->refs[nb] = 1;
+            tab.push_back(nb);
+        }
+        for (uint32_t k = 0; k < count[i]; k++) {
+            const uint32_t pos = len + k;
+            slots_out[o++] = tab[pos / B] * B + pos % B;
+        }
+        s.len[layer] = len + count[i];
+        s.used = ++p->clock;
+        p->rows += count[i];
+    }
+    p->layers++;
+    // A shared block's filled slots are copied before the caller writes into the copy.
+    return copy_blocks(p, src, dst);
+}
+
+int qvkv_pool_tables(const qvkv_pool *p, const uint32_t *seqs, uint32_t n_seqs, uint32_t layer,
+                     uint32_t *blocks_out, uint64_t blocks_cap, uint64_t *n_table_out,
+                     uint32_t *table_at_out, uint32_t *pos_out) {
+    if (!p || !n_table_out || (n_seqs && (!seqs || !table_at_out || !pos_out)))
+        return err(QVKV_E_SHAPE, "shape mismatch in pool: null argument");
+    std::lock_guard<std::mutex> lk(p->mu);
+    if (layer >= p->n_layers) return err(QVKV_E_SHAPE, "shape mismatch in pool: no such layer");
+    const uint32_t B = p->layout.block;
+    uint64_t at = 0;
+    for (uint32_t i = 0; i < n_seqs; i++) {
+        const Seq *s = seq_of(p, seqs[i]);
+        if (!s) return err(QVKV_E_SHAPE, "shape mismatch in pool: no such sequence");
+        const uint32_t len = s->len[layer];
+        if (len == 0) return err(QVKV_E_SHAPE, "shape mismatch in pool: a sequence with no positions");
+        const uint32_t nb = (len + B - 1) / B;
+        if (at + nb > blocks_cap) return err(QVKV_E_SHAPE, "shape mismatch in pool: blocks_out too small");
+        if (at > 0xffffffffull) return err(QVKV_E_SHAPE, "shape mismatch in pool: table too long");
+        table_at_out[i] = (uint32_t)at;
+        pos_out[i] = len - 1;
+        if (blocks_out) std::copy(s->blocks[layer].begin(), s->blocks[layer].begin() + nb, blocks_out + at);
+        at += nb;
+    }
+    *n_table_out = at;
+    return QVKV_OK;
+}
+
+int qvkv_pool_evict_lru(qvkv_pool *p, uint64_t target_blocks, uint32_t *released_out,
+                        uint32_t cap, uint32_t *n_released) {
+    if (!p || !n_released) return err(QVKV_E_SHAPE, "shape mismatch in pool: null argument");
+    std::lock_guard<std::mutex> lk(p->mu);
+    std::vector<uint32_t> order;
+    for (uint32_t h = 0; h < p->seqs.size(); h++)
+        if (p->seqs[h].live) order.push_back(h);
+    std::sort(order.begin(), order.end(), [&](uint32_t a, uint32_t b) {
+        return p->seqs[a].used != p->seqs[b].used ? p->seqs[a].used < p->seqs[b].used : a < b;
+    });
+    uint64_t freed = 0;
+    uint32_t n = 0;
+    for (uint32_t h : order) {
+        if (freed >= target_blocks) break;
+        freed += release(p, h);
+        if (released_out && n < cap) released_out[n] = h;
+        n++;
+    }
+    p->evicted += freed;
+    *n_released = n;
+    return QVKV_OK;
+}
+
+int qvkv_pool_compact(qvkv_pool *p, uint64_t seed, uint64_t *moved) {
+    if (!p) return err(QVKV_E_SHAPE, "shape mismatch in pool: null argument");
+    std::lock_guard<std::mutex> lk(p->mu);
+    const uint64_t N = p->n_blocks;
+    std::vector<uint32_t> live;
+    for (uint64_t b = 0; b < N; b++)
+        if (p->refs[b]) live.push_back((uint32_t)b);
+    const uint64_t K = live.size();
+    // New id of each live block: position j of the (seeded) permutation of 0..K-1.
+    std::vector<uint32_t> perm(K);
+    std::iota(perm.begin(), perm.end(), 0u);
+    if (seed) {
+        uint64_t st = seed;
+        for (uint64_t i = K; i > 1; i--) std::swap(perm[i - 1], perm[splitmix(st) % i]);
+    }
+    std::vector<int64_t> newid(N, -1);
+    for (uint64_t j = 0; j < K; j++) newid[live[j]] = perm[j];
+    // Pending moves (src -> dst).  A move runs when its dst is vacant; a batch never
+    // reads a block another move of the batch writes.  Cycles are broken through a
+    // spare block (a free id >= K).
+    std::vector<uint8_t> occupied(N, 0);
+    for (uint32_t b : live) occupied[b] = 1;
+    std::vector<std::pair<uint32_t, uint32_t>> pending;
+    for (uint32_t b : live)
+        if ((uint64_t)newid[b] != b) pending.push_back({b, (uint32_t)newid[b]});
+    std::vector<uint32_t> spares;
+    for (uint64_t b = K; b < N; b++)
+        if (!occupied[b]) spares.push_back((uint32_t)b);
+    uint64_t copies = 0;
+    while (!pending.empty()) {
+        std::vector<uint32_t> src, dst;
+        std::vector<std::pair<uint32_t, uint32_t>> rest;
+        for (auto &m : pending) {
+            if (!occupied[m.second]) {
+                src.push_back(m.first);
+                dst.push_back(m.second);
+            } else {
+                rest.push_back(m);
+            }
+        }
+        if (src.empty()) {
+            // Every remaining dst holds data still to move: only cycles are left.  Park
+            // one member of as many cycles as there are spares.
+            if (spares.empty())
+                return err(QVKV_E_OOM, "hip device is out of memory: compaction of a full pool needs one free block");
+            std::vector<uint8_t> in_batch(N, 0);
+            rest.clear();
+            for (auto &m : pending) {
+                // m.first's data goes to a spare unless a member of its cycle was parked
+                // in this batch already (then its dst frees up next round anyway).
+                if (!spares.empty() && !in_batch[m.second] && !in_batch[m.first]) {
+                    const uint32_t sp = spares.back();
+                    spares.pop_back();
+                    src.push_back(m.first);
+                    dst.push_back(sp);
+                    in_batch[m.first] = in_batch[m.second] = 1;
+                    rest.push_back({sp, m.second});
+                } else {
+                    rest.push_back(m);
+                }
+            }
+        }
+        if (int rc = copy_blocks(p, src, dst)) return rc;
+        copies += src.size();
+        for (size_t i = 0; i < src.size(); i++) {
+            occupied[src[i]] = 0;
+            occupied[dst[i]] = 1;
+        }
+        // spares that were read from become spares again
+        for (uint32_t s : src)
+            if (s >= K && !occupied[s]) spares.push_back(s);
+        pending.swap(rest);
+    }
+    // Tables, reference counts and the free list under the new ids.
+    for (auto &s : p->seqs) {
+        if (!s.live) continue;
+        for (auto &l : s.blocks)
+            for (auto &b : l) b = (uint32_t)newid[b];
+    }
+    std::vector<uint32_t> refs(N, 0);
+    for (uint32_t b : live) refs[newid[b]] = p->refs[b];
+    p->refs.swap(refs);
+    p->free.clear();
+    for (uint64_t b = N; b > K; b--) p->free.push_back((uint32_t)(b - 1));
+    p->moved += copies;
+    if (moved) *moved = copies;
+    return QVKV_OK;
+}
+
+int qvkv_pool_refcount(const qvkv_pool *p, uint32_t block, uint32_t *out) {
+    if (!p || !out) return err(QVKV_E_SHAPE, "shape mismatch in pool: null argument");
+    std::lock_guard<std::mutex> lk(p->mu);
+    if (block >= p->n_blocks) return err(QVKV_E_SHAPE, "shape mismatch in pool: no such block");
+    *out = p->refs[block];
+    return QVKV_OK;
+}
+
+}  // extern "C"

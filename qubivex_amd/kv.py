@@ -1,0 +1,324 @@
+"""Host-side mirror of the reference's interface for the paged KV path.
+
+`HipDevice` plays the part of a `DiscreteDevice` backend
+(crates/qubivex-compute/src/discrete.rs:433-570): name/describe/usage/transfers,
+alloc/write, and the KV entry points.  `KvPool` is the runtime's pool and block tables
+(crates/qubivex-runtime/src/discrete.rs:209-290,951-1009) with paged sharing.  Both call
+straight into libqvkv.so; device tensors are torch tensors (plumbing: device memory and
+streams), and every kernel is the library's HIP code.
+"""
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+from ._lib import F16, F32, Q8_0, check, lib
+
+_DTYPES = {"f16": F16, "q8_0": Q8_0}
+
+
+@dataclass(frozen=True)
+class KvLayout:
+    """Storage layout of a pool: dtype ("f16" or "q8_0"), kv_heads, head_dim, block."""
+
+    dtype: str
+    kv_heads: int
+    head_dim: int
+    block: int = 16
+
+    @property
+    def code(self):
+        return _DTYPES[self.dtype]
+
+    @property
+    def c(self):
+        return _lib.Layout(self.code, self.kv_heads, self.head_dim, self.block)
+
+    @property
+    def kv_out(self):
+        return self.kv_heads * self.head_dim
+
+    @property
+    def block_bytes(self):
+        out = ctypes.c_uint64()
+        check(lib.qvkv_block_bytes(ctypes.byref(self.c), ctypes.byref(out)))
+        return out.value
+
+
+def _ptr(x):
+    """Device pointer of a torch tensor (or None)."""
+    if x is None:
+        return None
+    return ctypes.c_void_p(x.data_ptr())
+
+
+def _stream(stream):
+    import torch
+
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _np(a, dtype):
+    a = np.ascontiguousarray(a, dtype=dtype)
+    return a, a.ctypes.data_as(ctypes.c_void_p)
+
+
+class DeviceBuffer:
+    """Device memory from HipDevice.alloc: freed by close() or when collected (the
+    reference's DeviceBuffer, freed on its last clone, discrete.rs:24-95)."""
+
+    def __init__(self, dev, handle):
+        self.dev, self.handle = dev, handle
+
+    @property
+    def ptr(self):
+        return lib.qvkv_buf_ptr(self.handle)
+
+    def __len__(self):
+        return lib.qvkv_buf_len(self.handle)
+
+    def close(self):
+        if self.handle:
+            lib.qvkv_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        self.close()
+
+
+class HipDevice:
+    """One HIP device through libqvkv (the `DiscreteDevice` trait's surface)."""
+
+    def __init__(self, device: int = 0):
+        h = ctypes.c_void_p()
+        check(lib.qvkv_open(device, ctypes.byref(h)))
+        self.handle = h
+
+    # -- DiscreteDevice surface --
+    @staticmethod
+    def name():
+        return "hip"
+
+    def describe(self):
+        buf = ctypes.create_string_buffer(256)
+        check(lib.qvkv_describe(self.handle, buf, len(buf)))
+        return buf.value.decode()
+
+    @staticmethod
+    def supports(dtype: str):
+        return dtype in _DTYPES
+
+    def usage(self):
+        u = _lib.Usage()
+        check(lib.qvkv_usage(self.handle, ctypes.byref(u)))
+        return {k: getattr(u, k) for k, _ in u._fields_}
+
+    def transfers(self):
+        t = _lib.Transfers()
+        check(lib.qvkv_transfers(self.handle, ctypes.byref(t)))
+        return {k: getattr(t, k) for k, _ in t._fields_}
+
+    def alloc(self, n: int) -> DeviceBuffer:
+        h = ctypes.c_void_p()
+        check(lib.qvkv_alloc(self.handle, n, ctypes.byref(h)))
+        return DeviceBuffer(self, h)
+
+    def write(self, buf: DeviceBuffer, offset: int, data: bytes):
+        a, p = _np(np.frombuffer(data, np.uint8), np.uint8)
+        check(lib.qvkv_write(self.handle, buf.handle, offset, p, a.nbytes))
+
+    def read(self, buf: DeviceBuffer, offset: int, n: int) -> bytes:
+        a = np.zeros(n, np.uint8)
+        check(lib.qvkv_read(self.handle, buf.handle, offset, a.ctypes.data_as(ctypes.c_void_p), n))
+        return a.tobytes()
+
+    @property
+    def stream(self):
+        return lib.qvkv_stream(self.handle)
+
+    def check(self, stream=None):
+        """Waits for `stream` and raises ShapeError for an index error a kernel latched."""
+        check(lib.qvkv_check(self.handle, _stream(stream)))
+
+    def close(self):
+        if self.handle:
+            lib.qvkv_close(self.handle)
+            self.handle = None
+
+    # -- the hot path on torch device tensors (enqueued on the current torch stream) --
+    def append(self, layout: KvLayout, pool, pool_blocks, k, v, slots, stream=None):
+        n = slots.numel()
+        check(lib.qvkv_append_async(self.handle, ctypes.byref(layout.c), _ptr(pool), pool_blocks,
+                                    _ptr(k), _ptr(v), _ptr(slots), n, _stream(stream)))
+
+    def gather(self, layout: KvLayout, pool, pool_blocks, blocks, table_at, lens, out_at,
+               max_len, out_k, out_v, out_dtype="f32", stream=None):
+        od = F32 if out_dtype == "f32" else F16
+        elem = 4 if od == F32 else 2
+        out_positions = out_k.numel() * out_k.element_size() // (layout.kv_out * elem)
+        check(lib.qvkv_gather_async(self.handle, ctypes.byref(layout.c), _ptr(pool), pool_blocks,
+                                    _ptr(blocks), blocks.numel(), _ptr(table_at), _ptr(lens),
+                                    _ptr(out_at), lens.numel(), max_len, od, out_positions,
+                                    _ptr(out_k), _ptr(out_v), _stream(stream)))
+
+    def attention(self, layout: KvLayout, pool, pool_blocks, q, blocks, table_at, pos, heads,
+                  max_pos, out, stream=None):
+        check(lib.qvkv_attention_async(self.handle, ctypes.byref(layout.c), _ptr(pool),
+                                       pool_blocks, _ptr(q), _ptr(blocks), blocks.numel(),
+                                       _ptr(table_at), _ptr(pos), pos.numel(), heads, max_pos,
+                                       _ptr(out), _stream(stream)))
+
+    def block_copy(self, layout: KvLayout, pool, pool_blocks, src, dst, stream=None):
+        check(lib.qvkv_block_copy_async(self.handle, ctypes.byref(layout.c), _ptr(pool),
+                                        pool_blocks, _ptr(src), _ptr(dst), src.numel(),
+                                        _stream(stream)))
+
+    # -- host-memory forms (synchronous) --
+    def append_host(self, layout, buf: DeviceBuffer, k, v, slots):
+        k, kp = _np(k, np.float32)
+        v, vp = _np(v, np.float32)
+        s, sp = _np(slots, np.uint32)
+        check(lib.qvkv_append(self.handle, ctypes.byref(layout.c), buf.handle, kp, vp, sp, s.size))
+
+    def gather_host(self, layout, buf: DeviceBuffer, blocks, table_at, lens, out_at,
+                    out_positions, out_dtype="f32"):
+        od = F32 if out_dtype == "f32" else F16
+        npd = np.float32 if od == F32 else np.uint16
+        b, bp = _np(blocks, np.uint32)
+        t, tp = _np(table_at, np.uint32)
+        ln, lp = _np(lens, np.uint32)
+        o, op = _np(out_at, np.uint64)
+        ok = np.zeros(out_positions * layout.kv_out, npd)
+        ov = np.zeros_like(ok)
+        check(lib.qvkv_gather(self.handle, ctypes.byref(layout.c), buf.handle, bp, b.size, tp, lp,
+                              op, ln.size, od, out_positions, ok.ctypes.data_as(ctypes.c_void_p),
+                              ov.ctypes.data_as(ctypes.c_void_p)))
+        return ok, ov
+
+    def block_copy_host(self, layout, buf: DeviceBuffer, src, dst):
+        s, sp = _np(src, np.uint32)
+        d, dp = _np(dst, np.uint32)
+        check(lib.qvkv_block_copy(self.handle, ctypes.byref(layout.c), buf.handle, sp, dp, s.size))
+
+    def decode_attention(self, layout, buf: DeviceBuffer, q, heads, pos, blocks, table_at,
+                         sync, sync_to, k_new, v_new):
+        """One DeviceMoeAttention's KV work (sync rows, new rows, attention), host memory."""
+        q, qp = _np(q, np.float32)
+        pos, pp = _np(pos, np.uint32)
+        b, bp = _np(blocks, np.uint32)
+        t, tp = _np(table_at, np.uint32)
+        sy, syp = _np(sync, np.float32)
+        st, stp = _np(sync_to, np.uint32)
+        kn, knp = _np(k_new, np.float32)
+        vn, vnp = _np(v_new, np.float32)
+        out = np.zeros(pos.size * heads * layout.head_dim, np.float32)
+        check(lib.qvkv_decode_attention(self.handle, ctypes.byref(layout.c), buf.handle, qp, heads,
+                                        pp, pos.size, bp, b.size, tp, syp, stp, st.size, knp, vnp,
+                                        out.ctypes.data_as(ctypes.c_void_p)))
+        return out.reshape(pos.size, heads, layout.head_dim)
+
+    def __del__(self):
+        self.close()
+
+
+class KvPool:
+    """The block pool and block tables (qvkv_pool_*).  dev=None: host-only bookkeeping,
+    whose block copies are returned by take_copies() instead of run."""
+
+    def __init__(self, dev, layout: KvLayout, n_blocks: int, n_layers: int):
+        self.dev, self.layout, self.n_blocks, self.n_layers = dev, layout, n_blocks, n_layers
+        h = ctypes.c_void_p()
+        check(lib.qvkv_pool_create(dev.handle if dev else None, ctypes.byref(layout.c), n_blocks,
+                                   n_layers, ctypes.byref(h)))
+        self.handle = h
+
+    @property
+    def ptr(self):
+        return lib.qvkv_pool_ptr(self.handle)
+
+    def stats(self):
+        s = _lib.PoolStats()
+        check(lib.qvkv_pool_stats(self.handle, ctypes.byref(s)))
+        return {k: getattr(s, k) for k, _ in s._fields_}
+
+    def create(self):
+        h = ctypes.c_uint32()
+        check(lib.qvkv_seq_create(self.handle, ctypes.byref(h)))
+        return h.value
+
+    def release(self, seq):
+        check(lib.qvkv_seq_release(self.handle, seq))
+
+    def fork(self, parent, positions):
+        h = ctypes.c_uint32()
+        check(lib.qvkv_seq_fork(self.handle, parent, positions, ctypes.byref(h)))
+        return h.value
+
+    def length(self, seq, layer=0):
+        n = ctypes.c_uint32()
+        check(lib.qvkv_seq_len(self.handle, seq, layer, ctypes.byref(n)))
+        return n.value
+
+    def touch(self, seq):
+        check(lib.qvkv_seq_touch(self.handle, seq))
+
+    def plan_append(self, seqs, counts, layer):
+        s, sp = _np(seqs, np.uint32)
+        c, cp = _np(counts, np.uint32)
+        out = np.zeros(int(c.sum()), np.uint32)
+        check(lib.qvkv_pool_plan_append(self.handle, sp, cp, s.size, layer,
+                                        out.ctypes.data_as(ctypes.c_void_p)))
+        return out
+
+    def tables(self, seqs, layer):
+        s, sp = _np(seqs, np.uint32)
+        cap = sum((self.length(int(x), layer) + self.layout.block - 1) // self.layout.block
+                  for x in s)
+        blocks = np.zeros(max(cap, 1), np.uint32)
+        table_at = np.zeros(s.size, np.uint32)
+        pos = np.zeros(s.size, np.uint32)
+        n = ctypes.c_uint64()
+        check(lib.qvkv_pool_tables(self.handle, sp, s.size, layer,
+                                   blocks.ctypes.data_as(ctypes.c_void_p), blocks.size,
+                                   ctypes.byref(n), table_at.ctypes.data_as(ctypes.c_void_p),
+                                   pos.ctypes.data_as(ctypes.c_void_p)))
+        return blocks[:n.value], table_at, pos
+
+    def evict_lru(self, target_blocks):
+        cap = 1 << 16
+        out = np.zeros(cap, np.uint32)
+        n = ctypes.c_uint32()
+        check(lib.qvkv_pool_evict_lru(self.handle, target_blocks,
+                                      out.ctypes.data_as(ctypes.c_void_p), cap, ctypes.byref(n)))
+        return out[:min(n.value, cap)].tolist()
+
+    def compact(self, seed=0):
+        moved = ctypes.c_uint64()
+        check(lib.qvkv_pool_compact(self.handle, seed, ctypes.byref(moved)))
+        return moved.value
+
+    def refcount(self, block):
+        r = ctypes.c_uint32()
+        check(lib.qvkv_pool_refcount(self.handle, block, ctypes.byref(r)))
+        return r.value
+
+    def take_copies(self):
+        n = ctypes.c_uint64()
+        check(lib.qvkv_pool_take_copies(self.handle, None, None, 0, ctypes.byref(n)))
+        src = np.zeros(n.value, np.uint32)
+        dst = np.zeros(n.value, np.uint32)
+        if n.value:
+            check(lib.qvkv_pool_take_copies(self.handle, src.ctypes.data_as(ctypes.c_void_p),
+                                            dst.ctypes.data_as(ctypes.c_void_p), n.value,
+                                            ctypes.byref(n)))
+        return src, dst
+
+    def close(self):
+        if self.handle:
+            lib.qvkv_pool_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        self.close()
