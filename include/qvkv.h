@@ -14,8 +14,8 @@
  *  - Functions without the `_async` suffix take HOST memory, run on the device's own
  *    stream and complete before they return (the trait's "completes before return"
  *    semantics, crates/qubivex-backend-vulkan/src/lib.rs:212-225).
- *  - `_async` functions take DEVICE pointers and enqueue on `stream` (a hipStream_t, or
- *    NULL for the device's own stream).  Index errors found by a kernel (a block id
+ *  - `_async` functions take DEVICE pointers and enqueue on `stream`, a hipStream_t used
+ *    as given (0 is HIP's null stream; qvkv_stream() returns the device's own).  Index errors found by a kernel (a block id
  *    past the pool, a table too short) are latched on the device and reported by the
  *    next qvkv_check().  Kernels never touch memory outside the pool for such input.
  *  - A pool position is `slot = block * layout.block + offset` (the reference's
@@ -97,8 +97,8 @@ size_t qvkv_buf_len(const qvkv_buf *buf);
 int qvkv_write(qvkv_dev *dev, qvkv_buf *buf, size_t offset, const void *host, size_t len);
 /* Device bytes back to the host (the readback of k_new/v_new in the reference). */
 int qvkv_read(qvkv_dev *dev, const qvkv_buf *buf, size_t offset, void *host, size_t len);
-/* Waits for `stream` (NULL: the device's) and reports any index error a kernel latched
- * since the last check (QVKV_E_SHAPE), clearing it. */
+/* Waits for `stream` (as given: 0 is the null stream) and reports any index error a
+ * kernel latched since the last check (QVKV_E_SHAPE), clearing it. */
 int qvkv_check(qvkv_dev *dev, void *stream);
 
 /* ---- layout ---- */

@@ -82,9 +82,7 @@ int set_device(qvkv_dev *dev) {
     return e == hipSuccess ? QVKV_OK : hip_fail(e, "hipSetDevice");
 }
 
-hipStream_t pick(qvkv_dev *dev, void *stream) {
-    return stream ? (hipStream_t)stream : dev->stream;
-}
+hipStream_t pick(qvkv_dev *, void *stream) { return (hipStream_t)stream; }
 
 void account_alloc(qvkv_dev *dev, uint64_t n) {
     uint64_t u = dev->used.fetch_add(n) + n;
