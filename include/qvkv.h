@@ -205,8 +205,9 @@ typedef struct qvkv_pool_stats_t {
 int qvkv_pool_create(qvkv_dev *dev, const qvkv_layout *layout, uint64_t n_blocks,
                      uint32_t n_layers, qvkv_pool **out);
 /* Host-only pools: the block copies (src, dst) issued since the last call, in issue
- * order (each batch's pairs are independent).  *n receives the count pending; at most
- * cap pairs are returned and removed. */
+ * order; the pair (UINT32_MAX, UINT32_MAX) ends each batch (one kernel launch, whose
+ * pairs are independent).  *n receives the count pending; at most cap pairs are
+ * returned and removed. */
 int qvkv_pool_take_copies(qvkv_pool *pool, uint32_t *src, uint32_t *dst, uint64_t cap,
                           uint64_t *n);
 void qvkv_pool_destroy(qvkv_pool *pool);
@@ -256,6 +257,42 @@ int qvkv_pool_evict_lru(qvkv_pool *pool, uint64_t target_blocks, uint32_t *relea
 int qvkv_pool_compact(qvkv_pool *pool, uint64_t seed, uint64_t *moved);
 /* Reference count of one block (0 = free). */
 int qvkv_pool_refcount(const qvkv_pool *pool, uint32_t block, uint32_t *out);
+
+/* ---- prefix-cache index ----
+ *
+ * The reference's PrefixCache (crates/qubivex-kv-cache/src/lib.rs:21-223) with its rules
+ * unchanged (MIN_REUSE = 32, longest prefix per scope, last token never reused, LRU,
+ * covering inserts).  A value is an opaque 64-bit handle, normally a pool sequence: a
+ * hit is taken with qvkv_seq_fork(value, reuse), which shares blocks instead of copying
+ * (KvCache::restore_from, crates/qubivex-arch/src/lib.rs:409-432).  Values that leave
+ * the index are queued for qvkv_prefix_take_dropped (the caller releases them). */
+
+typedef struct qvkv_prefix qvkv_prefix;
+
+/* PrefixStats (crates/qubivex-kv-cache/src/lib.rs:44-62). */
+typedef struct qvkv_prefix_stats_t {
+    uint64_t lookups, hits, tokens_reused, inserted, evicted, entries, cost;
+} qvkv_prefix_stats_t;
+
+/* PrefixCache::new (lib.rs:77-92). */
+int qvkv_prefix_create(uint64_t budget, qvkv_prefix **out);
+void qvkv_prefix_destroy(qvkv_prefix *pc);
+/* PrefixCache::lookup (lib.rs:130-157).  scope NULL is the unscoped space.  On a hit
+ * *reuse > 0 and *value is the entry's value; *reuse == 0 means no hit. */
+int qvkv_prefix_lookup(qvkv_prefix *pc, const char *scope, const uint32_t *prompt, uint32_t n,
+                       uint64_t *value, uint32_t *reuse);
+/* PrefixCache::insert (lib.rs:159-195); *kept as its bool. */
+int qvkv_prefix_insert(qvkv_prefix *pc, const char *scope, const uint32_t *tokens, uint32_t n,
+                       uint64_t cost, uint64_t value, int *kept);
+/* PrefixCache::evict_oldest (lib.rs:197-213); *evicted as its bool. */
+int qvkv_prefix_evict_oldest(qvkv_prefix *pc, int *evicted);
+/* PrefixCache::clear (lib.rs:215-219). */
+int qvkv_prefix_clear(qvkv_prefix *pc);
+/* PrefixCache::stats (lib.rs:112-116). */
+int qvkv_prefix_stats(qvkv_prefix *pc, qvkv_prefix_stats_t *out);
+/* Values that left the index (evicted, replaced or cleared) since the last call; *n
+ * receives the count pending, at most cap are returned and removed. */
+int qvkv_prefix_take_dropped(qvkv_prefix *pc, uint64_t *values, uint64_t cap, uint64_t *n);
 
 #ifdef __cplusplus
 }

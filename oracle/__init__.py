@@ -59,6 +59,7 @@ def lib():
         u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
         L.orc_f16_encode.argtypes = [f32p, sz, u16p]
         L.orc_f16_decode.argtypes = [u16p, sz, f32p]
+        L.orc_exp_vec.argtypes = [f32p, sz, f32p]
         _lib = L
     return _lib
 
@@ -101,6 +102,13 @@ def f16_values(h):
 
 def exp(x):
     return float(lib().orc_exp(float(x)))
+
+
+def exp_vec(x):
+    x = _f32(x).reshape(-1)
+    out = np.zeros(x.size, np.float32)
+    lib().orc_exp_vec(x, x.size, out)
+    return out
 
 
 def q8_0_quantize(x):

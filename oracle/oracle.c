@@ -378,6 +378,11 @@ int orc_max_threads(void) {
 #endif
 }
 
+/* Vector form of orc_exp (test convenience). */
+void orc_exp_vec(const float *x, size_t n, float *out) {
+    for (size_t i = 0; i < n; i++) out[i] = orc_exp(x[i]);
+}
+
 /* Vector form of orc_f32_to_f16 (test convenience). */
 void orc_f16_encode(const float *x, size_t n, uint16_t *out) {
     for (size_t i = 0; i < n; i++) out[i] = orc_f32_to_f16(x[i]);

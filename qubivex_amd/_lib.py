@@ -58,6 +58,11 @@ class PoolStats(ctypes.Structure):
                                                 "evicted_blocks", "moved_blocks")]
 
 
+class PrefixStats(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in ("lookups", "hits", "tokens_reused", "inserted",
+                                                "evicted", "entries", "cost")]
+
+
 def _load():
     if not os.path.exists(LIB):
         raise ImportError(
@@ -116,6 +121,14 @@ SIGNATURES = {
     "qvkv_pool_evict_lru": (_i32, [_vp, _u64, _vp, _u32, _P(_u32)]),
     "qvkv_pool_compact": (_i32, [_vp, _u64, _P(_u64)]),
     "qvkv_pool_refcount": (_i32, [_vp, _u32, _P(_u32)]),
+    "qvkv_prefix_create": (_i32, [_u64, _P(_vp)]),
+    "qvkv_prefix_destroy": (None, [_vp]),
+    "qvkv_prefix_lookup": (_i32, [_vp, ctypes.c_char_p, _vp, _u32, _P(_u64), _P(_u32)]),
+    "qvkv_prefix_insert": (_i32, [_vp, ctypes.c_char_p, _vp, _u32, _u64, _u64, _P(_i32)]),
+    "qvkv_prefix_evict_oldest": (_i32, [_vp, _P(_i32)]),
+    "qvkv_prefix_clear": (_i32, [_vp]),
+    "qvkv_prefix_stats": (_i32, [_vp, _P(PrefixStats)]),
+    "qvkv_prefix_take_dropped": (_i32, [_vp, _vp, _u64, _P(_u64)]),
 }
 
 for _name, (_res, _args) in SIGNATURES.items():

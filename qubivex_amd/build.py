@@ -16,7 +16,7 @@ LIB = os.path.join(OUT_DIR, "libqvkv.so")
 ARCH = os.environ.get("QVKV_ARCH", "gfx950")
 
 HIP_SOURCES = ["kernels.hip", "abi.hip"]
-CXX_SOURCES = ["pool.cpp"]
+CXX_SOURCES = ["pool.cpp", "prefix.cpp"]
 
 
 def _run(cmd, verbose):

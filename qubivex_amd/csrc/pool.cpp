@@ -103,6 +103,8 @@ int copy_blocks(qvkv_pool *p, const std::vector<uint32_t> &src, const std::vecto
     if (!p->dev) {
         p->log_src.insert(p->log_src.end(), src.begin(), src.end());
         p->log_dst.insert(p->log_dst.end(), dst.begin(), dst.end());
+        p->log_src.push_back(UINT32_MAX);  // end of one batch (one kernel launch)
+        p->log_dst.push_back(UINT32_MAX);
         return QVKV_OK;
     }
     return qvkv_block_copy(p->dev, &p->layout, p->buf, src.data(), dst.data(), (uint32_t)src.size());

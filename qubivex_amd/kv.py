@@ -92,6 +92,7 @@ class HipDevice:
     """One HIP device through libqvkv (the `DiscreteDevice` trait's surface)."""
 
     def __init__(self, device: int = 0):
+        self.handle = None
         h = ctypes.c_void_p()
         check(lib.qvkv_open(device, ctypes.byref(h)))
         self.handle = h
@@ -223,12 +224,97 @@ class HipDevice:
         self.close()
 
 
+class PrefixCache:
+    """The prefix-cache index (qvkv_prefix_*), the reference's PrefixCache<V>
+    (crates/qubivex-kv-cache/src/lib.rs:68-219).  Values may be any Python object (held
+    here by id); the C index stores the id.  A paged caller stores pool sequence handles
+    and takes a hit with KvPool.fork(value, reuse)."""
+
+    def __init__(self, budget: int):
+        h = ctypes.c_void_p()
+        check(lib.qvkv_prefix_create(budget, ctypes.byref(h)))
+        self.handle = h
+        self.budget = budget
+        self._values = {}
+        self._next = 1
+
+    @staticmethod
+    def _scope(scope):
+        return None if scope is None else scope.encode()
+
+    def lookup(self, scope, prompt):
+        """(value, reuse) of the longest usable prefix, or None."""
+        p, pp = _np(prompt, np.uint32)
+        val, reuse = ctypes.c_uint64(), ctypes.c_uint32()
+        check(lib.qvkv_prefix_lookup(self.handle, self._scope(scope), pp, p.size,
+                                     ctypes.byref(val), ctypes.byref(reuse)))
+        if reuse.value == 0:
+            return None
+        return self._values[val.value], reuse.value
+
+    def insert(self, scope, tokens, cost, value):
+        t, tp = _np(tokens, np.uint32)
+        key = self._next
+        self._next += 1
+        self._values[key] = value
+        kept = ctypes.c_int()
+        check(lib.qvkv_prefix_insert(self.handle, self._scope(scope), tp, t.size, cost, key,
+                                     ctypes.byref(kept)))
+        if not kept.value:
+            del self._values[key]
+        self._forget_dropped()
+        return bool(kept.value)
+
+    def evict_oldest(self):
+        ev = ctypes.c_int()
+        check(lib.qvkv_prefix_evict_oldest(self.handle, ctypes.byref(ev)))
+        self._forget_dropped()
+        return bool(ev.value)
+
+    def clear(self):
+        check(lib.qvkv_prefix_clear(self.handle))
+        self._forget_dropped()
+
+    def cost(self):
+        return self.stats()["cost"]
+
+    def stats(self):
+        s = _lib.PrefixStats()
+        check(lib.qvkv_prefix_stats(self.handle, ctypes.byref(s)))
+        return {k: getattr(s, k) for k, _ in s._fields_}
+
+    def _forget_dropped(self):
+        self.dropped = getattr(self, "dropped", [])
+        n = ctypes.c_uint64()
+        check(lib.qvkv_prefix_take_dropped(self.handle, None, 0, ctypes.byref(n)))
+        if n.value:
+            out = np.zeros(n.value, np.uint64)
+            check(lib.qvkv_prefix_take_dropped(self.handle, out.ctypes.data_as(ctypes.c_void_p),
+                                               n.value, ctypes.byref(n)))
+            for key in out.tolist():
+                self.dropped.append(self._values.pop(key))
+
+    def take_dropped(self):
+        """Values that left the index since the last call (evicted, replaced, cleared)."""
+        d, self.dropped = getattr(self, "dropped", []), []
+        return d
+
+    def close(self):
+        if self.handle:
+            lib.qvkv_prefix_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        self.close()
+
+
 class KvPool:
     """The block pool and block tables (qvkv_pool_*).  dev=None: host-only bookkeeping,
     whose block copies are returned by take_copies() instead of run."""
 
     def __init__(self, dev, layout: KvLayout, n_blocks: int, n_layers: int):
         self.dev, self.layout, self.n_blocks, self.n_layers = dev, layout, n_blocks, n_layers
+        self.handle = None
         h = ctypes.c_void_p()
         check(lib.qvkv_pool_create(dev.handle if dev else None, ctypes.byref(layout.c), n_blocks,
                                    n_layers, ctypes.byref(h)))
@@ -314,6 +400,17 @@ class KvPool:
                                             dst.ctypes.data_as(ctypes.c_void_p), n.value,
                                             ctypes.byref(n)))
         return src, dst
+
+    def take_batches(self):
+        """Host-only pools: the block copies issued since the last call, as a list of
+        (src, dst) arrays, one per batch (kernel launch)."""
+        src, dst = self.take_copies()
+        cut = np.nonzero(src == 0xFFFFFFFF)[0]
+        out, start = [], 0
+        for c in cut:
+            out.append((src[start:c], dst[start:c]))
+            start = c + 1
+        return out
 
     def close(self):
         if self.handle:
