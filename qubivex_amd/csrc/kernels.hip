@@ -22,6 +22,7 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include "internal.h"
 
@@ -66,7 +67,58 @@ __device__ __forceinline__ uint32_t vperm(uint32_t d, uint32_t D) {
 // quantizer: d = amax/127 (f32), scale = f16(d) RNE, inv = d > 0 ? 1/d : 0 from the
 // f32 d, q = clamp(round_half_away(x*inv), -127, 127), NaN -> 0.
 // ---------------------------------------------------------------------------------
-template <int DT>
+typedef float f4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+
+template <bool NT>
+__device__ __forceinline__ float4 load_f4(const float *p) {
+    if constexpr (NT) {
+        const f4v x = __builtin_nontemporal_load((const f4v *)p);
+        return make_float4(x.x, x.y, x.z, x.w);
+    } else {
+        return *(const float4 *)p;
+    }
+}
+
+// One 8-value chunk: where it comes from and where it goes.
+struct AppendItem {
+    const float *src;
+    uint8_t *base;     // its block
+    uint64_t rowidx;   // (head, position) row inside the K or V region
+    uint32_t i;        // first value's index along d
+    bool isv, ok;
+};
+
+__device__ __forceinline__ AppendItem append_item(uint32_t w, uint32_t total, uint32_t cpr,
+                                                  uint8_t *pool, uint64_t pool_blocks,
+                                                  const float *k, const float *v,
+                                                  const uint32_t *slots, const Geo &geo,
+                                                  int *err) {
+    AppendItem it{};
+    it.ok = false;
+    if (w >= total) return it;
+    const uint32_t D = (uint32_t)geo.D, B = (uint32_t)geo.B;
+    const uint32_t row = w / (2u * cpr);
+    const uint32_t rem = w - row * 2u * cpr;
+    it.isv = rem >= cpr;
+    const uint32_t e = (it.isv ? rem - cpr : rem) * 8u;
+    const uint32_t g = e / D;
+    it.i = e - g * D;
+    const uint32_t slot = slots[row];
+    const uint32_t blk = slot / B;
+    if (blk >= pool_blocks) {  // whole rows: every lane of a q8_0 group agrees
+        flag(err, ERR_BLOCK);
+        return it;
+    }
+    it.src = (it.isv ? v : k) + (uint64_t)row * geo.kv_out + e;
+    it.base = pool + (uint64_t)blk * geo.bb;
+    it.rowidx = (uint64_t)g * B + (slot - blk * B);
+    it.ok = true;
+    return it;
+}
+
+// U chunks per thread per round, all loads issued before any store.
+template <int DT, int U, bool NT>
 __global__ __launch_bounds__(256) void k_append(uint8_t *__restrict__ pool, uint64_t pool_blocks,
                                                 const float *__restrict__ k,
                                                 const float *__restrict__ v,
@@ -74,25 +126,27 @@ __global__ __launch_bounds__(256) void k_append(uint8_t *__restrict__ pool, uint
                                                 Geo geo, int *err) {
     const uint32_t cpr = geo.kv_out >> 3;  // 8-value chunks per K (or V) row
     const uint32_t total = n * 2u * cpr;
-    const uint32_t D = (uint32_t)geo.D, B = (uint32_t)geo.B;
-    for (uint32_t w = blockIdx.x * 256u + threadIdx.x; w < total; w += gridDim.x * 256u) {
-        const uint32_t row = w / (2u * cpr);
-        uint32_t rem = w - row * 2u * cpr;
-        const bool isv = rem >= cpr;
-        const uint32_t e = (isv ? rem - cpr : rem) * 8u;
-        const uint32_t g = e / D, i = e - g * D;
-        const uint32_t slot = slots[row];
-        const uint64_t blk = slot / B;
-        const uint32_t off = slot - (uint32_t)blk * B;
-        if (blk >= pool_blocks) {  // whole rows: every lane of a q8_0 group agrees
-            flag(err, ERR_BLOCK);
-            continue;
+    const uint32_t D = (uint32_t)geo.D;
+    for (uint32_t b0 = blockIdx.x * 256u * U; b0 < total; b0 += gridDim.x * 256u * U) {
+        AppendItem its[U];
+        float4 xa[U], xb[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            its[u] = append_item(b0 + u * 256u + threadIdx.x, total, cpr, pool, pool_blocks, k, v,
+                                 slots, geo, err);
+            if (its[u].ok) {
+                xa[u] = load_f4<NT>(its[u].src);
+                xb[u] = load_f4<NT>(its[u].src + 4);
+            }
         }
-        const float *src = (isv ? v : k) + (uint64_t)row * geo.kv_out + e;
-        const float4 x0 = *(const float4 *)src;
-        const float4 x1 = *(const float4 *)(src + 4);
-        uint8_t *base = pool + blk * geo.bb;
-        const uint64_t rowidx = (uint64_t)g * B + off;  // (head, position) row in its region
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+        if (!its[u].ok) continue;
+        const float4 x0 = xa[u], x1 = xb[u];
+        uint8_t *base = its[u].base;
+        const uint64_t rowidx = its[u].rowidx;
+        const uint32_t i = its[u].i;
+        const bool isv = its[u].isv;
         if (DT == QVKV_F16) {
             uint4 o;
             o.x = pack_h2(x0.x, x0.y);
@@ -138,6 +192,7 @@ __global__ __launch_bounds__(256) void k_append(uint8_t *__restrict__ pool, uint
                 }
             }
         }
+        }
     }
 }
 
@@ -182,6 +237,35 @@ __global__ __launch_bounds__(256) void k_gather(const uint8_t *__restrict__ pool
     const uint8_t *base = pool + (uint64_t)blk * geo.bb;
     const uint32_t c8 = D >> 3;                 // 8-value chunks per row
     const uint32_t per_kv = G * 16u * c8;       // chunks per tile for K (or V)
+    if (DT == QVKV_F16 && OUT == QVKV_F16) {
+        // A byte copy of the tile's rows: 8 loads in flight per thread, then 8 stores.
+        constexpr int U = 8;
+        for (uint32_t b0 = 0; b0 < 2u * per_kv; b0 += 256u * U) {
+            u4v x[U];
+            uint16_t *dst[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                dst[u] = nullptr;
+                const uint32_t idx = b0 + u * 256u + threadIdx.x;
+                if (idx >= 2u * per_kv) continue;
+                const bool isv = idx >= per_kv;
+                uint32_t r = isv ? idx - per_kv : idx;
+                const uint32_t e = (r % c8) * 8u;
+                r /= c8;
+                const uint32_t row = r & 15u, g = r >> 4, p = p0 + row;
+                if (p >= len) continue;
+                x[u] = __builtin_nontemporal_load(
+                    (const u4v *)(base + (isv ? geo.v_off : geo.k_off) +
+                                  (((uint64_t)g * B + r0 + row) * D + e) * 2u));
+                dst[u] = (uint16_t *)(isv ? out_v : out_k) + oat * (uint64_t)G * D +
+                         ((uint64_t)g * len + p) * D + e;
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++)
+                if (dst[u]) *(u4v *)dst[u] = x[u];
+        }
+        return;
+    }
     for (uint32_t idx = threadIdx.x; idx < 2u * per_kv; idx += 256u) {
         const bool isv = idx >= per_kv;
         uint32_t r = isv ? idx - per_kv : idx;
@@ -235,8 +319,9 @@ __global__ __launch_bounds__(256) void k_gather(const uint8_t *__restrict__ pool
 }
 
 // ---------------------------------------------------------------------------------
-// Block copy: workgroup = 16 KiB of one (src, dst) pair.
+// Block copy: workgroup = U * 4 KiB of one (src, dst) pair, all loads before stores.
 // ---------------------------------------------------------------------------------
+template <int U>
 __global__ __launch_bounds__(256) void k_block_copy(uint8_t *__restrict__ pool,
                                                     uint64_t pool_blocks,
                                                     const uint32_t *__restrict__ src,
@@ -251,19 +336,18 @@ __global__ __launch_bounds__(256) void k_block_copy(uint8_t *__restrict__ pool,
         if (threadIdx.x == 0 && part == 0) flag(err, ERR_BLOCK);
         return;
     }
-    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
-    const u4 *from = (const u4 *)(pool + (uint64_t)s * bb);
-    u4 *to = (u4 *)(pool + (uint64_t)d * bb);
+    const u4v *from = (const u4v *)(pool + (uint64_t)s * bb);
+    u4v *to = (u4v *)(pool + (uint64_t)d * bb);
     const uint64_t words = bb >> 4;
-    const uint64_t begin = (uint64_t)part * 1024u;  // 1024 x 16 B per workgroup
-    u4 r[4];
+    const uint64_t begin = (uint64_t)part * 256u * U;
+    u4v r[U];
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
+    for (int u = 0; u < U; u++) {
         const uint64_t i = begin + threadIdx.x + u * 256u;
         if (i < words) r[u] = __builtin_nontemporal_load(from + i);
     }
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
+    for (int u = 0; u < U; u++) {
         const uint64_t i = begin + threadIdx.x + u * 256u;
         if (i < words) __builtin_nontemporal_store(r[u], to + i);
     }
@@ -298,23 +382,208 @@ __device__ __forceinline__ _Float16 split_part(float x, bool hi_part) {
     return hi_part ? hi : lo;
 }
 
-template <int NB>
+typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+
+// NB bytes (4, 8 or a multiple of 16) into words; NT: non-temporal (streamed once).
+template <int NB, bool NT>
 __device__ __forceinline__ void load_bytes(const uint8_t *p, uint32_t *w) {
     if constexpr (NB == 4) {
-        w[0] = *(const uint32_t *)p;
+        w[0] = NT ? __builtin_nontemporal_load((const uint32_t *)p) : *(const uint32_t *)p;
     } else if constexpr (NB == 8) {
-        const uint2 x = *(const uint2 *)p;
+        const u2v x = NT ? __builtin_nontemporal_load((const u2v *)p) : *(const u2v *)p;
         w[0] = x.x; w[1] = x.y;
     } else {
 #pragma unroll
         for (int i = 0; i < NB / 16; i++) {
-            const uint4 x = *(const uint4 *)(p + 16 * i);
+            const u4v x = NT ? __builtin_nontemporal_load((const u4v *)(p + 16 * i))
+                             : *(const u4v *)(p + 16 * i);
             w[4 * i] = x.x; w[4 * i + 1] = x.y; w[4 * i + 2] = x.z; w[4 * i + 3] = x.w;
         }
     }
 }
 
+template <int NB>
+__device__ __forceinline__ void load_bytes(const uint8_t *p, uint32_t *w) {
+    load_bytes<NB, false>(p, w);
+}
+
+// One 16-position tile's operands for one lane, as loaded from the pool.
 template <int D, bool Q8>
+struct Tile {
+    static constexpr int KW = Q8 ? D / 16 : D / 8;                    // key words
+    static constexpr int VW = Q8 ? (D / 64 > 0 ? D / 64 : 1) : D / 32;  // value words per row
+    static constexpr int SW = Q8 ? 2 * (D / 32) : 1;                  // scale words (4 rows)
+    uint32_t k[KW];
+    uint32_t v[4][VW];
+    uint32_t ks[SW], vs[SW];
+    uint32_t p0;
+    bool ok;
+};
+
+template <int D, bool Q8, bool NT>
+__device__ __forceinline__ void load_tile(Tile<D, Q8> &t, uint32_t tt, const uint8_t *pool,
+                                          uint64_t pool_blocks, const uint32_t *blocks,
+                                          uint32_t tab, uint32_t g, uint32_t c, uint32_t qg,
+                                          const Geo &geo, int *err) {
+    const uint32_t B = (uint32_t)geo.B;
+    t.p0 = tt * 16u;
+    const uint32_t blk = blocks[tab + t.p0 / B];
+    t.ok = blk < pool_blocks;
+    if (!t.ok) {
+        if ((threadIdx.x & 63u) == 0) flag(err, ERR_BLOCK);
+        return;
+    }
+    const uint8_t *base = pool + (uint64_t)blk * geo.bb;
+    const uint64_t rows = (uint64_t)g * B + t.p0 % B;  // first (head, position) row of the tile
+    if constexpr (!Q8) {
+        // K row c: 16-byte pieces at d = 32i + 8qg; V rows 4qg..4qg+3 at d = c*D/16
+        const uint8_t *kr = base + geo.k_off + ((rows + c) * D + 8 * qg) * 2u;
+#pragma unroll
+        for (int i = 0; i < D / 32; i++) load_bytes<16, NT>(kr + 64u * i, t.k + 4 * i);
+        const uint8_t *vr = base + geo.v_off + ((rows + 4 * qg) * D + c * (D / 16)) * 2u;
+#pragma unroll
+        for (int i = 0; i < 4; i++) load_bytes<D / 8, NT>(vr + (uint64_t)i * D * 2u, t.v[i]);
+    } else {
+        load_bytes<D / 4, NT>(base + geo.k_off + (rows + c) * D + qg * (D / 4), t.k);
+        load_bytes<8 * (D / 32), NT>(base + geo.ks_off + (rows + 4 * qg) * (D / 32) * 2u, t.ks);
+        load_bytes<8 * (D / 32), NT>(base + geo.vs_off + (rows + 4 * qg) * (D / 32) * 2u, t.vs);
+        const uint8_t *vr = base + geo.v_off + (rows + 4 * qg) * D + c * (D / 16);
+#pragma unroll
+        for (int i = 0; i < 4; i++) load_bytes<D / 16, NT>(vr + (uint64_t)i * D, t.v[i]);
+    }
+}
+
+// Online-softmax state of one lane: running max and partial sum (head c % 8), and the
+// output accumulator (rows 4qg..4qg+3 of the MFMA tile, columns by d mapping).
+template <int D>
+struct SoftmaxState {
+    float m, l;
+    f4 acc[D / 16];
+};
+
+template <int D, bool Q8>
+__device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<D> &st,
+                                             const h4 *qf, uint32_t n, uint32_t qg, bool hi_col) {
+    constexpr int NJ = D / 16;
+    constexpr int NG = D / 32;
+    if (!t.ok) return;
+    const uint32_t p0 = t.p0;
+    // ---- scores S^T[position][column] = K . Q^T
+    f4 s = f4{0.f, 0.f, 0.f, 0.f};
+    float vsc[4][NG];
+    uint32_t vw[4][Tile<D, Q8>::VW];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int x = 0; x < Tile<D, Q8>::VW; x++) vw[i][x] = t.v[i][x];
+    if constexpr (!Q8) {
+#pragma unroll
+        for (int i = 0; i < NG; i++) {
+            s = __builtin_amdgcn_mfma_f32_16x16x16f16(h4_of(t.k[4 * i], t.k[4 * i + 1]), qf[2 * i], s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_16x16x16f16(h4_of(t.k[4 * i + 2], t.k[4 * i + 3]), qf[2 * i + 1], s, 0, 0, 0);
+        }
+    } else {
+        const _Float16 *ksh = (const _Float16 *)t.ks;
+        const _Float16 *vsh = (const _Float16 *)t.vs;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int gi = 0; gi < NG; gi++) vsc[i][gi] = (float)vsh[i * NG + gi];
+#pragma unroll
+        for (int gi = 0; gi < NG; gi++) {
+            f4 sg = f4{0.f, 0.f, 0.f, 0.f};
+            sg = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4(t.k[2 * gi]), qf[2 * gi], sg, 0, 0, 0);
+            sg = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4(t.k[2 * gi + 1]), qf[2 * gi + 1], sg, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) s[i] = fmaf(sg[i], (float)ksh[i * NG + gi], s[i]);
+        }
+    }
+
+    // ---- high + residual columns, mask, online softmax (log2 domain)
+    float sc[4];
+    const bool partial = p0 + 16u > n;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float v2 = s[i] + __shfl_xor(s[i], 8);
+        if (partial && p0 + 4 * qg + i >= n) v2 = -INFINITY;
+        sc[i] = v2;
+    }
+    float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float mnew = fmaxf(st.m, tmax);
+    const float msafe = mnew == -INFINITY ? 0.0f : mnew;
+    const float alpha = __builtin_amdgcn_exp2f(st.m - msafe);
+    float pr[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) pr[i] = __builtin_amdgcn_exp2f(sc[i] - msafe);
+    st.l = st.l * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
+    if (__any(mnew > st.m)) {
+        float ar[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) ar[i] = __shfl(alpha, 4 * qg + i);
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) st.acc[j][i] *= ar[i];
+    }
+    st.m = mnew;
+
+    // ---- O += P . V
+    if constexpr (!Q8) {
+        if (partial) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (p0 + 4 * qg + i >= n)
+#pragma unroll
+                    for (int x = 0; x < D / 32; x++) vw[i][x] = 0u;
+        }
+        const h4 pa = h4{split_part(pr[0], hi_col), split_part(pr[1], hi_col),
+                         split_part(pr[2], hi_col), split_part(pr[3], hi_col)};
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+            const uint32_t w0 = __builtin_amdgcn_perm(vw[1][j >> 1], vw[0][j >> 1], sel);
+            const uint32_t w1 = __builtin_amdgcn_perm(vw[3][j >> 1], vw[2][j >> 1], sel);
+            st.acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, h4_of(w0, w1), st.acc[j], 0, 0, 0);
+        }
+    } else {
+        if (partial) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (p0 + 4 * qg + i >= n) {
+#pragma unroll
+                    for (int x = 0; x < Tile<D, Q8>::VW; x++) vw[i][x] = 0u;
+#pragma unroll
+                    for (int gi = 0; gi < NG; gi++) vsc[i][gi] = 0.0f;
+                }
+        }
+#pragma unroll
+        for (int gi = 0; gi < NG; gi++) {
+            const h4 pa = h4{split_part(pr[0] * vsc[0][gi], hi_col),
+                             split_part(pr[1] * vsc[1][gi], hi_col),
+                             split_part(pr[2] * vsc[2][gi], hi_col),
+                             split_part(pr[3] * vsc[3][gi], hi_col)};
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const int j = 2 * gi + u;
+                const uint32_t bsel = (uint32_t)(j & 3);
+                const uint32_t sel = 0x0c000c00u | ((4u + bsel) << 16) | bsel;
+                const uint32_t a01 = __builtin_amdgcn_perm(vw[1][j >> 2] ^ 0x80808080u,
+                                                           vw[0][j >> 2] ^ 0x80808080u, sel) | 0x64006400u;
+                const uint32_t a23 = __builtin_amdgcn_perm(vw[3][j >> 2] ^ 0x80808080u,
+                                                           vw[2][j >> 2] ^ 0x80808080u, sel) | 0x64006400u;
+                const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+                const h2 x01 = __builtin_bit_cast(h2, a01) - bias;
+                const h2 x23 = __builtin_bit_cast(h2, a23) - bias;
+                st.acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, h4{x01.x, x01.y, x23.x, x23.y},
+                                                                  st.acc[j], 0, 0, 0);
+            }
+        }
+    }
+}
+
+template <int D, bool Q8, bool NT>
 __global__ __launch_bounds__(256) void k_attn_mfma(
     const uint8_t *__restrict__ pool, uint64_t pool_blocks, const float *__restrict__ q,
     const uint32_t *__restrict__ blocks, uint64_t n_table, const uint32_t *__restrict__ table_at,
@@ -371,150 +640,20 @@ __global__ __launch_bounds__(256) void k_attn_mfma(
         }
     }
 
-    float m = -INFINITY, l = 0.0f;
-    f4 acc[NJ];
+    SoftmaxState<D> st;
+    st.m = -INFINITY;
+    st.l = 0.0f;
 #pragma unroll
-    for (int j = 0; j < NJ; j++) acc[j] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NJ; j++) st.acc[j] = f4{0.f, 0.f, 0.f, 0.f};
 
     for (uint32_t tt = t_begin + w; tt < t_end; tt += 4) {
-        const uint32_t p0 = tt * 16u;
-        const uint32_t blk = blocks[tab + p0 / B];
-        if (blk >= pool_blocks) {
-            if (lane == 0) flag(err, ERR_BLOCK);
-            continue;
-        }
-        const uint32_t r0 = p0 % B;
-        const uint8_t *base = pool + (uint64_t)blk * geo.bb;
-        const uint64_t rows = (uint64_t)g * B + r0;  // first (head, position) row of the tile
-
-        // ---- scores S^T[position][column] = K . Q^T
-        f4 s = f4{0.f, 0.f, 0.f, 0.f};
-        float vsc[4][NG];
-        uint32_t vw[4][Q8 ? D / 64 > 0 ? D / 64 : 1 : D / 32];
-        if constexpr (!Q8) {
-            const _Float16 *kr = (const _Float16 *)(base + geo.k_off) + (rows + c) * D;
-            uint4 kv[NG];
-#pragma unroll
-            for (int i = 0; i < NG; i++) kv[i] = *(const uint4 *)(kr + 32 * i + 8 * qg);
-            // V rows 4qg..4qg+3, columns c*D/16 .. +D/16 (issued early: independent of S)
-            const uint8_t *vr = base + geo.v_off + ((rows + 4 * qg) * D + c * (D / 16)) * 2u;
-#pragma unroll
-            for (int i = 0; i < 4; i++) load_bytes<D / 8>(vr + (uint64_t)i * D * 2u, vw[i]);
-#pragma unroll
-            for (int i = 0; i < NG; i++) {
-                s = __builtin_amdgcn_mfma_f32_16x16x16f16(h4_of(kv[i].x, kv[i].y), qf[2 * i], s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_16x16x16f16(h4_of(kv[i].z, kv[i].w), qf[2 * i + 1], s, 0, 0, 0);
-            }
-        } else {
-            const uint8_t *kr = base + geo.k_off + (rows + c) * D + qg * (D / 4);
-            uint32_t kw[D / 16];
-            load_bytes<D / 4>(kr, kw);
-            // scales of rows 4qg..4qg+3: 4*NG f16, contiguous
-            const _Float16 *ksp = (const _Float16 *)(base + geo.ks_off) + (rows + 4 * qg) * NG;
-            const _Float16 *vsp = (const _Float16 *)(base + geo.vs_off) + (rows + 4 * qg) * NG;
-            _Float16 ksh[4 * NG], vsh[4 * NG];
-            load_bytes<8 * NG>((const uint8_t *)ksp, (uint32_t *)ksh);
-            load_bytes<8 * NG>((const uint8_t *)vsp, (uint32_t *)vsh);
-            const uint8_t *vr = base + geo.v_off + (rows + 4 * qg) * D + c * (D / 16);
-#pragma unroll
-            for (int i = 0; i < 4; i++) load_bytes<D / 16>(vr + (uint64_t)i * D, vw[i]);
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int gi = 0; gi < NG; gi++) vsc[i][gi] = (float)vsh[i * NG + gi];
-#pragma unroll
-            for (int gi = 0; gi < NG; gi++) {
-                f4 sg = f4{0.f, 0.f, 0.f, 0.f};
-                sg = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4(kw[2 * gi]), qf[2 * gi], sg, 0, 0, 0);
-                sg = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4(kw[2 * gi + 1]), qf[2 * gi + 1], sg, 0, 0, 0);
-#pragma unroll
-                for (int i = 0; i < 4; i++) s[i] = fmaf(sg[i], (float)ksh[i * NG + gi], s[i]);
-            }
-        }
-
-        // ---- high + residual columns, mask, online softmax (log2 domain)
-        float sc[4];
-        const bool partial = p0 + 16u > n;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float v2 = s[i] + __shfl_xor(s[i], 8);
-            if (partial && p0 + 4 * qg + i >= n) v2 = -INFINITY;
-            sc[i] = v2;
-        }
-        float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        const float mnew = fmaxf(m, tmax);
-        const float msafe = mnew == -INFINITY ? 0.0f : mnew;
-        const float alpha = __builtin_amdgcn_exp2f(m - msafe);
-        float pr[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) pr[i] = __builtin_amdgcn_exp2f(sc[i] - msafe);
-        l = l * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
-        if (__any(mnew > m)) {
-            float ar[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) ar[i] = __shfl(alpha, 4 * qg + i);
-#pragma unroll
-            for (int j = 0; j < NJ; j++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) acc[j][i] *= ar[i];
-        }
-        m = mnew;
-
-        // ---- O += P . V
-        if constexpr (!Q8) {
-            if (partial) {
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    if (p0 + 4 * qg + i >= n)
-#pragma unroll
-                        for (int x = 0; x < D / 32; x++) vw[i][x] = 0u;
-            }
-            const h4 pa = h4{split_part(pr[0], hi_col), split_part(pr[1], hi_col),
-                             split_part(pr[2], hi_col), split_part(pr[3], hi_col)};
-#pragma unroll
-            for (int j = 0; j < NJ; j++) {
-                const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-                const uint32_t w0 = __builtin_amdgcn_perm(vw[1][j >> 1], vw[0][j >> 1], sel);
-                const uint32_t w1 = __builtin_amdgcn_perm(vw[3][j >> 1], vw[2][j >> 1], sel);
-                acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, h4_of(w0, w1), acc[j], 0, 0, 0);
-            }
-        } else {
-            if (partial) {
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    if (p0 + 4 * qg + i >= n) {
-#pragma unroll
-                        for (int x = 0; x < (D / 64 > 0 ? D / 64 : 1); x++) vw[i][x] = 0u;
-#pragma unroll
-                        for (int gi = 0; gi < NG; gi++) vsc[i][gi] = 0.0f;
-                    }
-            }
-#pragma unroll
-            for (int gi = 0; gi < NG; gi++) {
-                const h4 pa = h4{split_part(pr[0] * vsc[0][gi], hi_col),
-                                 split_part(pr[1] * vsc[1][gi], hi_col),
-                                 split_part(pr[2] * vsc[2][gi], hi_col),
-                                 split_part(pr[3] * vsc[3][gi], hi_col)};
-#pragma unroll
-                for (int u = 0; u < 2; u++) {
-                    const int j = 2 * gi + u;
-                    const uint32_t bsel = (uint32_t)(j & 3);
-                    const uint32_t sel = 0x0c000c00u | ((4u + bsel) << 16) | bsel;
-                    const uint32_t a01 = __builtin_amdgcn_perm(vw[1][j >> 2] ^ 0x80808080u,
-                                                               vw[0][j >> 2] ^ 0x80808080u, sel) | 0x64006400u;
-                    const uint32_t a23 = __builtin_amdgcn_perm(vw[3][j >> 2] ^ 0x80808080u,
-                                                               vw[2][j >> 2] ^ 0x80808080u, sel) | 0x64006400u;
-                    const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
-                    const h2 x01 = __builtin_bit_cast(h2, a01) - bias;
-                    const h2 x23 = __builtin_bit_cast(h2, a23) - bias;
-                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, h4{x01.x, x01.y, x23.x, x23.y},
-                                                                   acc[j], 0, 0, 0);
-                }
-            }
-        }
+        Tile<D, Q8> cur;
+        load_tile<D, Q8, NT>(cur, tt, pool, pool_blocks, blocks, tab, g, c, qg, geo, err);
+        compute_tile<D, Q8>(cur, st, qf, n, qg, hi_col);
     }
+    float l = st.l;
+    const float m = st.m;
+    f4 *acc = st.acc;
 
     // ---- wave totals: l over the 4 row groups; O high rows + residual rows
     l += __shfl_xor(l, 16);
@@ -758,6 +897,13 @@ int make_geometry(const qvkv_layout *l, Geometry *g, const char **why) {
     return QVKV_OK;
 }
 
+// Launch-shape knobs (defaults are the measured best); an environment variable of the
+// same name overrides one for measurement.
+static int tune(const char *name, int def) {
+    const char *s = getenv(name);
+    return s && *s ? atoi(s) : def;
+}
+
 static unsigned grid_for(uint64_t threads) {
     uint64_t wgs = (threads + 255) / 256;
     const uint64_t cap = 256ull * 64ull;  // 64 workgroups per CU, grid-stride beyond
@@ -769,18 +915,28 @@ hipError_t launch_append(const Geometry &g, void *pool, uint64_t pool_blocks, co
                          hipStream_t s) {
     const Geo geo = to_geo(g);
     const uint64_t per_row = 2 * (g.kv_out / 8);
+    const int U = tune("QVKV_APPEND_U", 4);
+    const bool NT = tune("QVKV_APPEND_NT", 0) != 0;
     // keep the flat index inside 32 bits: launch in row batches
     const uint32_t max_rows = (uint32_t)((0x7fffffffull / per_row));
     for (uint32_t r0 = 0; r0 < n; r0 += max_rows) {
         const uint32_t nr = n - r0 < max_rows ? n - r0 : max_rows;
-        const unsigned grid = grid_for((uint64_t)nr * per_row);
+        const unsigned grid = grid_for(((uint64_t)nr * per_row + U - 1) / U);
         const float *kk = k + (uint64_t)r0 * g.kv_out, *vv = v + (uint64_t)r0 * g.kv_out;
-        if (g.dtype == QVKV_F16)
-            hipLaunchKernelGGL(k_append<QVKV_F16>, dim3(grid), dim3(256), 0, s, (uint8_t *)pool,
-                               pool_blocks, kk, vv, slots + r0, nr, geo, err);
-        else
-            hipLaunchKernelGGL(k_append<QVKV_Q8_0>, dim3(grid), dim3(256), 0, s, (uint8_t *)pool,
-                               pool_blocks, kk, vv, slots + r0, nr, geo, err);
+#define QV_APPEND(DT, UU, NN)                                                                  \
+    hipLaunchKernelGGL((k_append<DT, UU, NN>), dim3(grid), dim3(256), 0, s, (uint8_t *)pool,   \
+                       pool_blocks, kk, vv, slots + r0, nr, geo, err)
+#define QV_APPEND_U(DT)                                                                        \
+    if (U <= 1) { if (NT) QV_APPEND(DT, 1, true); else QV_APPEND(DT, 1, false); }              \
+    else if (U == 2) { if (NT) QV_APPEND(DT, 2, true); else QV_APPEND(DT, 2, false); }         \
+    else { if (NT) QV_APPEND(DT, 4, true); else QV_APPEND(DT, 4, false); }
+        if (g.dtype == QVKV_F16) {
+            QV_APPEND_U(QVKV_F16)
+        } else {
+            QV_APPEND_U(QVKV_Q8_0)
+        }
+#undef QV_APPEND_U
+#undef QV_APPEND
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -813,11 +969,16 @@ hipError_t launch_block_copy(const Geometry &g, void *pool, uint64_t pool_blocks
                              const uint32_t *src, const uint32_t *dst, uint32_t n, int *err,
                              hipStream_t s) {
     if (n == 0) return hipSuccess;
-    const uint32_t per = (uint32_t)((g.block_bytes / 16 + 1023) / 1024);
+    const int U = tune("QVKV_COPY_U", 4) >= 8 ? 8 : 4;
+    const uint32_t per = (uint32_t)((g.block_bytes / 16 + 256 * U - 1) / (256 * U));
     const uint64_t grid = (uint64_t)per * n;
     if (grid > 0x7fffffffull) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_block_copy, dim3((unsigned)grid), dim3(256), 0, s, (uint8_t *)pool,
-                       pool_blocks, src, dst, n, per, g.block_bytes, err);
+    if (U == 8)
+        hipLaunchKernelGGL(k_block_copy<8>, dim3((unsigned)grid), dim3(256), 0, s, (uint8_t *)pool,
+                           pool_blocks, src, dst, n, per, g.block_bytes, err);
+    else
+        hipLaunchKernelGGL(k_block_copy<4>, dim3((unsigned)grid), dim3(256), 0, s, (uint8_t *)pool,
+                           pool_blocks, src, dst, n, per, g.block_bytes, err);
     return hipGetLastError();
 }
 
@@ -840,7 +1001,8 @@ int plan_attention(const Geometry &g, uint32_t n_items, uint32_t heads, uint32_t
     }
     const uint64_t units = (uint64_t)n_items * g.G * p->hc;
     const uint64_t max_tiles = ((uint64_t)max_pos + 1 + 15) / 16;
-    const uint64_t target = 2048;  // workgroups: 8 per CU keeps all 256 CUs busy
+    // workgroups to aim for: 8 per CU keeps all 256 CUs busy
+    const uint64_t target = (uint64_t)tune("QVKV_ATTN_TARGET", 2048);
     uint64_t nch = units >= target ? 1 : (target + units - 1) / units;
     const uint64_t cap = (max_tiles + 3) / 4;  // at least one tile per wave
     if (nch > cap) nch = cap;
@@ -875,14 +1037,17 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
     }
     const uint64_t grid = (uint64_t)n_items * g.G * p.hc * p.n_chunks;
     float *wsf = (float *)ws;
-#define QV_ATTN(DD, QQ)                                                                         \
-    hipLaunchKernelGGL((k_attn_mfma<DD, QQ>), dim3((unsigned)grid), dim3(256), 0, s, pp,        \
+#define QV_ATTN(DD, QQ, NN, PP)                                                                 \
+    hipLaunchKernelGGL((k_attn_mfma<DD, QQ, NN>), dim3((unsigned)grid), dim3(256), 0, s, pp,    \
                        pool_blocks, q, blocks, n_table, table_at, pos, n_items, heads, max_pos, \
                        out, wsf, p.hc, p.n_chunks, p.tpc, geo, err)
     const bool q8 = g.dtype == QVKV_Q8_0;
-    if (g.D == 64) { if (q8) QV_ATTN(64, true); else QV_ATTN(64, false); }
-    else if (g.D == 128) { if (q8) QV_ATTN(128, true); else QV_ATTN(128, false); }
-    else { if (q8) QV_ATTN(256, true); else QV_ATTN(256, false); }
+    // K/V tiles are streamed with non-temporal loads (read once); no software prefetch:
+    // at cfg5 both measured slower or equal (occupancy 5 -> 2 waves/SIMD with a tile
+    // held in flight).
+    if (g.D == 64) { if (q8) QV_ATTN(64, true, true, false); else QV_ATTN(64, false, true, false); }
+    else if (g.D == 128) { if (q8) QV_ATTN(128, true, true, false); else QV_ATTN(128, false, true, false); }
+    else { if (q8) QV_ATTN(256, true, true, false); else QV_ATTN(256, false, true, false); }
 #undef QV_ATTN
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.n_chunks == 1) return e;
