@@ -1,18 +1,20 @@
 """Benchmark of the paged KV-cache hot path on one MI355X.
 
-Workload ("cfg5"): Qwen3-30B-A3B-like KV, 48 layers, 4 KV heads,
-head_dim 128, 32 query heads (GQA 8:1), f16 storage, block 16, 128 sequences at 8192
-context (~103 GB of KV resident).  Block tables come from the library's pool manager
-after seeded alloc/free churn (fragmented).  The pool is filled by bulk prefill-appends
-of 512 tokens x 128 sequences x 48 layers per call (timed: the append leg).
+Default workload ("cfg5"): Qwen3-30B-A3B-like KV, 48 layers,
+4 KV heads, head_dim 128, 32 query heads (GQA 8:1), f16 storage, block 16, 128 sequences
+at 8192 context (~103 GB of KV resident).  Block tables come from the library's pool
+manager after seeded alloc/free churn (fragmented).  The pool is filled by bulk
+prefill-appends of 512 tokens x all sequences x all layers per call (the timed append leg).
 
-One step = one decode step: one append per sequence on every layer (position 8191) plus
-paged decode attention of 32 heads over positions 0..8191 on every layer; the value is
-tokens/s = 128 / step time.  Inputs are resident in HBM before the timed region.
-
-Also reported: block-table gather (f16 -> f16) and batched block copy GB/s, and the CPU
+One step = one decode step: one append per sequence on every layer (its newest position)
+plus paged decode attention of every query head over the whole context on every layer;
+value = tokens/s = sequences / step time.  Inputs are resident in HBM before the timed
+region.  Also reported: block-table gather and batched block copy GB/s, and the CPU
 baseline: the oracle's restatement of the reference CPU path (gather + `attend`, OpenMP
 over heads) on a sample of (sequence, layer) items, scaled to a whole step.
+
+--config cfg2 / cfg3 run the Llama-3-8B-like batched decode (contexts U[256, 4096]) and the
+q8_0 configuration (64 x 2048, 1 % x8 outliers) the same way.
 """
 import argparse
 import json
@@ -26,20 +28,33 @@ if ROOT not in sys.path:
 
 PEAK_HBM_GBS = 8000.0
 
+CONFIGS = {
+    # layers, kv heads, head dim, q heads, sequences, context (int or (lo, hi)), dtype, outliers
+    "cfg5": dict(layers=48, kv_heads=4, head_dim=128, q_heads=32, seqs=128, ctx=8192,
+                 dtype="f16", outliers=0.0,
+                 name="cfg5 (Qwen3-30B-A3B-like KV, 128 seqs x 8192)"),
+    "cfg2": dict(layers=32, kv_heads=8, head_dim=128, q_heads=32, seqs=32, ctx=(256, 4096),
+                 dtype="f16", outliers=0.0,
+                 name="cfg2 (Llama-3-8B-like KV, 32 seqs x U[256,4096])"),
+    "cfg3": dict(layers=32, kv_heads=8, head_dim=128, q_heads=32, seqs=64, ctx=2048,
+                 dtype="q8_0", outliers=0.01,
+                 name="cfg3 (q8_0 KV, 64 seqs x 2048, 1% x8 outliers)"),
+}
+
 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--seqs", type=int, default=128)
-    ap.add_argument("--ctx", type=int, default=8192)
-    ap.add_argument("--layers", type=int, default=48)
+    ap.add_argument("--config", default="cfg5", choices=sorted(CONFIGS))
+    ap.add_argument("--seqs", type=int, default=None, help="override the config's sequences")
+    ap.add_argument("--ctx", type=int, default=None, help="override the config's context")
+    ap.add_argument("--layers", type=int, default=None, help="override the config's layers")
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--legs", default="append,decode,gather,copy")
-    ap.add_argument("--dtype", default="f16", choices=["f16", "q8_0"])
     return ap.parse_args()
 
 
@@ -57,44 +72,41 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs the GPU"
     torch.cuda.init()
+    cfg = dict(CONFIGS[args.config])
+    for key in ("seqs", "ctx", "layers"):
+        if getattr(args, key) is not None:
+            cfg[key] = getattr(args, key)
     dev = HipDevice(0)
     legs = set(args.legs.split(","))
-    S, CTX, NL = args.seqs, args.ctx, args.layers
-    G, D, H, B = 4, 128, 32, 16
-    L = KvLayout(args.dtype, G, D, B)
+    S, NL = cfg["seqs"], cfg["layers"]
+    G, D, H, B = cfg["kv_heads"], cfg["head_dim"], cfg["q_heads"], 16
+    dtype = cfg["dtype"]
+    L = KvLayout(dtype, G, D, B)
     kv_out = G * D
-    bpl = (CTX + B - 1) // B  # blocks per (sequence, layer)
-    real_blocks = S * NL * bpl
+    bytes_per_value = 2 if dtype == "f16" else 34 / 32
+    r = np.random.default_rng(args.seed)
+    if isinstance(cfg["ctx"], tuple):
+        ctx = r.integers(cfg["ctx"][0], cfg["ctx"][1] + 1, S)
+    else:
+        ctx = np.full(S, cfg["ctx"])
+    real_blocks = int(sum((int(c) + B - 1) // B for c in ctx)) * NL
     n_blocks = int(real_blocks * 1.25) + 1024
     log = lambda *a: print(*a, file=sys.stderr, flush=True)  # noqa: E731
-    log(f"[bench] {dev.describe()}; pool {n_blocks} blocks x {L.block_bytes} B = "
+    log(f"[bench] {dev.describe()}; {cfg['name']}; pool {n_blocks} blocks x {L.block_bytes} B = "
         f"{n_blocks * L.block_bytes / 1e9:.1f} GB")
     pool = KvPool(dev, L, n_blocks, NL)
-    pool_ptr = pool.ptr
+    mem = pool.memory
 
     def cu32(a):
         return torch.from_numpy(np.ascontiguousarray(a, np.uint32).view(np.int32)).cuda()
 
-    class Raw:  # a device pointer in the shape the bindings take
-        def __init__(self, p):
-            self.p = p
-
-        def data_ptr(self):
-            return self.p
-
-    praw = Raw(pool_ptr)
-
     # ---- seeded churn: scatter the free list before the real sequences allocate
-    r = np.random.default_rng(args.seed)
     t0 = time.time()
-    dummies = []
-    budget = int(n_blocks * 0.2)
-    used = 0
-    while used < budget:
+    dummies, used = [], 0
+    while used < int(n_blocks * 0.2):
         s = pool.create()
-        layer = int(r.integers(NL))
         n = int(r.integers(16, 16 * 64))
-        pool.plan_append([s], [n], layer)
+        pool.plan_append([s], [n], int(r.integers(NL)))
         used += (n + B - 1) // B
         dummies.append(s)
     order = r.permutation(len(dummies))
@@ -104,37 +116,39 @@ def main():
     seqs = [pool.create() for _ in range(S)]
     log(f"[bench] churn: {len(dummies)} sequences, half released ({time.time() - t0:.1f}s)")
 
-    # ---- fill: bulk prefill-append of CHUNK tokens x S sequences x NL layers per call
+    # ---- fill: bulk prefill-append of up to CHUNK tokens per sequence, all layers per call
     CHUNK = 512
     gen = torch.Generator(device="cuda").manual_seed(args.seed)
-    append_ms, append_bytes = [], []
-    filled = 0
-    fill_to = CTX - 1  # the decode step writes position CTX-1
     stream = torch.cuda.current_stream()
-    while filled < fill_to:
-        c = min(CHUNK, fill_to - filled)
-        slots = np.concatenate([pool.plan_append(seqs, [c] * S, l) for l in range(NL)])
+    append_ms, append_bytes = [], []
+    fill_to = ctx - 1  # the decode step writes each sequence's position ctx-1
+    filled = np.zeros(S, np.int64)
+    while (filled < fill_to).any():
+        counts = np.minimum(CHUNK, fill_to - filled).astype(np.uint32)
+        slots = np.concatenate([pool.plan_append(seqs, counts, l) for l in range(NL)])
         n_rows = slots.size
         sl = cu32(slots)
         k = torch.randn((n_rows, kv_out), generator=gen, device="cuda", dtype=torch.float32)
         v = torch.randn((n_rows, kv_out), generator=gen, device="cuda", dtype=torch.float32)
+        if cfg["outliers"]:
+            for x in (k, v):
+                x[torch.rand(x.shape, generator=gen, device="cuda") < cfg["outliers"]] *= 8.0
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
-        dev.append(L, praw, n_blocks, k, v, sl)
+        dev.append(L, mem, n_blocks, k, v, sl)
         e1.record(stream)
         torch.cuda.synchronize()
         dev.check()
-        if c == CHUNK:
+        if (counts == CHUNK).all():
             append_ms.append(e0.elapsed_time(e1))
-            append_bytes.append(n_rows * kv_out * (4 * 2 + 2 * (2 if args.dtype == "f16" else 34 / 32))
-                                + n_rows * 4)
-        filled += c
+            append_bytes.append(n_rows * kv_out * (4 * 2 + 2 * bytes_per_value) + n_rows * 4)
+        filled += counts
         del k, v, sl
     for s in keep:
         pool.release(s)
-    log(f"[bench] filled {fill_to} positions x {S} seqs x {NL} layers ({time.time() - t0:.1f}s)")
+    log(f"[bench] filled {int(fill_to.sum())} positions x {NL} layers ({time.time() - t0:.1f}s)")
 
-    # ---- the decode step's inputs: one new token per (sequence, layer) at position CTX-1
+    # ---- the decode step's inputs: one new token per (sequence, layer) at position ctx-1
     slots = np.concatenate([pool.plan_append(seqs, [1] * S, l) for l in range(NL)])
     tabs = [pool.tables(seqs, l) for l in range(NL)]
     blocks = np.concatenate([t[0] for t in tabs])
@@ -142,7 +156,7 @@ def main():
     table_at = np.concatenate([t[1] + o for t, o in zip(tabs, offs)]).astype(np.uint32)
     pos = np.concatenate([t[2] for t in tabs]).astype(np.uint32)
     items = pos.size
-    assert items == S * NL and int(pos.max()) == CTX - 1 and int(pos.min()) == CTX - 1
+    assert items == S * NL and np.array_equal(pos, np.tile(ctx - 1, NL))
     frag = float(np.mean(np.diff(blocks.astype(np.int64)) != 1))
     d_slots, d_blocks, d_tat, d_pos = cu32(slots), cu32(blocks), cu32(table_at), cu32(pos)
     kn = torch.randn((items, kv_out), generator=gen, device="cuda")
@@ -150,16 +164,16 @@ def main():
     q = torch.randn((items, H, D), generator=gen, device="cuda")
     out = torch.empty((items, H, D), device="cuda")
     max_pos = int(pos.max())
-    kv_bytes_step = float(np.sum(pos.astype(np.float64) + 1)) * kv_out * 2 * (
-        2 if args.dtype == "f16" else 34 / 32)
-    attn_bytes = (kv_bytes_step + q.numel() * 4 * 2 + blocks.size * 4 + items * 8)
-    flops = 4.0 * H * D * float(np.sum(pos.astype(np.float64) + 1))
+    positions = float(np.sum(pos.astype(np.float64) + 1))
+    kv_bytes_step = positions * kv_out * 2 * bytes_per_value
+    attn_bytes = kv_bytes_step + q.numel() * 4 * 2 + blocks.size * 4 + items * 8
+    flops = 4.0 * H * D * positions
 
     def step(ev=None):
-        dev.append(L, praw, n_blocks, kn, vn, d_slots)
+        dev.append(L, mem, n_blocks, kn, vn, d_slots)
         if ev is not None:
             ev[0].record(stream)
-        dev.attention(L, praw, n_blocks, q, d_blocks, d_tat, d_pos, H, max_pos, out)
+        dev.attention(L, mem, n_blocks, q, d_blocks, d_tat, d_pos, H, max_pos, out)
         if ev is not None:
             ev[1].record(stream)
 
@@ -181,60 +195,59 @@ def main():
         attn_ms = float(np.mean([a.elapsed_time(b) for a, b in evs]))
         ms_step = wall * 1e3 / args.steps
         result.update(ms_per_step=ms_step, tokens_per_s=S / (ms_step / 1e3), attn_ms=attn_ms,
-                      attn_gbs=attn_bytes / (attn_ms / 1e3) / 1e9, attn_tflops=flops / (attn_ms / 1e3) / 1e12)
+                      attn_gbs=attn_bytes / (attn_ms / 1e3) / 1e9,
+                      attn_tflops=flops / (attn_ms / 1e3) / 1e12)
         log(f"[bench] decode step {ms_step:.3f} ms ({S / (ms_step / 1e3):.0f} tok/s); attention "
             f"{attn_ms:.3f} ms = {result['attn_gbs']:.0f} GB/s")
 
     if "gather" in legs:
-        # Gather NG layers' items (all positions) into contiguous f16 [G][n][d] per item.
+        # Gather up to 8 layers' items (all positions) into contiguous [G][n][d] per item.
         NGL = min(8, NL)
         gi = S * NGL
         lens = (pos[:gi] + 1).astype(np.uint32)
         out_at = np.concatenate([[0], np.cumsum(lens[:-1], dtype=np.uint64)]).astype(np.uint64)
         tot = int(lens.sum())
-        gdt = torch.float16 if args.dtype == "f16" else torch.float32
+        gdt = torch.float16 if dtype == "f16" else torch.float32
         ok = torch.empty(tot * kv_out, dtype=gdt, device="cuda")
         ov = torch.empty_like(ok)
         nt = int(table_at[gi]) if gi < items else blocks.size
-        d_gb = cu32(blocks[:nt])
-        d_gl = cu32(lens)
+        d_gb, d_gl = cu32(blocks[:nt]), cu32(lens)
         d_go = torch.from_numpy(out_at.view(np.int64)).cuda()
-        od = "f16" if args.dtype == "f16" else "f32"
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        od = "f16" if dtype == "f16" else "f32"
         for _ in range(2):
-            dev.gather(L, praw, n_blocks, d_gb, d_tat[:gi], d_gl, d_go, int(lens.max()), ok, ov, od)
+            dev.gather(L, mem, n_blocks, d_gb, d_tat[:gi], d_gl, d_go, int(lens.max()), ok, ov, od)
         torch.cuda.synchronize()
         reps = 5
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         for _ in range(reps):
-            dev.gather(L, praw, n_blocks, d_gb, d_tat[:gi], d_gl, d_go, int(lens.max()), ok, ov, od)
+            dev.gather(L, mem, n_blocks, d_gb, d_tat[:gi], d_gl, d_go, int(lens.max()), ok, ov, od)
         e1.record(stream)
         torch.cuda.synchronize()
         dev.check()
         g_ms = e0.elapsed_time(e1) / reps
-        g_bytes = tot * kv_out * 2 * (2 if args.dtype == "f16" else 34 / 32) + \
-            2 * ok.numel() * ok.element_size() + nt * 4 + gi * 16
+        g_bytes = (tot * kv_out * 2 * bytes_per_value + 2 * ok.numel() * ok.element_size()
+                   + nt * 4 + gi * 16)
         result.update(gather_ms=g_ms, gather_gbs=g_bytes / (g_ms / 1e3) / 1e9)
-        log(f"[bench] gather {NGL} layers: {g_ms:.3f} ms = {result['gather_gbs']:.0f} GB/s")
+        log(f"[bench] gather {NGL} layers ({od} out): {g_ms:.3f} ms = {result['gather_gbs']:.0f} GB/s")
         del ok, ov
 
     if "copy" in legs:
-        # Batched block copy: 65536 live blocks into free blocks (COW / compaction moves).
-        st = pool.stats()
-        ncp = min(65536, st["free"] - 16)
+        # Batched block copy: live blocks into free blocks (the COW / compaction move).
+        ncp = min(65536, pool.stats()["free"] - 16)
         src = blocks[:ncp]
         live = np.zeros(n_blocks, bool)
         live[blocks] = True
         dst = np.nonzero(~live)[0][:ncp].astype(np.uint32)
         d_src, d_dst = cu32(src), cu32(dst)
         for _ in range(2):
-            dev.block_copy(L, praw, n_blocks, d_src, d_dst)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            dev.block_copy(L, mem, n_blocks, d_src, d_dst)
         reps = 5
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         e0.record(stream)
         for _ in range(reps):
-            dev.block_copy(L, praw, n_blocks, d_src, d_dst)
+            dev.block_copy(L, mem, n_blocks, d_src, d_dst)
         e1.record(stream)
         torch.cuda.synchronize()
         dev.check()
@@ -251,11 +264,15 @@ def main():
 
     cpu = None
     if not args.no_cpu and "decode" in legs:
-        cpu = cpu_baseline(args, G, D, H, B, CTX, S * NL, S, result["ms_per_step"], log)
+        cpu = cpu_baseline(args, dtype, G, D, H, B, int(ctx.max()), positions, S,
+                           result["ms_per_step"], log)
 
     stats = pool.stats()
+    ctx_desc = (f"{S} seqs x {int(ctx[0])} ctx" if (ctx == ctx[0]).all()
+                else f"{S} seqs x ctx U[{cfg['ctx'][0]},{cfg['ctx'][1]}] (sum {int(ctx.sum())})")
     line = {
-        "metric": "paged decode-attn tokens/s at 128x8k (Qwen3-30B-A3B-like KV); KV append/gather HBM GB/s",
+        "metric": "paged decode-attn tokens/s at 128x8k (Qwen3-30B-A3B-like KV); "
+                  "KV append/gather HBM GB/s",
         "value": round(result.get("tokens_per_s", 0.0), 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -265,14 +282,15 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": args.dtype,
+        "dtype": dtype,
         "data": "synthetic N(0,1) K/V/Q from a seeded generator; fragmented block tables",
         "config": {
-            "workload": f"cfg5: {NL} layers, {G} KV heads, d {D}, {H} q heads (GQA {H // G}:1), "
-                        f"{args.dtype} KV, block {B}, {S} seqs x {CTX} ctx; step = 1 append/seq/layer "
-                        "+ paged decode attention over all layers",
-            "seqs": S, "ctx": CTX, "layers": NL, "kv_heads": G, "head_dim": D, "q_heads": H,
-            "block": B, "pool_blocks": n_blocks, "pool_gb": round(n_blocks * L.block_bytes / 1e9, 1),
+            "workload": f"{cfg['name']}: {NL} layers, {G} KV heads, d {D}, {H} q heads "
+                        f"(GQA {H // G}:1), {dtype} KV, block {B}, {ctx_desc}; step = 1 append/"
+                        "seq/layer + paged decode attention over all layers",
+            "seqs": S, "layers": NL, "kv_heads": G, "head_dim": D, "q_heads": H, "block": B,
+            "context_positions_per_layer": int(ctx.sum()), "pool_blocks": n_blocks,
+            "pool_gb": round(n_blocks * L.block_bytes / 1e9, 1),
             "table_discontinuity": round(frag, 3), "seed": args.seed,
         },
         "roofline": None,
@@ -287,8 +305,8 @@ def main():
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(result["attn_gbs"] / PEAK_HBM_GBS, 4),
-            "traffic": None,
-            "kernel": "k_attn_mfma<128,false>",
+            "traffic": traffic_from_profile(args.config, attn_bytes),
+            "kernel": f"k_attn_mfma<{D},{'q8_0' if dtype == 'q8_0' else 'f16'}>",
             "algorithmic_bytes_per_launch": attn_bytes,
             "avg_launch_ms": round(result["attn_ms"], 4),
         }
@@ -303,10 +321,24 @@ def main():
     dev.close()
 
 
-def cpu_baseline(args, G, D, H, B, CTX, items_per_step, S, gpu_ms, log):
+def traffic_from_profile(config, algorithmic):
+    """HBM bytes per attention launch from the committed rocprofv3 --pmc summary of this
+    workload (FETCH_SIZE and WRITE_SIZE scaled by the copy-kernel calibration), when one
+    exists for the same algorithmic bytes; else None."""
+    path = os.path.join(ROOT, "profiles", f"attention_{config}_pmc.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        p = json.load(f)
+    if abs(p.get("algorithmic_bytes", 0) - algorithmic) > 1e-6 * algorithmic:
+        return None
+    return p.get("traffic_bytes")
+
+
+def cpu_baseline(args, dtype, G, D, H, B, CTX, positions_per_step, S, gpu_ms, log):
     """The reference CPU path restated (oracle): gather through the block table + `attend`
-    per (item, head), OpenMP over heads, on a sample of (sequence, layer) items at the full
-    context; scaled to one whole step (items_per_step items)."""
+    per (item, head), OpenMP over heads, on a sample of (sequence, layer) items at CTX
+    positions; scaled by positions to one whole step."""
     import numpy as np
 
     import oracle
@@ -316,9 +348,8 @@ def cpu_baseline(args, G, D, H, B, CTX, items_per_step, S, gpu_ms, log):
     r = np.random.default_rng(args.seed + 1)
     bpl = (CTX + B - 1) // B
     nb = n_items * bpl
-    sim = oracle.SimPool(nb, G, D, B, oracle.F16 if args.dtype == "f16" else oracle.Q8_0)
-    ids = r.permutation(nb).astype(np.uint32)
-    blocks = ids
+    sim = oracle.SimPool(nb, G, D, B, oracle.F16 if dtype == "f16" else oracle.Q8_0)
+    blocks = r.permutation(nb).astype(np.uint32)
     table_at = (np.arange(n_items) * bpl).astype(np.uint32)
     pos = np.full(n_items, CTX - 1, np.uint32)
     for t in range(n_items):
@@ -334,15 +365,17 @@ def cpu_baseline(args, G, D, H, B, CTX, items_per_step, S, gpu_ms, log):
         done += n_items
         if time.perf_counter() - t0 >= args.cpu_seconds:
             break
-    per_item = (time.perf_counter() - t0) / done
-    step_s = per_item * items_per_step
+    per_position = (time.perf_counter() - t0) / (done * CTX)
+    step_s = per_position * positions_per_step
     tok_s = S / step_s
-    log(f"[bench] CPU baseline: {per_item * 1e3:.1f} ms per (seq, layer) item on {threads} threads "
-        f"-> {step_s:.1f} s per step, {tok_s:.2f} tok/s (GPU/CPU {step_s * 1e3 / gpu_ms:.0f}x)")
-    return {"value": round(tok_s, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+    log(f"[bench] CPU baseline: {per_position * CTX * 1e3:.1f} ms per {CTX}-position item on "
+        f"{threads} threads -> {step_s:.1f} s per step, {tok_s:.3f} tok/s "
+        f"(GPU/CPU {step_s * 1e3 / gpu_ms:.0f}x)")
+    return {"value": round(tok_s, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"{done} (sequence, layer) items of gather + attend over {CTX} positions "
-                      f"({n_items} distinct, {H} heads each), scaled x{items_per_step}/item to one "
-                      "step; oracle restatement of SimDevice::attention + math::attend"}
+                      f"({n_items} distinct, {H} heads each), scaled by positions to one step "
+                      f"({int(positions_per_step)} positions); oracle restatement of "
+                      "SimDevice::attention + math::attend"}
 
 
 if __name__ == "__main__":

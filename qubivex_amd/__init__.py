@@ -7,4 +7,4 @@ eviction, compaction).  This package is its Python binding.
 """
 from ._lib import (ComputeError, DeviceError, OutOfDeviceMemory, ShapeError,  # noqa: F401
                    UnsupportedError)
-from .kv import DeviceBuffer, HipDevice, KvLayout, KvPool, PrefixCache  # noqa: F401
+from .kv import DeviceBuffer, DevicePtr, HipDevice, KvLayout, KvPool, PrefixCache  # noqa: F401

@@ -46,8 +46,18 @@ class KvLayout:
         return out.value
 
 
+class DevicePtr:
+    """A raw device address in the shape the bindings take (what `data_ptr()` returns)."""
+
+    def __init__(self, address: int):
+        self.address = int(address)
+
+    def data_ptr(self):
+        return self.address
+
+
 def _ptr(x):
-    """Device pointer of a torch tensor (or None)."""
+    """Device pointer of a torch tensor or DevicePtr (or None)."""
     if x is None:
         return None
     return ctypes.c_void_p(x.data_ptr())
@@ -323,6 +333,11 @@ class KvPool:
     @property
     def ptr(self):
         return lib.qvkv_pool_ptr(self.handle)
+
+    @property
+    def memory(self):
+        """The pool's device memory, for the HipDevice kernel entry points."""
+        return DevicePtr(self.ptr)
 
     def stats(self):
         s = _lib.PoolStats()
