@@ -407,6 +407,12 @@ __device__ __forceinline__ void load_bytes(const uint8_t *p, uint32_t *w) {
     load_bytes<NB, false>(p, w);
 }
 
+// f16 number idx of a packed word array, as f32 (idx is a compile-time constant).
+__device__ __forceinline__ float half_at(const uint32_t *w, int idx) {
+    const uint32_t x = w[idx >> 1];
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)((idx & 1) ? (x >> 16) : (x & 0xffffu)));
+}
+
 // One 16-position tile's operands for one lane, as loaded from the pool.
 template <int D, bool Q8>
 struct Tile {
@@ -470,7 +476,6 @@ __device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<
     const uint32_t p0 = t.p0;
     // ---- scores S^T[position][column] = K . Q^T
     f4 s = f4{0.f, 0.f, 0.f, 0.f};
-    float vsc[4][NG];
     uint32_t vw[4][Tile<D, Q8>::VW];
 #pragma unroll
     for (int i = 0; i < 4; i++)
@@ -483,19 +488,13 @@ __device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<
             s = __builtin_amdgcn_mfma_f32_16x16x16f16(h4_of(t.k[4 * i + 2], t.k[4 * i + 3]), qf[2 * i + 1], s, 0, 0, 0);
         }
     } else {
-        const _Float16 *ksh = (const _Float16 *)t.ks;
-        const _Float16 *vsh = (const _Float16 *)t.vs;
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int gi = 0; gi < NG; gi++) vsc[i][gi] = (float)vsh[i * NG + gi];
 #pragma unroll
         for (int gi = 0; gi < NG; gi++) {
             f4 sg = f4{0.f, 0.f, 0.f, 0.f};
             sg = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4(t.k[2 * gi]), qf[2 * gi], sg, 0, 0, 0);
             sg = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4(t.k[2 * gi + 1]), qf[2 * gi + 1], sg, 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < 4; i++) s[i] = fmaf(sg[i], (float)ksh[i * NG + gi], s[i]);
+            for (int i = 0; i < 4; i++) s[i] = fmaf(sg[i], half_at(t.ks, i * NG + gi), s[i]);
         }
     }
 
@@ -548,50 +547,77 @@ __device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<
             st.acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, h4_of(w0, w1), st.acc[j], 0, 0, 0);
         }
     } else {
-        if (partial) {
+        // V operand of MFMA j (group j/2): rows 4qg..4qg+3 at byte j of each row's run,
+        // int8 exactly as f16.  The rows' scales of group j/2 fold into the probabilities
+        // (P' = p * scale in f32, then f16 high part + residual: exact to ~2^-22), so the
+        // products the MFMA forms are exact.
+        uint32_t vsw[4][Tile<D, Q8>::VW];  // biased bytes x ^ 0x80
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-                if (p0 + 4 * qg + i >= n) {
+        for (int i = 0; i < 4; i++) {
+            const bool dead = partial && p0 + 4 * qg + i >= n;
 #pragma unroll
-                    for (int x = 0; x < Tile<D, Q8>::VW; x++) vw[i][x] = 0u;
-#pragma unroll
-                    for (int gi = 0; gi < NG; gi++) vsc[i][gi] = 0.0f;
-                }
+            for (int x = 0; x < Tile<D, Q8>::VW; x++) vsw[i][x] = dead ? 0x80808080u : vw[i][x] ^ 0x80808080u;
         }
+        const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+        const float lo_part = hi_col ? 0.0f : 1.0f;
 #pragma unroll
         for (int gi = 0; gi < NG; gi++) {
-            const h4 pa = h4{split_part(pr[0] * vsc[0][gi], hi_col),
-                             split_part(pr[1] * vsc[1][gi], hi_col),
-                             split_part(pr[2] * vsc[2][gi], hi_col),
-                             split_part(pr[3] * vsc[3][gi], hi_col)};
+            _Float16 pg[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float x = pr[i] * half_at(t.vs, i * NG + gi);
+                if (partial && p0 + 4 * qg + i >= n) x = 0.0f;  // a never-written slot's scale
+                const _Float16 u = (_Float16)x;
+                pg[i] = (_Float16)fmaf(-lo_part, (float)u, x);  // u, or the residual x - u
+            }
+            const h4 pa = h4{pg[0], pg[1], pg[2], pg[3]};
+            // bytes j and j+1 (j = 2gi) of rows 0,1 and of rows 2,3: one perm each
+            const int j = 2 * gi;
+            const uint32_t b = (uint32_t)(j & 3);
+            const uint32_t sel = ((4u + b + 1) << 24) | ((b + 1) << 16) | ((4u + b) << 8) | b;
+            const uint32_t t01 = __builtin_amdgcn_perm(vsw[1][j >> 2], vsw[0][j >> 2], sel);
+            const uint32_t t23 = __builtin_amdgcn_perm(vsw[3][j >> 2], vsw[2][j >> 2], sel);
 #pragma unroll
             for (int u = 0; u < 2; u++) {
-                const int j = 2 * gi + u;
-                const uint32_t bsel = (uint32_t)(j & 3);
-                const uint32_t sel = 0x0c000c00u | ((4u + bsel) << 16) | bsel;
-                const uint32_t a01 = __builtin_amdgcn_perm(vw[1][j >> 2] ^ 0x80808080u,
-                                                           vw[0][j >> 2] ^ 0x80808080u, sel) | 0x64006400u;
-                const uint32_t a23 = __builtin_amdgcn_perm(vw[3][j >> 2] ^ 0x80808080u,
-                                                           vw[2][j >> 2] ^ 0x80808080u, sel) | 0x64006400u;
-                const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
-                const h2 x01 = __builtin_bit_cast(h2, a01) - bias;
-                const h2 x23 = __builtin_bit_cast(h2, a23) - bias;
-                st.acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, h4{x01.x, x01.y, x23.x, x23.y},
-                                                                  st.acc[j], 0, 0, 0);
+                const uint32_t spread = u ? 0x04030402u : 0x04010400u;
+                const h2 x01 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, t01, spread)) - bias;
+                const h2 x23 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, t23, spread)) - bias;
+                st.acc[j + u] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, h4{x01.x, x01.y, x23.x, x23.y},
+                                                                      st.acc[j + u], 0, 0, 0);
             }
         }
     }
 }
 
+#define QV_ATTN_PARAMS                                                                          \
+    const uint8_t *__restrict__ pool, uint64_t pool_blocks, const float *__restrict__ q,        \
+        const uint32_t *__restrict__ blocks, uint64_t n_table,                                  \
+        const uint32_t *__restrict__ table_at, const uint32_t *__restrict__ pos,                \
+        uint32_t n_items, uint32_t H, uint32_t max_pos, float *__restrict__ out,                \
+        float *__restrict__ ws, uint32_t hc_n, uint32_t n_chunks, uint32_t tpc, Geo geo,        \
+        int *err
+#define QV_ATTN_ARGS                                                                            \
+    pool, pool_blocks, q, blocks, n_table, table_at, pos, n_items, H, max_pos, out, ws, hc_n,   \
+        n_chunks, tpc, geo, err
+
 template <int D, bool Q8, bool NT>
-__global__ __launch_bounds__(256) void k_attn_mfma(
-    const uint8_t *__restrict__ pool, uint64_t pool_blocks, const float *__restrict__ q,
-    const uint32_t *__restrict__ blocks, uint64_t n_table, const uint32_t *__restrict__ table_at,
-    const uint32_t *__restrict__ pos, uint32_t n_items, uint32_t H, uint32_t max_pos,
-    float *__restrict__ out, float *__restrict__ ws, uint32_t hc_n, uint32_t n_chunks,
-    uint32_t tpc, Geo geo, int *err) {
+__device__ __forceinline__ void attn_body(QV_ATTN_PARAMS);
+
+template <int D, bool Q8, bool NT>
+__global__ __launch_bounds__(256) void k_attn_mfma(QV_ATTN_PARAMS) {
+    attn_body<D, Q8, NT>(QV_ATTN_ARGS);
+}
+
+// The same kernel held to the registers of W waves per SIMD (512 / W per lane).
+template <int D, bool Q8, bool NT, int W>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W)))
+void k_attn_mfma_w(QV_ATTN_PARAMS) {
+    attn_body<D, Q8, NT>(QV_ATTN_ARGS);
+}
+
+template <int D, bool Q8, bool NT>
+__device__ __forceinline__ void attn_body(QV_ATTN_PARAMS) {
     constexpr int NJ = D / 16;  // MFMA steps over d
-    constexpr int NG = D / 32;  // 32-value groups per row
     __shared__ float sm[4][8], sl[4][8];
     __shared__ float so[4][8][D];
 
@@ -1037,17 +1063,32 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
     }
     const uint64_t grid = (uint64_t)n_items * g.G * p.hc * p.n_chunks;
     float *wsf = (float *)ws;
-#define QV_ATTN(DD, QQ, NN, PP)                                                                 \
-    hipLaunchKernelGGL((k_attn_mfma<DD, QQ, NN>), dim3((unsigned)grid), dim3(256), 0, s, pp,    \
+    // K/V tiles are streamed with non-temporal loads (read once).
+    // Occupancy: `mode` 0 is the compiler's register choice (3 waves/SIMD at d=128), 4
+    // holds the kernel to 4 waves per SIMD (125 VGPRs, no spill).  Measured (cfg5 f16,
+    // cfg3 q8_0): f16 is best at 0 (6.48 vs 5.90 TB/s), q8_0 at 4 (4.82 vs 4.14 TB/s):
+    // the q8_0 tile has about twice the VALU work per byte and more waves hide it.
+    // Software pipelining one tile ahead (2 waves/SIMD) and 5 waves/SIMD (spills) were
+    // slower for both.
+#define QV_ATTN(DD, QQ)                                                                         \
+    hipLaunchKernelGGL((k_attn_mfma<DD, QQ, true>), dim3((unsigned)grid), dim3(256), 0, s, pp,  \
                        pool_blocks, q, blocks, n_table, table_at, pos, n_items, heads, max_pos, \
                        out, wsf, p.hc, p.n_chunks, p.tpc, geo, err)
+#define QV_ATTN_W4(DD, QQ)                                                                      \
+    hipLaunchKernelGGL((k_attn_mfma_w<DD, QQ, true, 4>), dim3((unsigned)grid), dim3(256), 0, s, \
+                       pp, pool_blocks, q, blocks, n_table, table_at, pos, n_items, heads,      \
+                       max_pos, out, wsf, p.hc, p.n_chunks, p.tpc, geo, err)
     const bool q8 = g.dtype == QVKV_Q8_0;
-    // K/V tiles are streamed with non-temporal loads (read once); no software prefetch:
-    // at cfg5 both measured slower or equal (occupancy 5 -> 2 waves/SIMD with a tile
-    // held in flight).
-    if (g.D == 64) { if (q8) QV_ATTN(64, true, true, false); else QV_ATTN(64, false, true, false); }
-    else if (g.D == 128) { if (q8) QV_ATTN(128, true, true, false); else QV_ATTN(128, false, true, false); }
-    else { if (q8) QV_ATTN(256, true, true, false); else QV_ATTN(256, false, true, false); }
+    const bool w4 = tune(q8 ? "QVKV_ATTN_WAVES4_Q8" : "QVKV_ATTN_WAVES4_F16", q8 ? 1 : 0) != 0;
+    if (g.D == 64) {
+        if (q8) QV_ATTN(64, true); else QV_ATTN(64, false);
+    } else if (g.D == 128) {
+        if (q8) { if (w4) QV_ATTN_W4(128, true); else QV_ATTN(128, true); }
+        else { if (w4) QV_ATTN_W4(128, false); else QV_ATTN(128, false); }
+    } else {
+        if (q8) QV_ATTN(256, true); else QV_ATTN(256, false);
+    }
+#undef QV_ATTN_W4
 #undef QV_ATTN
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.n_chunks == 1) return e;
