@@ -467,9 +467,14 @@ struct SoftmaxState {
     f4 acc[D / 16];
 };
 
-template <int D, bool Q8>
+// PK ("packed", q8_0 with at most 4 query heads per KV head): MFMA columns c and c^4
+// carry the same head (c & 3), and in the P.V step lane c's row holds the scaled
+// probabilities of group 2m + sigma (sigma = (c >> 2) & 1), so one A operand serves two
+// 32-value groups and each lane scales for one group instead of two.
+template <int D, bool Q8, bool PK>
 __device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<D> &st,
-                                             const h4 *qf, uint32_t n, uint32_t qg, bool hi_col) {
+                                             const h4 *qf, uint32_t n, uint32_t qg, bool hi_col,
+                                             uint32_t sigma) {
     constexpr int NJ = D / 16;
     constexpr int NG = D / 32;
     if (!t.ok) return;
@@ -560,18 +565,20 @@ __device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<
         }
         const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
         const float lo_part = hi_col ? 0.0f : 1.0f;
-#pragma unroll
-        for (int gi = 0; gi < NG; gi++) {
+        // The A operand of scaled probabilities for group g (this lane's scale pick).
+        auto scaled = [&](float sc_of_row[4]) {
             _Float16 pg[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                float x = pr[i] * half_at(t.vs, i * NG + gi);
+                float x = pr[i] * sc_of_row[i];
                 if (partial && p0 + 4 * qg + i >= n) x = 0.0f;  // a never-written slot's scale
                 const _Float16 u = (_Float16)x;
                 pg[i] = (_Float16)fmaf(-lo_part, (float)u, x);  // u, or the residual x - u
             }
-            const h4 pa = h4{pg[0], pg[1], pg[2], pg[3]};
-            // bytes j and j+1 (j = 2gi) of rows 0,1 and of rows 2,3: one perm each
+            return h4{pg[0], pg[1], pg[2], pg[3]};
+        };
+        // P'.V for the two MFMAs of group gi (bytes 2gi, 2gi+1 of each row's run).
+        auto pv_group = [&](const h4 &pa, int gi) {
             const int j = 2 * gi;
             const uint32_t b = (uint32_t)(j & 3);
             const uint32_t sel = ((4u + b + 1) << 24) | ((b + 1) << 16) | ((4u + b) << 8) | b;
@@ -584,6 +591,30 @@ __device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<
                 const h2 x23 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, t23, spread)) - bias;
                 st.acc[j + u] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, h4{x01.x, x01.y, x23.x, x23.y},
                                                                       st.acc[j + u], 0, 0, 0);
+            }
+        };
+        if constexpr (PK) {
+            // Groups 2m and 2m+1 share one A operand: the scales of row i are the low and
+            // high f16 of word i*NG/2 + m (row-major [row][group] f16 scales).
+#pragma unroll
+            for (int m = 0; m < NG / 2; m++) {
+                float sc[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t w = t.vs[(i * NG) / 2 + m] >> (16u * sigma);
+                    sc[i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+                }
+                const h4 pa = scaled(sc);
+                pv_group(pa, 2 * m);
+                pv_group(pa, 2 * m + 1);
+            }
+        } else {
+#pragma unroll
+            for (int gi = 0; gi < NG; gi++) {
+                float sc[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) sc[i] = half_at(t.vs, i * NG + gi);
+                pv_group(scaled(sc), gi);
             }
         }
     }
@@ -600,22 +631,22 @@ __device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<
     pool, pool_blocks, q, blocks, n_table, table_at, pos, n_items, H, max_pos, out, ws, hc_n,   \
         n_chunks, tpc, geo, err
 
-template <int D, bool Q8, bool NT>
+template <int D, bool Q8, bool NT, bool PK>
 __device__ __forceinline__ void attn_body(QV_ATTN_PARAMS);
 
-template <int D, bool Q8, bool NT>
+template <int D, bool Q8, bool NT, bool PK>
 __global__ __launch_bounds__(256) void k_attn_mfma(QV_ATTN_PARAMS) {
-    attn_body<D, Q8, NT>(QV_ATTN_ARGS);
+    attn_body<D, Q8, NT, PK>(QV_ATTN_ARGS);
 }
 
 // The same kernel held to the registers of W waves per SIMD (512 / W per lane).
-template <int D, bool Q8, bool NT, int W>
+template <int D, bool Q8, bool NT, bool PK, int W>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W)))
 void k_attn_mfma_w(QV_ATTN_PARAMS) {
-    attn_body<D, Q8, NT>(QV_ATTN_ARGS);
+    attn_body<D, Q8, NT, PK>(QV_ATTN_ARGS);
 }
 
-template <int D, bool Q8, bool NT>
+template <int D, bool Q8, bool NT, bool PK>
 __device__ __forceinline__ void attn_body(QV_ATTN_PARAMS) {
     constexpr int NJ = D / 16;  // MFMA steps over d
     __shared__ float sm[4][8], sl[4][8];
@@ -649,8 +680,9 @@ __device__ __forceinline__ void attn_body(QV_ATTN_PARAMS) {
     const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
     const uint32_t c = lane & 15u, qg = lane >> 4;
     const bool hi_col = c < 8;
-    const uint32_t hidx = hc * 8 + (c & 7u);
+    const uint32_t hidx = PK ? (c & 3u) : hc * 8 + (c & 7u);  // query head within the group
     const bool hvalid = hidx < GS;
+    const uint32_t sigma = (c >> 2) & 1u;  // PK: which group of a pair this lane scales for
 
     // Query fragments (B operand of QK^T): column c, k-step j holds d = dset(qg, j).
     h4 qf[NJ];
@@ -675,7 +707,7 @@ __device__ __forceinline__ void attn_body(QV_ATTN_PARAMS) {
     for (uint32_t tt = t_begin + w; tt < t_end; tt += 4) {
         Tile<D, Q8> cur;
         load_tile<D, Q8, NT>(cur, tt, pool, pool_blocks, blocks, tab, g, c, qg, geo, err);
-        compute_tile<D, Q8>(cur, st, qf, n, qg, hi_col);
+        compute_tile<D, Q8, PK>(cur, st, qf, n, qg, hi_col, sigma);
     }
     float l = st.l;
     const float m = st.m;
@@ -696,8 +728,10 @@ __device__ __forceinline__ void attn_body(QV_ATTN_PARAMS) {
 #pragma unroll
         for (int j = 0; j < NJ; j++) {
             const int d = Q8 ? 32 * (j >> 1) + 2 * (int)c + (j & 1) : (int)c * (D / 16) + j;
+            // PK: rows 4*sigma + h hold head h for the groups with (group & 1) == sigma
+            if (PK && qg != (uint32_t)((j >> 1) & 1)) continue;
 #pragma unroll
-            for (int i = 0; i < 4; i++) so[w][4 * qg + i][d] = acc[j][i];
+            for (int i = 0; i < 4; i++) so[w][PK ? i : 4 * qg + i][d] = acc[j][i];
         }
     }
     __syncthreads();
@@ -1070,23 +1104,30 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
     // the q8_0 tile has about twice the VALU work per byte and more waves hide it.
     // Software pipelining one tile ahead (2 waves/SIMD) and 5 waves/SIMD (spills) were
     // slower for both.
-#define QV_ATTN(DD, QQ)                                                                         \
-    hipLaunchKernelGGL((k_attn_mfma<DD, QQ, true>), dim3((unsigned)grid), dim3(256), 0, s, pp,  \
-                       pool_blocks, q, blocks, n_table, table_at, pos, n_items, heads, max_pos, \
-                       out, wsf, p.hc, p.n_chunks, p.tpc, geo, err)
-#define QV_ATTN_W4(DD, QQ)                                                                      \
-    hipLaunchKernelGGL((k_attn_mfma_w<DD, QQ, true, 4>), dim3((unsigned)grid), dim3(256), 0, s, \
+#define QV_ATTN(DD, QQ, PK)                                                                     \
+    hipLaunchKernelGGL((k_attn_mfma<DD, QQ, true, PK>), dim3((unsigned)grid), dim3(256), 0, s,  \
                        pp, pool_blocks, q, blocks, n_table, table_at, pos, n_items, heads,      \
                        max_pos, out, wsf, p.hc, p.n_chunks, p.tpc, geo, err)
+#define QV_ATTN_W4(DD, QQ, PK)                                                                  \
+    hipLaunchKernelGGL((k_attn_mfma_w<DD, QQ, true, PK, 4>), dim3((unsigned)grid), dim3(256),   \
+                       0, s, pp, pool_blocks, q, blocks, n_table, table_at, pos, n_items,       \
+                       heads, max_pos, out, wsf, p.hc, p.n_chunks, p.tpc, geo, err)
     const bool q8 = g.dtype == QVKV_Q8_0;
     const bool w4 = tune(q8 ? "QVKV_ATTN_WAVES4_Q8" : "QVKV_ATTN_WAVES4_F16", q8 ? 1 : 0) != 0;
+    // q8_0 with <= 4 query heads per KV head: two groups' probabilities per A operand
+    const bool pk = q8 && heads / (uint32_t)g.G <= 4 && tune("QVKV_ATTN_PACK", 1) != 0;
     if (g.D == 64) {
-        if (q8) QV_ATTN(64, true); else QV_ATTN(64, false);
+        if (!q8) QV_ATTN(64, false, false);
+        else if (pk) QV_ATTN(64, true, true);
+        else QV_ATTN(64, true, false);
     } else if (g.D == 128) {
-        if (q8) { if (w4) QV_ATTN_W4(128, true); else QV_ATTN(128, true); }
-        else { if (w4) QV_ATTN_W4(128, false); else QV_ATTN(128, false); }
+        if (!q8) { if (w4) QV_ATTN_W4(128, false, false); else QV_ATTN(128, false, false); }
+        else if (pk) { if (w4) QV_ATTN_W4(128, true, true); else QV_ATTN(128, true, true); }
+        else { if (w4) QV_ATTN_W4(128, true, false); else QV_ATTN(128, true, false); }
     } else {
-        if (q8) QV_ATTN(256, true); else QV_ATTN(256, false);
+        if (!q8) QV_ATTN(256, false, false);
+        else if (pk) QV_ATTN(256, true, true);
+        else QV_ATTN(256, true, false);
     }
 #undef QV_ATTN_W4
 #undef QV_ATTN
