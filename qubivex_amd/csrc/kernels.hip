@@ -38,11 +38,14 @@ struct Geo {  // kernel-side copy of Geometry
     int dtype, G, D, B;
     uint32_t kv_out;
     uint64_t bb, k_off, ks_off, v_off, vs_off;
+    uint32_t xcd_map;  // attention: XCD-aware workgroup order
 };
+
+static int tune(const char *name, int def);
 
 static Geo to_geo(const Geometry &g) {
     return Geo{g.dtype, g.G, g.D, g.B, (uint32_t)g.kv_out, g.block_bytes,
-               g.k_off, g.ks_off, g.v_off, g.vs_off};
+               g.k_off, g.ks_off, g.v_off, g.vs_off, (uint32_t)tune("QVKV_ATTN_XCD", 1)};
 }
 
 __device__ __forceinline__ void flag(int *err, int bit) { atomicOr(err, bit); }
@@ -153,7 +156,10 @@ __global__ __launch_bounds__(256) void k_append(uint8_t *__restrict__ pool, uint
             o.y = pack_h2(x0.z, x0.w);
             o.z = pack_h2(x1.x, x1.y);
             o.w = pack_h2(x1.z, x1.w);
-            *(uint4 *)(base + (isv ? geo.v_off : geo.k_off) + (rowidx * D + i) * 2u) = o;
+            u4v* dst = (u4v *)(base + (isv ? geo.v_off : geo.k_off) + (rowidx * D + i) * 2u);
+            const u4v ov = {o.x, o.y, o.z, o.w};
+            if constexpr (NT) __builtin_nontemporal_store(ov, dst);
+            else *dst = ov;
         } else {
             float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
             float amax = 0.0f;
@@ -654,8 +660,17 @@ __device__ __forceinline__ void attn_body(QV_ATTN_PARAMS) {
 
     const uint32_t G = (uint32_t)geo.G, B = (uint32_t)geo.B;
     const uint32_t GS = H / G;
-    const uint32_t chunk = blockIdx.x % n_chunks;
-    const uint32_t unit = blockIdx.x / n_chunks;
+    // Workgroups are dealt to the 8 XCDs round-robin (id % 8).  With xcd_map set, logical
+    // unit ids are laid out so consecutive units (the KV heads and context chunks of one
+    // item, which read the same blocks) run on the same XCD and share its L2.
+    uint32_t bid = blockIdx.x;
+    if (geo.xcd_map) {
+        const uint32_t nb = gridDim.x, qn = nb / 8, rn = nb % 8;
+        const uint32_t x = bid % 8, i = bid / 8;
+        bid = x < rn ? x * (qn + 1) + i : rn * (qn + 1) + (x - rn) * qn + i;
+    }
+    const uint32_t chunk = bid % n_chunks;
+    const uint32_t unit = bid / n_chunks;
     const uint32_t hc = unit % hc_n;
     const uint32_t ug = unit / hc_n;
     const uint32_t g = ug % G;
@@ -976,7 +991,7 @@ hipError_t launch_append(const Geometry &g, void *pool, uint64_t pool_blocks, co
     const Geo geo = to_geo(g);
     const uint64_t per_row = 2 * (g.kv_out / 8);
     const int U = tune("QVKV_APPEND_U", 4);
-    const bool NT = tune("QVKV_APPEND_NT", 0) != 0;
+    const bool NT = tune("QVKV_APPEND_NT", 1) != 0;
     // keep the flat index inside 32 bits: launch in row batches
     const uint32_t max_rows = (uint32_t)((0x7fffffffull / per_row));
     for (uint32_t r0 = 0; r0 < n; r0 += max_rows) {
@@ -989,7 +1004,8 @@ hipError_t launch_append(const Geometry &g, void *pool, uint64_t pool_blocks, co
 #define QV_APPEND_U(DT)                                                                        \
     if (U <= 1) { if (NT) QV_APPEND(DT, 1, true); else QV_APPEND(DT, 1, false); }              \
     else if (U == 2) { if (NT) QV_APPEND(DT, 2, true); else QV_APPEND(DT, 2, false); }         \
-    else { if (NT) QV_APPEND(DT, 4, true); else QV_APPEND(DT, 4, false); }
+    else if (U == 4) { if (NT) QV_APPEND(DT, 4, true); else QV_APPEND(DT, 4, false); }         \
+    else { if (NT) QV_APPEND(DT, 8, true); else QV_APPEND(DT, 8, false); }
         if (g.dtype == QVKV_F16) {
             QV_APPEND_U(QVKV_F16)
         } else {
