@@ -238,6 +238,25 @@ int qvkv_seq_touch(qvkv_pool *pool, uint32_t seq);
  * (discrete.rs:988-994). */
 int qvkv_pool_plan_append(qvkv_pool *pool, const uint32_t *seqs, const uint32_t *count,
                           uint32_t n_seqs, uint32_t layer, uint32_t *slots_out);
+/* The attention plan of one decode pass on `layer` with a host-authoritative cache:
+ * attention_plan (crates/qubivex-runtime/src/discrete.rs:951-1009).  For each seqs[i] with
+ * the host's newest position pos[i] and cache epoch epochs[i]: a sequence whose epoch
+ * changed gives its blocks back and starts again; positions past the host's count are
+ * written again (synced = min(synced, pos)); the table grows to pos/B + 1 blocks from the
+ * free list (copy-on-write of a shared block a write lands in); the host rows
+ * [synced, pos) are listed to copy in (sync_to = their slots, sync_item / sync_pos = which
+ * sequence and position each is); new_slot[i] is position pos[i]'s slot.  Outputs are
+ * AttnPlan's blocks / table_at / pos (pos is the input).  The plan marks the layer synced
+ * to pos+1 (a failed pass is repaired by the min above on the next plan).  A dry free list
+ * returns QVKV_E_OOM and counts `full`; blocks taken before it stay with their sequence, as
+ * in the reference.  blocks_cap / sync_cap bound the outputs. */
+int qvkv_pool_plan_attention(qvkv_pool *pool, const uint32_t *seqs, const uint32_t *pos,
+                             const uint64_t *epochs, uint32_t n_seqs, uint32_t layer,
+                             uint32_t *blocks_out, uint64_t blocks_cap, uint64_t *n_table_out,
+                             uint32_t *table_at_out, uint32_t *new_slot_out,
+                             uint32_t *sync_to_out, uint32_t *sync_item_out,
+                             uint32_t *sync_pos_out, uint64_t sync_cap, uint64_t *n_sync_out);
+
 /* Flattened block tables of seqs[i] on `layer` (AttnPlan.blocks/table_at/pos,
  * discrete.rs:995-997).  blocks_cap bounds blocks_out; *n_table_out receives the
  * entries written; pos_out[i] = len-1 (the newest position). */

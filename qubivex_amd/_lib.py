@@ -118,6 +118,8 @@ SIGNATURES = {
     "qvkv_seq_touch": (_i32, [_vp, _u32]),
     "qvkv_pool_plan_append": (_i32, [_vp, _vp, _vp, _u32, _u32, _vp]),
     "qvkv_pool_tables": (_i32, [_vp, _vp, _u32, _u32, _vp, _u64, _P(_u64), _vp, _vp]),
+    "qvkv_pool_plan_attention": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _vp, _u64, _P(_u64), _vp,
+                                        _vp, _vp, _vp, _vp, _u64, _P(_u64)]),
     "qvkv_pool_evict_lru": (_i32, [_vp, _u64, _vp, _u32, _P(_u32)]),
     "qvkv_pool_compact": (_i32, [_vp, _u64, _P(_u64)]),
     "qvkv_pool_refcount": (_i32, [_vp, _u32, _P(_u32)]),

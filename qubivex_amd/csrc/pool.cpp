@@ -28,6 +28,7 @@
 struct Seq {
     bool live = false;
     uint64_t used = 0;
+    uint64_t epoch = 0;                         // host cache epoch the tables belong to
     std::vector<std::vector<uint32_t>> blocks;  // per layer, in position order
     std::vector<uint32_t> len;                  // per layer, positions written
 };
@@ -310,6 +311,95 @@ int qvkv_pool_plan_append(qvkv_pool *p, const uint32_t *seqs, const uint32_t *co
     }
     p->layers++;
     // A shared block's filled slots are copied before the caller writes into the copy.
+    return copy_blocks(p, src, dst);
+}
+
+int qvkv_pool_plan_attention(qvkv_pool *p, const uint32_t *seqs, const uint32_t *pos,
+                             const uint64_t *epochs, uint32_t n_seqs, uint32_t layer,
+                             uint32_t *blocks_out, uint64_t blocks_cap, uint64_t *n_table_out,
+                             uint32_t *table_at_out, uint32_t *new_slot_out,
+                             uint32_t *sync_to_out, uint32_t *sync_item_out,
+                             uint32_t *sync_pos_out, uint64_t sync_cap, uint64_t *n_sync_out) {
+    if (!p || !n_table_out || !n_sync_out ||
+        (n_seqs && (!seqs || !pos || !epochs || !table_at_out || !new_slot_out)))
+        return err(QVKV_E_SHAPE, "shape mismatch in pool: null argument");
+    std::lock_guard<std::mutex> lk(p->mu);
+    if (layer >= p->n_layers) return err(QVKV_E_SHAPE, "shape mismatch in pool: no such layer");
+    const uint32_t B = p->layout.block;
+    for (uint32_t i = 0; i < n_seqs; i++) {
+        if (!seq_of(p, seqs[i])) return err(QVKV_E_SHAPE, "shape mismatch in pool: no such sequence");
+        for (uint32_t j = 0; j < i; j++)
+            if (seqs[j] == seqs[i]) return err(QVKV_E_SHAPE, "shape mismatch in pool: a sequence twice in one plan");
+    }
+    uint64_t at = 0, ns = 0;
+    std::vector<uint32_t> src, dst;
+    for (uint32_t i = 0; i < n_seqs; i++) {
+        Seq &s = p->seqs[seqs[i]];
+        // A mirror of another epoch (the host cache was cleared or restored) starts again
+        // (discrete.rs:975-978): every block back, in table order.
+        if (s.epoch != epochs[i]) {
+            for (uint32_t l = 0; l < p->n_layers; l++) {
+                for (uint32_t b : s.blocks[l]) unref(p, b, nullptr);
+                s.blocks[l].clear();
+                s.len[l] = 0;
+            }
+            s.epoch = epochs[i];
+        }
+        auto &tab = s.blocks[layer];
+        // Rows past the host's count may be from a pass that failed after the device
+        // stored them: they are written again (discrete.rs:983-985).
+        const uint32_t synced = std::min(s.len[layer], pos[i]);
+        // A write into a shared block copies it first (positions synced..pos).
+        for (uint64_t bi = synced / B; bi <= pos[i] / B && bi < tab.size(); bi++) {
+            const uint32_t old = tab[bi];
+            if (p->refs[old] > 1) {
+                if (p->free.empty()) {
+                    p->full++;
+                    copy_blocks(p, src, dst);
+                    return err(QVKV_E_OOM, "hip device is out of memory: the KV pool has no free block");
+                }
+                const uint32_t nb = p->free.back();
+                p->free.pop_back();
+                p->refs[nb] = 1;
+                p->refs[old]--;
+                tab[bi] = nb;
+                src.push_back(old);
+                dst.push_back(nb);
+                p->cow++;
+            }
+        }
+        const uint64_t need = (uint64_t)pos[i] / B + 1;  // discrete.rs:988-994
+        while (tab.size() < need) {
+            if (p->free.empty()) {
+                p->full++;
+                copy_blocks(p, src, dst);
+                return err(QVKV_E_OOM, "hip device is out of memory: the KV pool has no free block");
+            }
+            const uint32_t nb = p->free.back();
+            p->free.pop_back();
+            p->refs[nb] = 1;
+            tab.push_back(nb);
+        }
+        if (at + need > blocks_cap || at > 0xffffffffull)
+            return err(QVKV_E_SHAPE, "shape mismatch in pool: blocks_out too small");
+        table_at_out[i] = (uint32_t)at;
+        if (blocks_out) std::copy(tab.begin(), tab.begin() + need, blocks_out + at);
+        at += need;
+        for (uint32_t q = synced; q < pos[i]; q++) {
+            if (ns >= sync_cap) return err(QVKV_E_SHAPE, "shape mismatch in pool: sync outputs too small");
+            sync_to_out[ns] = tab[q / B] * B + q % B;
+            sync_item_out[ns] = i;
+            sync_pos_out[ns] = q;
+            ns++;
+        }
+        new_slot_out[i] = tab[pos[i] / B] * B + pos[i] % B;
+        s.len[layer] = pos[i] + 1;
+        s.used = ++p->clock;
+    }
+    *n_table_out = at;
+    *n_sync_out = ns;
+    p->layers++;
+    p->rows += ns;
     return copy_blocks(p, src, dst);
 }
 

@@ -373,6 +373,30 @@ class KvPool:
                                         out.ctypes.data_as(ctypes.c_void_p)))
         return out
 
+    def plan_attention(self, seqs, pos, epochs, layer):
+        """attention_plan of one pass (qvkv_pool_plan_attention): returns a dict with
+        blocks, table_at, pos, new_slot, sync_to, sync_item, sync_pos."""
+        s, sp = _np(seqs, np.uint32)
+        p, pp = _np(pos, np.uint32)
+        e, ep = _np(epochs, np.uint64)
+        cap_b = int(sum(int(x) // self.layout.block + 1 for x in p))
+        cap_s = int(p.astype(np.int64).sum())
+        blocks = np.zeros(max(cap_b, 1), np.uint32)
+        table_at = np.zeros(s.size, np.uint32)
+        new_slot = np.zeros(s.size, np.uint32)
+        sync_to = np.zeros(max(cap_s, 1), np.uint32)
+        sync_item = np.zeros_like(sync_to)
+        sync_pos = np.zeros_like(sync_to)
+        nt, ns = ctypes.c_uint64(), ctypes.c_uint64()
+        vp = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
+        check(lib.qvkv_pool_plan_attention(self.handle, sp, pp, ep, s.size, layer, vp(blocks),
+                                           blocks.size, ctypes.byref(nt), vp(table_at),
+                                           vp(new_slot), vp(sync_to), vp(sync_item), vp(sync_pos),
+                                           sync_to.size, ctypes.byref(ns)))
+        n = ns.value
+        return {"blocks": blocks[:nt.value], "table_at": table_at, "pos": p, "new_slot": new_slot,
+                "sync_to": sync_to[:n], "sync_item": sync_item[:n], "sync_pos": sync_pos[:n]}
+
     def tables(self, seqs, layer):
         s, sp = _np(seqs, np.uint32)
         cap = sum((self.length(int(x), layer) + self.layout.block - 1) // self.layout.block

@@ -1,0 +1,122 @@
+"""The host-memory entry points (what a Rust DiscreteDevice binds: qvkv_alloc / write /
+append / gather / block_copy / decode_attention), concurrent callers on one device, and the
+device's counters (usage, transfers)."""
+import threading
+
+import numpy as np
+import pytest
+
+import oracle
+from helpers import MAX_ABS, REL_L2, attn_errors, random_tables, slots_of
+
+pytestmark = pytest.mark.gpu
+
+
+def test_write_read_round_trip_and_bounds(hip):
+    from qubivex_amd import DeviceError
+
+    buf = hip.alloc(4096)
+    data = np.arange(1024, dtype=np.uint32).tobytes()
+    hip.write(buf, 0, data)
+    assert hip.read(buf, 0, 4096) == data
+    hip.write(buf, 100, b"\x07" * 8)
+    assert hip.read(buf, 100, 8) == b"\x07" * 8
+    with pytest.raises(DeviceError):
+        hip.write(buf, 4090, b"\x00" * 8)  # past the end: DiscreteDevice::write's error
+    u = hip.usage()
+    assert u["used"] >= 4096 and u["capacity"] > 200 * 2**30
+    buf.close()
+
+
+@pytest.mark.parametrize("dtype", ["f16", "q8_0"])
+def test_host_append_gather_copy_match_the_oracle(hip, dtype):
+    from qubivex_amd import KvLayout
+
+    r = np.random.default_rng(31)
+    L = KvLayout(dtype, 4, 64, 16)
+    N = 24
+    buf = hip.alloc(N * L.block_bytes)
+    lens = [5, 16, 40]
+    blocks, table_at = random_tables(r, lens, 16, N - 6)
+    k = r.standard_normal((sum(lens), L.kv_out)).astype(np.float32)
+    v = r.standard_normal((sum(lens), L.kv_out)).astype(np.float32)
+    slots = np.concatenate([slots_of(blocks, table_at, t, np.arange(n), 16) for t, n in enumerate(lens)])
+    hip.append_host(L, buf, k, v, slots)
+    sim = oracle.SimPool(N, 4, 64, 16, oracle.F16 if dtype == "f16" else oracle.Q8_0)
+    sim.store(k, v, slots)
+    out_at = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.uint64)
+    gk, gv = hip.gather_host(L, buf, blocks, table_at, lens, out_at, sum(lens))
+    for t, n in enumerate(lens):
+        wk, wv = sim.gather(blocks, table_at, t, n)
+        a = int(out_at[t]) * L.kv_out
+        assert np.array_equal(gk[a:a + n * L.kv_out].reshape(4, n, 64), wk)
+        assert np.array_equal(gv[a:a + n * L.kv_out].reshape(4, n, 64), wv)
+    # copy the first item's block to a free one: the copy reads the same
+    free = sorted(set(range(N)) - set(blocks.tolist()))
+    hip.block_copy_host(L, buf, [blocks[0]], [free[0]])
+    b2 = blocks.copy()
+    b2[0] = free[0]
+    gk2, _ = hip.gather_host(L, buf, b2, table_at, lens, out_at, sum(lens))
+    assert np.array_equal(gk2, gk)
+    tr = hip.transfers()
+    assert tr["submissions"] > 0 and tr["upload_bytes"] > k.nbytes
+    buf.close()
+
+
+def test_host_entry_points_reject_out_of_range_ids(hip):
+    from qubivex_amd import KvLayout, ShapeError
+
+    L = KvLayout("f16", 2, 64, 16)
+    buf = hip.alloc(4 * L.block_bytes)
+    k = np.ones((1, L.kv_out), np.float32)
+    with pytest.raises(ShapeError):
+        hip.append_host(L, buf, k, k, [4 * 16])
+    with pytest.raises(ShapeError):
+        hip.block_copy_host(L, buf, [0], [7])
+    with pytest.raises(ShapeError):
+        hip.gather_host(L, buf, [0], [0], [20], [0], 20)  # one block for 20 positions
+    buf.close()
+
+
+def test_concurrent_callers_on_one_device(hip):
+    """Four threads run decode steps through the host entry point at once (the trait is
+    Send + Sync); every result matches its own oracle."""
+    from qubivex_amd import KvLayout
+
+    L = KvLayout("f16", 2, 64, 16)
+    H = 8
+    errors = []
+
+    def worker(seed):
+        try:
+            r = np.random.default_rng(seed)
+            N = 16
+            buf = hip.alloc(N * L.block_bytes)
+            pos = np.array([int(r.integers(1, 60))], np.uint32)
+            blocks, table_at = random_tables(r, [int(pos[0]) + 1], 16, N)
+            n = int(pos[0])
+            sync = r.standard_normal((n, 2 * L.kv_out)).astype(np.float32)
+            sync_to = slots_of(blocks, table_at, 0, np.arange(n), 16)
+            kn = r.standard_normal((1, L.kv_out)).astype(np.float32)
+            vn = r.standard_normal((1, L.kv_out)).astype(np.float32)
+            q = r.standard_normal((1, H, 64)).astype(np.float32)
+            for _ in range(5):
+                got = hip.decode_attention(L, buf, q, H, pos, blocks, table_at, sync.reshape(-1),
+                                           sync_to, kn, vn)
+            sim = oracle.SimPool(N, 2, 64, 16, oracle.F16)
+            sim.store(sync[:, :L.kv_out], sync[:, L.kv_out:], sync_to)
+            sim.store(kn, vn, slots_of(blocks, table_at, 0, [n], 16))
+            want = sim.attention(q, H, blocks, table_at, pos)
+            e = attn_errors(got, want)
+            if not (e[0] <= MAX_ABS and e[1] <= REL_L2):
+                errors.append((seed, e))
+            buf.close()
+        except Exception as ex:  # noqa: BLE001 - reported below
+            errors.append((seed, repr(ex)))
+
+    threads = [threading.Thread(target=worker, args=(s,)) for s in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors

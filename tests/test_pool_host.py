@@ -102,6 +102,90 @@ def test_tables_follow_attention_plan_restated():
     assert p.stats()["free"] == len(ref.free)
 
 
+def test_plan_attention_equals_restated_attention_plan():
+    """Host-authoritative decode passes with prompts, decode steps, clears (epoch changes)
+    and releases: blocks, table_at, pos and sync_to equal the restated attention_plan
+    (crates/qubivex-runtime/src/discrete.rs:951-1009) pass for pass."""
+    r = np.random.default_rng(11)
+    n_blocks, n_layers = 5000, 2
+    p = host_pool(n_blocks, n_layers)
+    ref = KvPoolRef(n_blocks, B)
+    live = {}  # handle -> [SeqRef, host positions held]
+    for step in range(150):
+        if len(live) < 5 and r.random() < 0.3:
+            h = p.create()
+            live[h] = [SeqRef(epoch=int(r.integers(0, 3))), int(r.integers(0, 100))]
+        if live and r.random() < 0.05:  # a cache dropped: its mirror gives its blocks back
+            h = list(live)[int(r.integers(len(live)))]
+            p.release(h)
+            q = live.pop(h)[0]
+            if q.mirror is not None:
+                q.mirror.release()  # the reference's Mirror drop
+        if live and r.random() < 0.08:  # clear and refill: a new epoch
+            h = list(live)[int(r.integers(len(live)))]
+            live[h][0].epoch += 1
+            live[h][1] = int(r.integers(0, 40))
+        if not live:
+            continue
+        handles = sorted(live)
+        for h in handles:  # this pass's token sits at the host's next position
+            live[h][0].pos = live[h][1]
+        for layer in range(n_layers):
+            seqs = [live[h][0] for h in handles]
+            for q in seqs:
+                q.host_k = q.host_v = []
+            want = attention_plan(ref, seqs, 0, 0, layer)
+            assert want is not None
+            after_run(ref, seqs, layer, want)
+            got = p.plan_attention(handles, [live[h][0].pos for h in handles],
+                                   [live[h][0].epoch for h in handles], layer)
+            assert got["blocks"].tolist() == want["blocks"], (step, layer)
+            assert got["table_at"].tolist() == want["table_at"]
+            assert got["pos"].tolist() == want["pos"]
+            assert got["sync_to"].tolist() == want["sync_to"], (step, layer)
+        for h in handles:
+            live[h][1] += 1  # the pass's token is now in the host cache
+    assert p.stats()["free"] == len(ref.free)
+
+
+def test_plan_attention_declines_the_layer_a_short_pool_cannot_hold():
+    """crates/qubivex-runtime/tests/discrete.rs:735-760: a pool one block short of every
+    layer declines that layer each step (`full`), and gives every block back on drop; the
+    prompt's rows are copied in once per layer."""
+    from qubivex_amd import OutOfDeviceMemory
+
+    L, prompt, steps = 4, 5, 8  # every position stays inside one block per layer
+    p = host_pool(L - 1, L)
+    s = p.create()
+    ran = 0
+    for step in range(steps):
+        pos = prompt + step
+        for layer in range(L):
+            try:
+                p.plan_attention([s], [pos], [0], layer)
+                ran += 1
+            except OutOfDeviceMemory:
+                assert layer == L - 1
+    st = p.stats()
+    assert (ran, st["full"]) == (steps * (L - 1), steps)
+    assert st["synced_rows"] == prompt * (L - 1)  # the prompt, once per layer that ran
+    p.release(s)
+    assert p.stats()["free"] == p.stats()["blocks"]
+
+
+def test_plan_attention_epoch_restart_copies_the_new_rows_in():
+    p = host_pool(32, 1)
+    s = p.create()
+    first = p.plan_attention([s], [40], [0], 0)
+    assert first["sync_to"].size == 40 and p.stats()["free"] == 29
+    again = p.plan_attention([s], [41], [0], 0)
+    assert again["sync_to"].size == 0  # nothing new on the host side
+    restarted = p.plan_attention([s], [5], [1], 0)  # the cache was cleared and refilled
+    assert restarted["sync_to"].size == 5 and p.stats()["free"] == 31
+    # the released blocks went back in table order, so the last one comes out first
+    assert first["blocks"].tolist() == [0, 1, 2] and restarted["blocks"].tolist() == [2]
+
+
 def test_every_block_returns_on_release():
     p = host_pool(64, 2)
     seqs = [p.create() for _ in range(4)]
