@@ -212,6 +212,9 @@ int qvkv_pool_take_copies(qvkv_pool *pool, uint32_t *src, uint32_t *dst, uint64_
                           uint64_t *n);
 void qvkv_pool_destroy(qvkv_pool *pool);
 void *qvkv_pool_ptr(const qvkv_pool *pool);
+/* The pool's device memory as a buffer for the host-memory entry points (owned by the
+ * pool; NULL for a host-only pool).  The runtime's kv_buffer (discrete.rs:502-512). */
+qvkv_buf *qvkv_pool_buffer(const qvkv_pool *pool);
 int qvkv_pool_stats(const qvkv_pool *pool, qvkv_pool_stats_t *out);
 
 /* A new empty sequence (a KvCache's mirror, discrete.rs:247-280). */

@@ -110,6 +110,7 @@ SIGNATURES = {
     "qvkv_pool_take_copies": (_i32, [_vp, _vp, _vp, _u64, _P(_u64)]),
     "qvkv_pool_destroy": (None, [_vp]),
     "qvkv_pool_ptr": (_vp, [_vp]),
+    "qvkv_pool_buffer": (_vp, [_vp]),
     "qvkv_pool_stats": (_i32, [_vp, _P(PoolStats)]),
     "qvkv_seq_create": (_i32, [_vp, _P(_u32)]),
     "qvkv_seq_release": (_i32, [_vp, _u32]),

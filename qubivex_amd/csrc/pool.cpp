@@ -172,6 +172,8 @@ int qvkv_pool_take_copies(qvkv_pool *p, uint32_t *src, uint32_t *dst, uint64_t c
 
 void *qvkv_pool_ptr(const qvkv_pool *pool) { return pool && pool->buf ? qvkv_buf_ptr(pool->buf) : nullptr; }
 
+qvkv_buf *qvkv_pool_buffer(const qvkv_pool *pool) { return pool ? pool->buf : nullptr; }
+
 int qvkv_pool_stats(const qvkv_pool *p, qvkv_pool_stats_t *out) {
     if (!p || !out) return err(QVKV_E_SHAPE, "shape mismatch in pool: null argument");
     std::lock_guard<std::mutex> lk(p->mu);

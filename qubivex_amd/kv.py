@@ -79,8 +79,8 @@ class DeviceBuffer:
     """Device memory from HipDevice.alloc: freed by close() or when collected (the
     reference's DeviceBuffer, freed on its last clone, discrete.rs:24-95)."""
 
-    def __init__(self, dev, handle):
-        self.dev, self.handle = dev, handle
+    def __init__(self, dev, handle, owned=True):
+        self.dev, self.handle, self.owned = dev, handle, owned
 
     @property
     def ptr(self):
@@ -90,9 +90,9 @@ class DeviceBuffer:
         return lib.qvkv_buf_len(self.handle)
 
     def close(self):
-        if self.handle:
+        if self.handle and self.owned:
             lib.qvkv_free(self.handle)
-            self.handle = None
+        self.handle = None
 
     def __del__(self):
         self.close()
@@ -338,6 +338,13 @@ class KvPool:
     def memory(self):
         """The pool's device memory, for the HipDevice kernel entry points."""
         return DevicePtr(self.ptr)
+
+    @property
+    def buffer(self):
+        """The pool's device memory as a buffer for the host-memory entry points (owned by
+        the pool: not freed by this object)."""
+        return DeviceBuffer(self.dev, ctypes.c_void_p(lib.qvkv_pool_buffer(self.handle)),
+                            owned=False)
 
     def stats(self):
         s = _lib.PoolStats()

@@ -78,6 +78,71 @@ def test_host_entry_points_reject_out_of_range_ids(hip):
     buf.close()
 
 
+def test_runtime_loop_with_host_authoritative_caches(hip):
+    """The reference runtime's decode loop on this library: each pass plans every layer
+    with qvkv_pool_plan_attention (attention_plan), copies in the host rows the pool lacks,
+    stores the new token and attends (qvkv_decode_attention).  Three sequences, a prompt,
+    decode steps, and one cache cleared and refilled (epoch change); every output is
+    checked against the oracle's attention over the host cache (f16-narrowed), and the
+    counters follow the reference's tests (crates/qubivex-runtime/tests/discrete.rs:692-733):
+    the prompt's rows are copied in once per layer and every block returns on drop."""
+    from qubivex_amd import KvLayout, KvPool
+
+    r = np.random.default_rng(77)
+    G, D, H, L, B = 2, 64, 4, 3, 16
+    layout = KvLayout("f16", G, D, B)
+    pool = KvPool(hip, layout, 64, L)
+    buf = pool.buffer
+    seqs = [pool.create() for _ in range(3)]
+    prompts = [20, 33, 7]
+    host = [[[] for _ in range(L)] for _ in seqs]  # per seq, per layer: list of (k, v) rows
+    epochs = [0, 0, 0]
+    for i, n in enumerate(prompts):
+        for layer in range(L):
+            for _ in range(n):
+                host[i][layer].append((r.standard_normal(G * D).astype(np.float32),
+                                       r.standard_normal(G * D).astype(np.float32)))
+
+    def one_pass():
+        pos = [len(host[i][0]) for i in range(len(seqs))]
+        for layer in range(L):
+            plan = pool.plan_attention(seqs, pos, epochs, layer)
+            sync = np.concatenate([np.concatenate(host[int(i)][layer][int(p)])
+                                   for i, p in zip(plan["sync_item"], plan["sync_pos"])]
+                                  ) if plan["sync_to"].size else np.zeros(0, np.float32)
+            kn = r.standard_normal((len(seqs), G * D)).astype(np.float32)
+            vn = r.standard_normal((len(seqs), G * D)).astype(np.float32)
+            q = r.standard_normal((len(seqs), H, D)).astype(np.float32)
+            got = hip.decode_attention(layout, buf, q, H, plan["pos"], plan["blocks"],
+                                       plan["table_at"], sync, plan["sync_to"], kn, vn)
+            for i in range(len(seqs)):
+                host[i][layer].append((kn[i], vn[i]))
+                ks = np.stack([k for k, _ in host[i][layer]]).astype(np.float16).astype(np.float32)
+                vs = np.stack([v for _, v in host[i][layer]]).astype(np.float16).astype(np.float32)
+                for h in range(H):
+                    g = h // (H // G)
+                    want = oracle.attend(q[i, h], ks[:, g * D:(g + 1) * D], vs[:, g * D:(g + 1) * D],
+                                         pos[i])
+                    e = attn_errors(got[i, h], want)
+                    assert e[0] <= MAX_ABS and e[1] <= REL_L2, (i, layer, h, e)
+
+    one_pass()
+    assert pool.stats()["synced_rows"] == sum(prompts) * L
+    for _ in range(4):
+        one_pass()
+    assert pool.stats()["synced_rows"] == sum(prompts) * L  # decode steps copy nothing in
+    # sequence 1's cache is cleared and refilled with another prompt: a new epoch
+    epochs[1] += 1
+    host[1] = [[(r.standard_normal(G * D).astype(np.float32),
+                 r.standard_normal(G * D).astype(np.float32)) for _ in range(12)] for _ in range(L)]
+    one_pass()
+    assert pool.stats()["synced_rows"] == (sum(prompts) + 12) * L
+    for s in seqs:
+        pool.release(s)
+    assert pool.stats()["free"] == pool.stats()["blocks"]
+    pool.close()
+
+
 def test_concurrent_callers_on_one_device(hip):
     """Four threads run decode steps through the host entry point at once (the trait is
     Send + Sync); every result matches its own oracle."""
