@@ -178,6 +178,46 @@ int qvkv_decode_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *po
                           const float *sync, const uint32_t *sync_to, uint32_t n_sync,
                           const float *k_new, const float *v_new, float *out);
 
+/* ---- the attention prelude feeding the append ----
+ *
+ * Bias, clip, Q/K RMSNorm and RoPE on the projection outputs, in place, bit for bit as
+ * the reference's forward pass (crates/qubivex-arch/src/lib.rs:1258-1292 with
+ * math::rms_norm, math::rope_rotate and the 64-lane reduce::dot shape; the device form
+ * is attn_prelude.comp).  Per-head norms (Qwen3) are supported, which the reference's
+ * device path declines. */
+
+#define QVKV_NORM_NONE 0
+#define QVKV_NORM_FULL 1     /* QkNorm::Full: one norm over each token's q (or k) row */
+#define QVKV_NORM_PER_HEAD 2 /* QkNorm::PerHead: one norm per head, weights of d */
+
+typedef struct qvkv_prelude_t {
+    uint32_t heads;    /* query heads (KV heads and d come from the layout) */
+    uint32_t norm;     /* QVKV_NORM_* */
+    uint32_t has_clip; /* clamp q, k, v to [-clip, clip] after the bias */
+    float clip;
+    float eps;         /* the norms' epsilon, as f32 (rms_scale casts it) */
+    const float *q_bias, *k_bias, *v_bias; /* q_out / kv_out values each, or NULL */
+    const float *q_norm, *k_norm; /* q_out / kv_out (full) or d (per head) weights */
+    const float *rope; /* [s][d] per token: cos of the d/2 pairs, then sin (Rope::table) */
+} qvkv_prelude_t;
+
+/* The prelude on device arrays (q [s][heads*d], k and v [s][G*d], all in place; the
+ * pointers inside *p are device pointers). */
+int qvkv_prelude_async(qvkv_dev *dev, const qvkv_layout *layout, const qvkv_prelude_t *p,
+                       float *q, float *k, float *v, uint32_t s, void *stream);
+
+/* The KV part of one DeviceMoeAttention submission from the projection outputs (the
+ * device side of SimDevice::attention, crates/qubivex-backend-cpu/src/sim.rs:310-436,
+ * without the matmuls): the prelude on q/k/v, the sync rows, then token t's k/v row at
+ * pos[t], then attention.  Host memory; *p's pointers are host pointers.  k_new and
+ * v_new receive the post-prelude rows for the host cache (discrete.rs:302-306). */
+int qvkv_prelude_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *pool,
+                           const qvkv_prelude_t *p, const float *q, const float *k,
+                           const float *v, const uint32_t *pos, uint32_t s,
+                           const uint32_t *blocks, uint64_t n_table, const uint32_t *table_at,
+                           const float *sync, const uint32_t *sync_to, uint32_t n_sync,
+                           float *out, float *k_new, float *v_new);
+
 /* ---- host pool manager: block pool, block tables, sharing, eviction, compaction ----
  *
  * The host side of the path, above the kernels: the reference's KvPool / KvFree /

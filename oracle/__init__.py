@@ -60,6 +60,13 @@ def lib():
         L.orc_f16_encode.argtypes = [f32p, sz, u16p]
         L.orc_f16_decode.argtypes = [u16p, sz, f32p]
         L.orc_exp_vec.argtypes = [f32p, sz, f32p]
+        L.orc_reduce_dot.argtypes = [f32p, f32p, sz]
+        L.orc_reduce_dot.restype = ctypes.c_float
+        L.orc_rms_norm.argtypes = [f32p, f32p, sz, ctypes.c_float]
+        L.orc_rope_rotate.argtypes = [f32p, f32p, sz]
+        vp = ctypes.c_void_p
+        L.orc_prelude.argtypes = [f32p, f32p, f32p, sz, sz, sz, sz, vp, vp, vp, ctypes.c_int,
+                                  ctypes.c_float, ctypes.c_int, vp, vp, ctypes.c_float, f32p]
         _lib = L
     return _lib
 
@@ -149,6 +156,44 @@ def attend_f64(q, k, v, pos):
     scores = np.zeros(pos + 1, np.float64)
     lib().orc_attend_f64(q, k, v, d, pos, out, scores)
     return out
+
+
+def reduce_dot(w, x):
+    w, x = _f32(w), _f32(x)
+    return float(lib().orc_reduce_dot(w, x, w.size))
+
+
+def rms_norm(x, w, eps):
+    x = _f32(x).copy()
+    lib().orc_rms_norm(x, _f32(w), x.size, float(eps))
+    return x
+
+
+def rope_rotate(head, cs):
+    head = _f32(head).copy()
+    lib().orc_rope_rotate(head, _f32(cs), head.size)
+    return head
+
+
+def prelude(q, k, v, heads, kvh, d, rope, q_bias=None, k_bias=None, v_bias=None, clip=None,
+            norm=0, q_norm=None, k_norm=None, eps=1e-6):
+    """The host forward pass's prelude (crates/qubivex-arch/src/lib.rs:1258-1292) on copies
+    of q [s][heads*d], k, v [s][kvh*d]; rope [s][d].  Returns (q, k, v)."""
+    q, k, v = _f32(q).copy(), _f32(k).copy(), _f32(v).copy()
+    keep = []
+
+    def ptr(a):
+        if a is None:
+            return None
+        a = _f32(a)
+        keep.append(a)
+        return a.ctypes.data_as(ctypes.c_void_p)
+
+    s = q.size // (heads * d)
+    lib().orc_prelude(q, k, v, s, heads, kvh, d, ptr(q_bias), ptr(k_bias), ptr(v_bias),
+                      int(clip is not None), float(clip or 0.0), int(norm), ptr(q_norm),
+                      ptr(k_norm), float(eps), _f32(rope))
+    return q, k, v
 
 
 class SimPool:

@@ -378,6 +378,76 @@ int orc_max_threads(void) {
 #endif
 }
 
+/* ---- the prelude: crates/qubivex-compute/src/reduce.rs, math.rs, arch/src/lib.rs ---- */
+
+/* reduce::dot (reduce.rs:11-50): 64 f32 lanes, one fma per lane per 64-element chunk,
+ * chunks in increasing order, the tail in lanes 0..rem, then the halving tree
+ * a[i] += a[i+w] for w = 32, 16, 8, 4 and (a0 + a1) + (a2 + a3). */
+float orc_reduce_dot(const float *w, const float *x, size_t n) {
+    float acc[64] = {0};
+    size_t full = n / 64 * 64;
+    for (size_t c = 0; c < full; c += 64)
+        for (int l = 0; l < 64; l++) acc[l] = fmaf(w[c + l], x[c + l], acc[l]);
+    for (size_t l = 0; l < n - full; l++) acc[l] = fmaf(w[full + l], x[full + l], acc[l]);
+    for (int wd = 32; wd >= 4; wd /= 2)
+        for (int i = 0; i < wd; i++) acc[i] += acc[i + wd];
+    return (acc[0] + acc[1]) + (acc[2] + acc[3]);
+}
+
+/* math::rms_norm / rms_scale / rms_scale_of (math.rs:89-116): x = (x * r) * w with
+ * r = 1 / sqrt(ss / n + eps), eps already cast to f32. */
+void orc_rms_norm(float *x, const float *w, size_t n, float eps) {
+    float ss = orc_reduce_dot(x, x, n);
+    float r = 1.0f / sqrtf(ss / (float)n + eps);
+    for (size_t i = 0; i < n; i++) x[i] = (x[i] * r) * w[i];
+}
+
+/* math::rope_rotate (math.rs:160-169): NeoX pairs i, i + d/2 with a table row
+ * cs = [cos..., sin...]. */
+void orc_rope_rotate(float *head, const float *cs, size_t d) {
+    size_t half = d / 2;
+    for (size_t i = 0; i < half; i++) {
+        float x1 = head[i], x2 = head[i + half];
+        head[i] = x1 * cs[i] - x2 * cs[half + i];
+        head[i + half] = x2 * cs[i] + x1 * cs[half + i];
+    }
+}
+
+/* The prelude of the host forward pass (crates/qubivex-arch/src/lib.rs:1258-1292), in
+ * place on s tokens: bias, clip, QK norm (0 none, 1 full width, 2 per head), RoPE with
+ * token t's table row rope[t*d ..]. */
+void orc_prelude(float *q, float *k, float *v, size_t s, size_t heads, size_t kvh, size_t d,
+                 const float *qb, const float *kb, const float *vb, int has_clip, float clip,
+                 int norm, const float *qn, const float *kn, float eps, const float *rope) {
+    size_t q_out = heads * d, kv_out = kvh * d;
+    float *ys[3] = {q, k, v};
+    const float *bs[3] = {qb, kb, vb};
+    size_t ns[3] = {q_out, kv_out, kv_out};
+    for (int part = 0; part < 3; part++)
+        if (bs[part])
+            for (size_t t = 0; t < s; t++)
+                for (size_t i = 0; i < ns[part]; i++) ys[part][t * ns[part] + i] += bs[part][i];
+    if (has_clip)
+        for (int part = 0; part < 3; part++)
+            for (size_t i = 0; i < s * ns[part]; i++) {
+                float z = ys[part][i];
+                ys[part][i] = z < -clip ? -clip : (z > clip ? clip : z);
+            }
+    if (norm == 1) {
+        for (size_t t = 0; t < s; t++) {
+            orc_rms_norm(q + t * q_out, qn, q_out, eps);
+            orc_rms_norm(k + t * kv_out, kn, kv_out, eps);
+        }
+    } else if (norm == 2) {
+        for (size_t r = 0; r < s * heads; r++) orc_rms_norm(q + r * d, qn, d, eps);
+        for (size_t r = 0; r < s * kvh; r++) orc_rms_norm(k + r * d, kn, d, eps);
+    }
+    for (size_t t = 0; t < s; t++) {
+        for (size_t h = 0; h < heads; h++) orc_rope_rotate(q + t * q_out + h * d, rope + t * d, d);
+        for (size_t h = 0; h < kvh; h++) orc_rope_rotate(k + t * kv_out + h * d, rope + t * d, d);
+    }
+}
+
 /* Vector form of orc_exp (test convenience). */
 void orc_exp_vec(const float *x, size_t n, float *out) {
     for (size_t i = 0; i < n; i++) out[i] = orc_exp(x[i]);

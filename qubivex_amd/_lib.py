@@ -58,6 +58,17 @@ class PoolStats(ctypes.Structure):
                                                 "evicted_blocks", "moved_blocks")]
 
 
+NORM_NONE, NORM_FULL, NORM_PER_HEAD = 0, 1, 2
+
+
+class Prelude(ctypes.Structure):
+    _fields_ = [("heads", ctypes.c_uint32), ("norm", ctypes.c_uint32),
+                ("has_clip", ctypes.c_uint32), ("clip", ctypes.c_float), ("eps", ctypes.c_float),
+                ("q_bias", ctypes.c_void_p), ("k_bias", ctypes.c_void_p),
+                ("v_bias", ctypes.c_void_p), ("q_norm", ctypes.c_void_p),
+                ("k_norm", ctypes.c_void_p), ("rope", ctypes.c_void_p)]
+
+
 class PrefixStats(ctypes.Structure):
     _fields_ = [(n, ctypes.c_uint64) for n in ("lookups", "hits", "tokens_reused", "inserted",
                                                 "evicted", "entries", "cost")]
@@ -106,6 +117,9 @@ SIGNATURES = {
     "qvkv_block_copy": (_i32, [_vp, _LP, _vp, _vp, _vp, _u32]),
     "qvkv_decode_attention": (_i32, [_vp, _LP, _vp, _vp, _u32, _vp, _u32, _vp, _u64, _vp, _vp,
                                      _vp, _u32, _vp, _vp, _vp]),
+    "qvkv_prelude_async": (_i32, [_vp, _LP, _P(Prelude), _vp, _vp, _vp, _u32, _vp]),
+    "qvkv_prelude_attention": (_i32, [_vp, _LP, _vp, _P(Prelude), _vp, _vp, _vp, _vp, _u32, _vp,
+                                      _u64, _vp, _vp, _vp, _u32, _vp, _vp, _vp]),
     "qvkv_pool_create": (_i32, [_vp, _LP, _u64, _u32, _P(_vp)]),
     "qvkv_pool_take_copies": (_i32, [_vp, _vp, _vp, _u64, _P(_u64)]),
     "qvkv_pool_destroy": (None, [_vp]),

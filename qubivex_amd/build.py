@@ -15,7 +15,7 @@ OUT_DIR = os.path.join(HERE, "lib")
 LIB = os.path.join(OUT_DIR, "libqvkv.so")
 ARCH = os.environ.get("QVKV_ARCH", "gfx950")
 
-HIP_SOURCES = ["kernels.hip", "abi.hip"]
+HIP_SOURCES = ["kernels.hip", "prelude.hip", "abi.hip"]
 CXX_SOURCES = ["pool.cpp", "prefix.cpp"]
 
 

@@ -622,4 +622,131 @@ int qvkv_decode_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *po
     return finish(dev, dev->stream);
 }
 
+// ---------------------------------------------------------------------------------
+// prelude
+// ---------------------------------------------------------------------------------
+
+static int prelude_shape(const Geometry &g, const qvkv_prelude_t *p) {
+    if (!p) return fail(QVKV_E_SHAPE, "shape mismatch in prelude: null parameters");
+    if (p->heads == 0 || p->heads % g.G != 0)
+        return fail(QVKV_E_SHAPE, "shape mismatch in prelude: %u heads, %d KV heads", p->heads, g.G);
+    if (g.D % 2 != 0) return fail(QVKV_E_SHAPE, "shape mismatch in prelude: odd head_dim");
+    if ((uint64_t)p->heads * g.D > 16384)
+        return fail(QVKV_E_SHAPE, "shape mismatch in prelude: heads*head_dim above 16384");
+    if (p->norm > QVKV_NORM_PER_HEAD) return fail(QVKV_E_UNSUPPORTED, "hip backend has no such norm");
+    if (!p->rope) return fail(QVKV_E_SHAPE, "shape mismatch in prelude: no rope rows");
+    return QVKV_OK;
+}
+
+static qvkv::PreludeArgs prelude_args(const qvkv_prelude_t *p) {
+    return qvkv::PreludeArgs{p->norm, p->has_clip, p->clip, p->eps, p->q_bias, p->k_bias,
+                             p->v_bias, p->norm ? p->q_norm : nullptr,
+                             p->norm ? p->k_norm : nullptr, p->rope};
+}
+
+int qvkv_prelude_async(qvkv_dev *dev, const qvkv_layout *layout, const qvkv_prelude_t *p,
+                       float *q, float *k, float *v, uint32_t s, void *stream) {
+    if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    Geometry g;
+    if (int rc = geometry(layout, &g)) return rc;
+    if (int rc = prelude_shape(g, p)) return rc;
+    if (s == 0) return QVKV_OK;
+    if (!q || !k || !v) return fail(QVKV_E_SHAPE, "shape mismatch in prelude: null pointer");
+    if (int rc = set_device(dev)) return rc;
+    return launched(dev, qvkv::launch_prelude(q, k, v, s, p->heads, (uint32_t)g.G, (uint32_t)g.D,
+                                              prelude_args(p), pick(dev, stream)),
+                    "prelude launch");
+}
+
+int qvkv_prelude_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *pool,
+                           const qvkv_prelude_t *p, const float *q, const float *k,
+                           const float *v, const uint32_t *pos, uint32_t s,
+                           const uint32_t *blocks, uint64_t n_table, const uint32_t *table_at,
+                           const float *sync, const uint32_t *sync_to, uint32_t n_sync,
+                           float *out, float *k_new, float *v_new) {
+    if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    Geometry g;
+    if (int rc = geometry(layout, &g)) return rc;
+    if (int rc = prelude_shape(g, p)) return rc;
+    uint64_t held;
+    if (int rc = pool_of(dev, pool, g, &held)) return rc;
+    const uint32_t heads = p->heads;
+    qvkv::AttnPlan plan;
+    const char *why = "";
+    uint32_t max_pos = 0;
+    for (uint32_t t = 0; t < s; t++) max_pos = std::max(max_pos, pos[t]);
+    if (int rc = qvkv::plan_attention(g, s, heads, max_pos, &plan, &why))
+        return fail(rc, "shape mismatch in routed moe attention: %s", why);
+    if (s == 0) return QVKV_OK;
+    for (uint64_t i = 0; i < n_table; i++)
+        if (blocks[i] >= held)
+            return fail(QVKV_E_SHAPE, "shape mismatch in routed moe attention: a block past the pool's %llu",
+                        (unsigned long long)held);
+    for (uint32_t i = 0; i < n_sync; i++)
+        if (sync_to[i] / g.B >= held)
+            return fail(QVKV_E_SHAPE, "shape mismatch in routed moe attention: a block past the pool's %llu",
+                        (unsigned long long)held);
+    std::vector<uint32_t> slots(s);
+    for (uint32_t t = 0; t < s; t++) {
+        if ((uint64_t)table_at[t] + pos[t] / g.B + 1 > n_table)
+            return fail(QVKV_E_SHAPE, "shape mismatch in routed moe attention: token %u has no block for position %u",
+                        t, pos[t]);
+        slots[t] = blocks[table_at[t] + pos[t] / g.B] * g.B + pos[t] % g.B;
+    }
+    std::vector<float> sk((uint64_t)n_sync * g.kv_out), sv((uint64_t)n_sync * g.kv_out);
+    for (uint32_t r = 0; r < n_sync; r++) {
+        memcpy(&sk[(uint64_t)r * g.kv_out], sync + (uint64_t)r * 2 * g.kv_out, g.kv_out * 4);
+        memcpy(&sv[(uint64_t)r * g.kv_out], sync + ((uint64_t)r * 2 + 1) * g.kv_out, g.kv_out * 4);
+    }
+    std::lock_guard<std::mutex> lk(dev->mu);
+    if (int rc = set_device(dev)) return rc;
+    if (plan.ws_bytes)
+        if (int rc = ensure(dev, &dev->ws, &dev->ws_bytes, plan.ws_bytes)) return rc;
+    const uint64_t q_out = (uint64_t)heads * g.D, rowb = g.kv_out * 4, qb = s * q_out * 4;
+    const uint64_t nq = p->norm == QVKV_NORM_PER_HEAD ? g.D : q_out;
+    const uint64_t nk = p->norm == QVKV_NORM_PER_HEAD ? g.D : g.kv_out;
+    Stager st;
+    const uint64_t qo = st.add(q, qb), ko = st.add(k, s * rowb), vo = st.add(v, s * rowb),
+                   ro = st.add(p->rope, (uint64_t)s * g.D * 4),
+                   qbo = p->q_bias ? st.add(p->q_bias, q_out * 4) : 0,
+                   kbo = p->k_bias ? st.add(p->k_bias, rowb) : 0,
+                   vbo = p->v_bias ? st.add(p->v_bias, rowb) : 0,
+                   qno = (p->norm && p->q_norm) ? st.add(p->q_norm, nq * 4) : 0,
+                   kno = (p->norm && p->k_norm) ? st.add(p->k_norm, nk * 4) : 0,
+                   sko = st.add(sk.data(), n_sync * rowb), svo = st.add(sv.data(), n_sync * rowb),
+                   sto = st.add(sync_to, n_sync * 4ull), slo = st.add(slots.data(), s * 4ull),
+                   po = st.add(pos, s * 4ull), bo = st.add(blocks, n_table * 4),
+                   tao = st.add(table_at, s * 4ull), oo = st.reserve(qb);
+    if (int rc = st.upload(dev)) return rc;
+    qvkv::PreludeArgs a = prelude_args(p);
+    a.q_bias = p->q_bias ? st.at<float>(dev, qbo) : nullptr;
+    a.k_bias = p->k_bias ? st.at<float>(dev, kbo) : nullptr;
+    a.v_bias = p->v_bias ? st.at<float>(dev, vbo) : nullptr;
+    a.q_norm = (p->norm && p->q_norm) ? st.at<float>(dev, qno) : nullptr;
+    a.k_norm = (p->norm && p->k_norm) ? st.at<float>(dev, kno) : nullptr;
+    a.rope = st.at<float>(dev, ro);
+    float *dq = st.at<float>(dev, qo), *dk = st.at<float>(dev, ko), *dv = st.at<float>(dev, vo);
+    hipError_t e = qvkv::launch_prelude(dq, dk, dv, s, heads, (uint32_t)g.G, (uint32_t)g.D, a,
+                                        dev->stream);
+    if (int rc = launched(dev, e, "prelude launch")) return rc;
+    if (n_sync) {
+        e = qvkv::launch_append(g, pool->ptr, held, st.at<float>(dev, sko), st.at<float>(dev, svo),
+                                st.at<uint32_t>(dev, sto), n_sync, dev->d_err, dev->stream);
+        if (int rc = launched(dev, e, "append launch (sync rows)")) return rc;
+    }
+    e = qvkv::launch_append(g, pool->ptr, held, dk, dv, st.at<uint32_t>(dev, slo), s, dev->d_err,
+                            dev->stream);
+    if (int rc = launched(dev, e, "append launch (new rows)")) return rc;
+    e = qvkv::launch_attention(g, plan, pool->ptr, held, dq, st.at<uint32_t>(dev, bo), n_table,
+                               st.at<uint32_t>(dev, tao), st.at<uint32_t>(dev, po), s, heads,
+                               max_pos, st.at<float>(dev, oo), dev->ws, dev->d_err, dev->stream);
+    if (int rc = launched(dev, e, "attention launch")) return rc;
+    if (int rc = download(dev, out, st.at<void>(dev, oo), qb)) return rc;
+    if (k_new)
+        if (int rc = download(dev, k_new, dk, s * rowb)) return rc;
+    if (v_new)
+        if (int rc = download(dev, v_new, dv, s * rowb)) return rc;
+    return finish(dev, dev->stream);
+}
+
 }  // extern "C"

@@ -38,6 +38,15 @@ hipError_t launch_block_copy(const Geometry &g, void *pool, uint64_t pool_blocks
                              const uint32_t *src, const uint32_t *dst, uint32_t n, int *err,
                              hipStream_t s);
 
+// The prelude (prelude.hip): device pointers, contract-off f32 arithmetic.
+struct PreludeArgs {
+    uint32_t norm, has_clip;
+    float clip, eps;
+    const float *q_bias, *k_bias, *v_bias, *q_norm, *k_norm, *rope;
+};
+hipError_t launch_prelude(float *q, float *k, float *v, uint32_t s, uint32_t heads,
+                          uint32_t kvh, uint32_t d, const PreludeArgs &a, hipStream_t st);
+
 // Attention: the launch plan decides the split over the context and the workspace.
 struct AttnPlan {
     int kind;           // 0: MFMA kernel, 1: generic kernel

@@ -186,6 +186,61 @@ class HipDevice:
                                         pool_blocks, _ptr(src), _ptr(dst), src.numel(),
                                         _stream(stream)))
 
+    @staticmethod
+    def _prelude_struct(heads, norm, clip, eps, ptrs):
+        nm = {"none": _lib.NORM_NONE, "full": _lib.NORM_FULL, "per_head": _lib.NORM_PER_HEAD}[norm]
+        return _lib.Prelude(heads, nm, int(clip is not None), float(clip or 0.0), float(eps),
+                            *[ptrs.get(n) for n in ("q_bias", "k_bias", "v_bias", "q_norm",
+                                                    "k_norm", "rope")])
+
+    def prelude(self, layout: KvLayout, heads, q, k, v, rope, norm="none", clip=None, eps=1e-6,
+                q_bias=None, k_bias=None, v_bias=None, q_norm=None, k_norm=None, stream=None):
+        """The prelude in place on device tensors q [s][heads*d], k, v [s][G*d]."""
+        ptrs = {n: (None if t is None else t.data_ptr()) for n, t in
+                (("q_bias", q_bias), ("k_bias", k_bias), ("v_bias", v_bias),
+                 ("q_norm", q_norm), ("k_norm", k_norm), ("rope", rope))}
+        p = self._prelude_struct(heads, norm, clip, eps, ptrs)
+        s = q.numel() // (heads * layout.head_dim)
+        check(lib.qvkv_prelude_async(self.handle, ctypes.byref(layout.c), ctypes.byref(p),
+                                     _ptr(q), _ptr(k), _ptr(v), s, _stream(stream)))
+
+    def prelude_attention(self, layout, buf: DeviceBuffer, heads, q, k, v, rope, pos, blocks,
+                          table_at, sync, sync_to, norm="none", clip=None, eps=1e-6,
+                          q_bias=None, k_bias=None, v_bias=None, q_norm=None, k_norm=None):
+        """One DeviceMoeAttention's KV work from projection outputs (host memory): returns
+        (attention out [s][heads][d], k_new, v_new after the prelude)."""
+        keep = {}
+
+        def host(name, a):
+            if a is None:
+                return None
+            arr, pp = _np(a, np.float32)
+            keep[name] = arr
+            return pp.value
+
+        ptrs = {n: host(n, a) for n, a in (("q_bias", q_bias), ("k_bias", k_bias),
+                                           ("v_bias", v_bias), ("q_norm", q_norm),
+                                           ("k_norm", k_norm), ("rope", rope))}
+        p = self._prelude_struct(heads, norm, clip, eps, ptrs)
+        q, qp = _np(q, np.float32)
+        k, kp = _np(k, np.float32)
+        v, vp = _np(v, np.float32)
+        pos, pp = _np(pos, np.uint32)
+        b, bp = _np(blocks, np.uint32)
+        t, tp = _np(table_at, np.uint32)
+        sy, syp = _np(sync, np.float32)
+        st, stp = _np(sync_to, np.uint32)
+        s = pos.size
+        out = np.zeros(s * heads * layout.head_dim, np.float32)
+        k_new = np.zeros(s * layout.kv_out, np.float32)
+        v_new = np.zeros_like(k_new)
+        vp_ = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
+        check(lib.qvkv_prelude_attention(self.handle, ctypes.byref(layout.c), buf.handle,
+                                         ctypes.byref(p), qp, kp, vp, pp, s, bp, b.size, tp, syp,
+                                         stp, st.size, vp_(out), vp_(k_new), vp_(v_new)))
+        return (out.reshape(s, heads, layout.head_dim), k_new.reshape(s, layout.kv_out),
+                v_new.reshape(s, layout.kv_out))
+
     # -- host-memory forms (synchronous) --
     def append_host(self, layout, buf: DeviceBuffer, k, v, slots):
         k, kp = _np(k, np.float32)

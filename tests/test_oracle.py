@@ -298,3 +298,77 @@ def test_reference_layout_addressing_at_block_256():
     assert words == set(range(2 * B * kv_out, 4 * B * kv_out))
     assert L.orc_key_word(kv_out, d, B, B + 3, 1, 2) == 2 * B * kv_out + (1 * d + 2) * B + 3
     assert L.orc_value_word(kv_out, d, B, B + 3, 1, 2) == 2 * B * kv_out + B * kv_out + 3 * kv_out + d + 2
+
+
+def test_reduce_dot_matches_f64_and_handles_tails():
+    """crates/qubivex-compute/src/reduce.rs:56-80, the reference's own test."""
+    for n in [0, 1, 31, 32, 63, 64, 65, 100, 128, 1000, 2048]:
+        i = np.arange(n)
+        w = (((i * 37) % 101).astype(np.float32) - 50) / np.float32(64)
+        x = (((i * 53) % 97).astype(np.float32) - 48) / np.float32(32)
+        want = float(np.sum(w.astype(np.float64) * x.astype(np.float64)))
+        got = oracle.reduce_dot(w, x)
+        assert abs(got - want) <= 1e-5 * max(abs(want), 1.0), (n, got, want)
+
+
+def test_reduce_dot_shape_is_observable():
+    """Positive control: a plain sequential sum gives other bits on some inputs, so a
+    kernel that matches the shape bit for bit does follow it."""
+    r = np.random.default_rng(12)
+    differ = 0
+    for _ in range(200):
+        x = (r.standard_normal(4096) * 10).astype(np.float32)
+        seq = np.float32(0)
+        for v in x:
+            seq = np.float32(np.fma(v, v, seq)) if hasattr(np, "fma") else np.float32(seq + v * v)
+        differ += oracle.reduce_dot(x, x) != float(seq)
+        if differ:
+            break
+    assert differ
+
+
+def test_rms_norm_and_rope_closed_forms():
+    # 64 threes: ss = 576 exactly, ss/n = 9, sqrt = 3, r = f32(1/3)
+    y = oracle.rms_norm(np.full(64, 3.0, np.float32), np.ones(64, np.float32), 0.0)
+    assert np.all(y == np.float32(3.0) * (np.float32(1.0) / np.float32(3.0)))
+    # the weights multiply after the scale
+    w = np.arange(64, dtype=np.float32)
+    y2 = oracle.rms_norm(np.full(64, 3.0, np.float32), w, 0.0)
+    assert np.array_equal(y2, y * w)
+    r = np.random.default_rng(13)
+    h = r.standard_normal(128).astype(np.float32)
+    ident = np.concatenate([np.ones(64), np.zeros(64)]).astype(np.float32)
+    assert np.array_equal(oracle.rope_rotate(h, ident), h)
+    quarter = np.concatenate([np.zeros(64), np.ones(64)]).astype(np.float32)
+    assert np.array_equal(oracle.rope_rotate(h, quarter), np.concatenate([-h[64:], h[:64]]))
+    # a rotation keeps each pair's length (to rounding)
+    a = r.uniform(0, 6.3, 64)
+    cs = np.concatenate([np.cos(a), np.sin(a)]).astype(np.float32)
+    y = oracle.rope_rotate(h, cs)
+    np.testing.assert_allclose(y[:64] ** 2 + y[64:] ** 2, h[:64] ** 2 + h[64:] ** 2, rtol=1e-5)
+
+
+def test_prelude_composes_bias_clip_norm_rope_in_order():
+    r = np.random.default_rng(14)
+    heads, kvh, d, s = 4, 2, 64, 3
+    q = (r.standard_normal((s, heads * d)) * 3).astype(np.float32)
+    k = (r.standard_normal((s, kvh * d)) * 3).astype(np.float32)
+    v = (r.standard_normal((s, kvh * d)) * 3).astype(np.float32)
+    rope = r.uniform(-1, 1, (s, d)).astype(np.float32)
+    qb = r.standard_normal(heads * d).astype(np.float32)
+    qn = r.uniform(0.5, 1.5, d).astype(np.float32)
+    kn = r.uniform(0.5, 1.5, d).astype(np.float32)
+    gq, gk, gv = oracle.prelude(q, k, v, heads, kvh, d, rope, q_bias=qb, clip=2.5, norm=2,
+                                q_norm=qn, k_norm=kn, eps=1e-6)
+    # by hand with the single-step functions
+    wq = np.clip(q + qb, -2.5, 2.5).astype(np.float32)
+    wk = np.clip(k, -2.5, 2.5).astype(np.float32)
+    for t in range(s):
+        for h in range(heads):
+            x = oracle.rms_norm(wq[t, h * d:(h + 1) * d], qn, 1e-6)
+            wq[t, h * d:(h + 1) * d] = oracle.rope_rotate(x, rope[t])
+        for h in range(kvh):
+            x = oracle.rms_norm(wk[t, h * d:(h + 1) * d], kn, 1e-6)
+            wk[t, h * d:(h + 1) * d] = oracle.rope_rotate(x, rope[t])
+    assert np.array_equal(gq.reshape(s, -1), wq) and np.array_equal(gk.reshape(s, -1), wk)
+    assert np.array_equal(gv.reshape(s, -1), np.clip(v, -2.5, 2.5))
