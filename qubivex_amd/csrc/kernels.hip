@@ -979,9 +979,13 @@ static int tune(const char *name, int def) {
     return s && *s ? atoi(s) : def;
 }
 
-static unsigned grid_for(uint64_t threads) {
+// Workgroups for a grid-stride kernel over `threads` work items, at most per_cu per CU.
+// A streaming kernel runs best with short-lived workgroups (one pass each): the hardware
+// dispatcher then keeps every CU full through the tail, where strided loops leave
+// stragglers.
+static unsigned grid_for(uint64_t threads, uint64_t per_cu) {
     uint64_t wgs = (threads + 255) / 256;
-    const uint64_t cap = 256ull * 64ull;  // 64 workgroups per CU, grid-stride beyond
+    const uint64_t cap = 256ull * per_cu;
     return (unsigned)(wgs < 1 ? 1 : (wgs > cap ? cap : wgs));
 }
 
@@ -990,13 +994,14 @@ hipError_t launch_append(const Geometry &g, void *pool, uint64_t pool_blocks, co
                          hipStream_t s) {
     const Geo geo = to_geo(g);
     const uint64_t per_row = 2 * (g.kv_out / 8);
-    const int U = tune("QVKV_APPEND_U", 4);
+    const int U = tune("QVKV_APPEND_U", 2);
+    const uint64_t per_cu = (uint64_t)tune("QVKV_APPEND_GRID_PER_CU", 1 << 20);
     const bool NT = tune("QVKV_APPEND_NT", 1) != 0;
     // keep the flat index inside 32 bits: launch in row batches
     const uint32_t max_rows = (uint32_t)((0x7fffffffull / per_row));
     for (uint32_t r0 = 0; r0 < n; r0 += max_rows) {
         const uint32_t nr = n - r0 < max_rows ? n - r0 : max_rows;
-        const unsigned grid = grid_for(((uint64_t)nr * per_row + U - 1) / U);
+        const unsigned grid = grid_for(((uint64_t)nr * per_row + U - 1) / U, per_cu);
         const float *kk = k + (uint64_t)r0 * g.kv_out, *vv = v + (uint64_t)r0 * g.kv_out;
 #define QV_APPEND(DT, UU, NN)                                                                  \
     hipLaunchKernelGGL((k_append<DT, UU, NN>), dim3(grid), dim3(256), 0, s, (uint8_t *)pool,   \
