@@ -54,7 +54,7 @@ def parse():
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--legs", default="append,decode,gather,copy")
+    ap.add_argument("--legs", default="append,decode,gather,copy,prefill")
     return ap.parse_args()
 
 
@@ -255,6 +255,39 @@ def main():
         c_bytes = 2.0 * ncp * L.block_bytes + ncp * 8
         result.update(copy_ms=c_ms, copy_gbs=c_bytes / (c_ms / 1e3) / 1e9)
         log(f"[bench] block copy {ncp} blocks: {c_ms:.3f} ms = {result['copy_gbs']:.0f} GB/s")
+
+    if "prefill" in legs:
+        # Paged prefill attention: a chunk of PF tokens at the end of every sequence's
+        # stored context (positions ctx-1-PF .. ctx-2) on one layer, causal.
+        PF = int(min(512, int(ctx.min()) - 1))
+        b0, t0_, p0_ = tabs[0]
+        seg_pos0 = (p0_.astype(np.int64) - PF).astype(np.uint32)  # p0_ = ctx-1
+        n_tok = np.full(S, PF, np.uint32)
+        q_at = (np.arange(S, dtype=np.uint32) * PF).astype(np.uint32)
+        qp = torch.randn((S * PF, H, D), generator=gen, device="cuda")
+        op = torch.empty_like(qp)
+        d_pb, d_pt, d_pp, d_qa, d_nt = cu32(b0), cu32(t0_), cu32(seg_pos0), cu32(q_at), cu32(n_tok)
+        pmax = int(seg_pos0.max()) + PF - 1
+        for _ in range(2):
+            dev.prefill_attention(L, mem, n_blocks, qp, d_pb, d_pt, d_pp, d_qa, d_nt, H, pmax, PF, op)
+        torch.cuda.synchronize()
+        dev.check()
+        reps = 5
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            dev.prefill_attention(L, mem, n_blocks, qp, d_pb, d_pt, d_pp, d_qa, d_nt, H, pmax, PF, op)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        dev.check()
+        p_ms = e0.elapsed_time(e1) / reps
+        seen = float(np.sum([PF * (int(p) + 1) + PF * (PF - 1) / 2 for p in seg_pos0]))
+        p_flops = 4.0 * H * D * seen
+        result.update(prefill_ms=p_ms, prefill_tok_s=S * PF / (p_ms / 1e3),
+                      prefill_tflops=p_flops / (p_ms / 1e3) / 1e12)
+        log(f"[bench] prefill {S} x {PF} tokens (1 layer, ctx {int(ctx.min())}..{int(ctx.max())}): "
+            f"{p_ms:.3f} ms = {result['prefill_tok_s']:.0f} tok/s, {result['prefill_tflops']:.1f} TFLOP/s")
+        del qp, op
 
     if append_ms:
         a_ms = float(np.mean(append_ms))

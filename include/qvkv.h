@@ -142,6 +142,22 @@ int qvkv_attention_async(qvkv_dev *dev, const qvkv_layout *layout, const void *p
                          uint32_t n_items, uint32_t heads, uint32_t max_pos, float *out,
                          void *stream);
 
+/* Paged prefill attention: segment i holds n_tok[i] consecutive tokens of one sequence
+ * whose rows are already stored; token j of it sits at position pos0[i] + j and reads
+ * q row q_at[i] + j ([q_rows][heads][d] f32) and writes the same out row.  It attends
+ * (causally) over positions 0..pos0[i]+j of its table exactly as qvkv_attention_async
+ * would for an item with pos = pos0[i]+j; max_pos bounds pos0[i]+n_tok[i]-1 and max_tok
+ * bounds n_tok[i].  Replaces the host prefill of the reference's forward pass, which
+ * stores a segment's rows and then runs math::attend per (token, head)
+ * (crates/qubivex-arch/src/lib.rs:1296-1320); the reference has no device prefill. */
+int qvkv_prefill_attention_async(qvkv_dev *dev, const qvkv_layout *layout, const void *pool,
+                                 uint64_t pool_blocks, const float *q, uint64_t q_rows,
+                                 const uint32_t *blocks, uint64_t n_table,
+                                 const uint32_t *table_at, const uint32_t *pos0,
+                                 const uint32_t *q_at, const uint32_t *n_tok, uint32_t n_seg,
+                                 uint32_t heads, uint32_t max_pos, uint32_t max_tok, float *out,
+                                 void *stream);
+
 /* Block copy: block src[i] -> block dst[i], i < n, byte for byte (copy-on-write of a
  * shared block; compaction moves).  No dst may appear twice or also be a src in the
  * same call.  No reference counterpart: the reference copies a whole prefix instead
@@ -171,7 +187,10 @@ int qvkv_block_copy(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *pool,
  * first the n_sync host rows (`sync`: n_sync * 2*G*d f32, key row then value row) to
  * `sync_to`, then token t's k_new/v_new row at its own position pos[t], then attention
  * of q over positions 0..=pos[t].  q, out: [s][heads][d]; k_new, v_new: [s][G*d].
- * blocks/table_at/pos as AttnPlan (crates/qubivex-runtime/src/discrete.rs:284-290). */
+ * blocks/table_at/pos as AttnPlan (crates/qubivex-runtime/src/discrete.rs:284-290).
+ * Runs of consecutive tokens with one table_at and consecutive positions (a prefill
+ * chunk) go through the prefill kernel of qvkv_prefill_attention_async; the results are
+ * those of attending each token on its own. */
 int qvkv_decode_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *pool,
                           const float *q, uint32_t heads, const uint32_t *pos, uint32_t s,
                           const uint32_t *blocks, uint64_t n_table, const uint32_t *table_at,

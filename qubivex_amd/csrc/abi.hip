@@ -200,7 +200,7 @@ int finish(qvkv_dev *dev, hipStream_t s) {
                     (bits & 1) ? "a block id past the pool; " : "",
                     (bits & 2) ? "a block table shorter than its positions; " : "",
                     (bits & 4) ? "a position past max_pos; " : "",
-                    (bits & 8) ? "an output range past out_positions; " : "");
+                    (bits & 8) ? "an output or query range past its bound (out_positions, q_rows); " : "");
     }
     return QVKV_OK;
 }
@@ -427,6 +427,29 @@ int qvkv_attention_async(qvkv_dev *dev, const qvkv_layout *layout, const void *p
                     "attention launch");
 }
 
+int qvkv_prefill_attention_async(qvkv_dev *dev, const qvkv_layout *layout, const void *pool,
+                                 uint64_t pool_blocks, const float *q, uint64_t q_rows,
+                                 const uint32_t *blocks, uint64_t n_table,
+                                 const uint32_t *table_at, const uint32_t *pos0,
+                                 const uint32_t *q_at, const uint32_t *n_tok, uint32_t n_seg,
+                                 uint32_t heads, uint32_t max_pos, uint32_t max_tok, float *out,
+                                 void *stream) {
+    if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    Geometry g;
+    if (int rc = geometry(layout, &g)) return rc;
+    const char *why = "";
+    if (int rc = qvkv::check_prefill(g, n_seg, heads, max_tok, &why))
+        return fail(rc, "shape mismatch in prefill attention: %s", why);
+    if (n_seg == 0 || max_tok == 0) return QVKV_OK;
+    if (!pool || !q || !blocks || !table_at || !pos0 || !q_at || !n_tok || !out)
+        return fail(QVKV_E_SHAPE, "shape mismatch in prefill attention: null pointer");
+    if (int rc = set_device(dev)) return rc;
+    return launched(dev, qvkv::launch_prefill(g, pool, pool_blocks, q, blocks, n_table, table_at,
+                                              pos0, q_at, n_tok, n_seg, heads, max_pos, max_tok,
+                                              q_rows, out, dev->d_err, pick(dev, stream)),
+                    "prefill attention launch");
+}
+
 int qvkv_block_copy_async(qvkv_dev *dev, const qvkv_layout *layout, void *pool,
                           uint64_t pool_blocks, const uint32_t *src, const uint32_t *dst,
                           uint32_t n, void *stream) {
@@ -552,6 +575,68 @@ int qvkv_block_copy(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *pool,
     return finish(dev, dev->stream);
 }
 
+}  // extern "C"
+
+namespace {
+
+// Runs of consecutive tokens that share a block table and have consecutive positions:
+// a prefill chunk of one sequence is one run, a decode batch is runs of one token.
+struct Segments {
+    std::vector<uint32_t> table_at, pos0, q_at, n_tok;
+    uint32_t max_tok = 0;
+};
+
+Segments segments_of(const uint32_t *table_at, const uint32_t *pos, uint32_t s) {
+    Segments r;
+    for (uint32_t t = 0; t < s;) {
+        uint32_t e = t + 1;
+        while (e < s && table_at[e] == table_at[t] && pos[e - 1] != UINT32_MAX &&
+               pos[e] == pos[e - 1] + 1)
+            e++;
+        r.table_at.push_back(table_at[t]);
+        r.pos0.push_back(pos[t]);
+        r.q_at.push_back(t);
+        r.n_tok.push_back(e - t);
+        r.max_tok = std::max(r.max_tok, e - t);
+        t = e;
+    }
+    return r;
+}
+
+// Device copies of a Segments, staged with the call's other inputs.
+struct StagedSegments {
+    uint64_t ta = 0, p0 = 0, qa = 0, nt = 0;
+    void add(Stager &st, const Segments &sg) {
+        const uint64_t b = sg.n_tok.size() * 4ull;
+        ta = st.add(sg.table_at.data(), b);
+        p0 = st.add(sg.pos0.data(), b);
+        qa = st.add(sg.q_at.data(), b);
+        nt = st.add(sg.n_tok.data(), b);
+    }
+};
+
+// Attention of s stored tokens: the prefill kernel when some run has two or more tokens
+// (every token then reads its table once per 32 query columns instead of once per token),
+// else the decode kernel.
+hipError_t attend_tokens(qvkv_dev *dev, const Geometry &g, const qvkv::AttnPlan &plan,
+                         const Segments &sg, const StagedSegments &ss, Stager &st,
+                         const void *pool, uint64_t held, const float *dq, const uint32_t *dblocks,
+                         uint64_t n_table, const uint32_t *dtable_at, const uint32_t *dpos,
+                         uint32_t s, uint32_t heads, uint32_t max_pos, float *dout) {
+    if (sg.max_tok >= 2)
+        return qvkv::launch_prefill(g, pool, held, dq, dblocks, n_table,
+                                    st.at<uint32_t>(dev, ss.ta), st.at<uint32_t>(dev, ss.p0),
+                                    st.at<uint32_t>(dev, ss.qa), st.at<uint32_t>(dev, ss.nt),
+                                    (uint32_t)sg.n_tok.size(), heads, max_pos, sg.max_tok, s,
+                                    dout, dev->d_err, dev->stream);
+    return qvkv::launch_attention(g, plan, pool, held, dq, dblocks, n_table, dtable_at, dpos, s,
+                                  heads, max_pos, dout, dev->ws, dev->d_err, dev->stream);
+}
+
+}  // namespace
+
+extern "C" {
+
 int qvkv_decode_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *pool,
                           const float *q, uint32_t heads, const uint32_t *pos, uint32_t s,
                           const uint32_t *blocks, uint64_t n_table, const uint32_t *table_at,
@@ -569,6 +654,9 @@ int qvkv_decode_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *po
     if (int rc = qvkv::plan_attention(g, s, heads, max_pos, &p, &why))
         return fail(rc, "shape mismatch in routed moe attention: %s", why);
     if (s == 0) return QVKV_OK;
+    const Segments sg = segments_of(table_at, pos, s);
+    if (int rc = qvkv::check_prefill(g, (uint32_t)sg.n_tok.size(), heads, sg.max_tok, &why))
+        return fail(rc, "shape mismatch in routed moe attention: %s", why);
     // The checks of SimDevice::attention (sim.rs:377-381): every block and sync target
     // inside the pool, every token with a block for each of its positions.
     for (uint64_t i = 0; i < n_table; i++)
@@ -604,6 +692,8 @@ int qvkv_decode_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *po
              vno = st.add(v_new, s * rowb), slo = st.add(slots.data(), s * 4ull),
              qo = st.add(q, qb), po = st.add(pos, s * 4ull), bo = st.add(blocks, n_table * 4),
              tao = st.add(table_at, s * 4ull), oo = st.reserve(qb);
+    StagedSegments ss;
+    ss.add(st, sg);
     if (int rc = st.upload(dev)) return rc;
     hipError_t e = hipSuccess;
     if (n_sync)
@@ -613,10 +703,9 @@ int qvkv_decode_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *po
     e = qvkv::launch_append(g, pool->ptr, held, st.at<float>(dev, kno), st.at<float>(dev, vno),
                             st.at<uint32_t>(dev, slo), s, dev->d_err, dev->stream);
     if (int rc = launched(dev, e, "append launch (new rows)")) return rc;
-    e = qvkv::launch_attention(g, p, pool->ptr, held, st.at<float>(dev, qo),
-                               st.at<uint32_t>(dev, bo), n_table, st.at<uint32_t>(dev, tao),
-                               st.at<uint32_t>(dev, po), s, heads, max_pos,
-                               st.at<float>(dev, oo), dev->ws, dev->d_err, dev->stream);
+    e = attend_tokens(dev, g, p, sg, ss, st, pool->ptr, held, st.at<float>(dev, qo),
+                      st.at<uint32_t>(dev, bo), n_table, st.at<uint32_t>(dev, tao),
+                      st.at<uint32_t>(dev, po), s, heads, max_pos, st.at<float>(dev, oo));
     if (int rc = launched(dev, e, "attention launch")) return rc;
     if (int rc = download(dev, out, st.at<void>(dev, oo), qb)) return rc;
     return finish(dev, dev->stream);
@@ -678,6 +767,9 @@ int qvkv_prelude_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *p
     if (int rc = qvkv::plan_attention(g, s, heads, max_pos, &plan, &why))
         return fail(rc, "shape mismatch in routed moe attention: %s", why);
     if (s == 0) return QVKV_OK;
+    const Segments sg = segments_of(table_at, pos, s);
+    if (int rc = qvkv::check_prefill(g, (uint32_t)sg.n_tok.size(), heads, sg.max_tok, &why))
+        return fail(rc, "shape mismatch in routed moe attention: %s", why);
     for (uint64_t i = 0; i < n_table; i++)
         if (blocks[i] >= held)
             return fail(QVKV_E_SHAPE, "shape mismatch in routed moe attention: a block past the pool's %llu",
@@ -717,6 +809,8 @@ int qvkv_prelude_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *p
                    sto = st.add(sync_to, n_sync * 4ull), slo = st.add(slots.data(), s * 4ull),
                    po = st.add(pos, s * 4ull), bo = st.add(blocks, n_table * 4),
                    tao = st.add(table_at, s * 4ull), oo = st.reserve(qb);
+    StagedSegments ss;
+    ss.add(st, sg);
     if (int rc = st.upload(dev)) return rc;
     qvkv::PreludeArgs a = prelude_args(p);
     a.q_bias = p->q_bias ? st.at<float>(dev, qbo) : nullptr;
@@ -737,9 +831,9 @@ int qvkv_prelude_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *p
     e = qvkv::launch_append(g, pool->ptr, held, dk, dv, st.at<uint32_t>(dev, slo), s, dev->d_err,
                             dev->stream);
     if (int rc = launched(dev, e, "append launch (new rows)")) return rc;
-    e = qvkv::launch_attention(g, plan, pool->ptr, held, dq, st.at<uint32_t>(dev, bo), n_table,
-                               st.at<uint32_t>(dev, tao), st.at<uint32_t>(dev, po), s, heads,
-                               max_pos, st.at<float>(dev, oo), dev->ws, dev->d_err, dev->stream);
+    e = attend_tokens(dev, g, plan, sg, ss, st, pool->ptr, held, dq, st.at<uint32_t>(dev, bo),
+                      n_table, st.at<uint32_t>(dev, tao), st.at<uint32_t>(dev, po), s, heads,
+                      max_pos, st.at<float>(dev, oo));
     if (int rc = launched(dev, e, "attention launch")) return rc;
     if (int rc = download(dev, out, st.at<void>(dev, oo), qb)) return rc;
     if (k_new)

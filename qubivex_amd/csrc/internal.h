@@ -57,6 +57,15 @@ struct AttnPlan {
 };
 int plan_attention(const Geometry &g, uint32_t n_items, uint32_t heads, uint32_t max_pos,
                    AttnPlan *p, const char **why);
+// Paged prefill attention over segments of consecutive tokens (kernels.hip).
+int check_prefill(const Geometry &g, uint32_t n_seg, uint32_t heads, uint32_t max_tok,
+                  const char **why);
+hipError_t launch_prefill(const Geometry &g, const void *pool, uint64_t pool_blocks,
+                          const float *q, const uint32_t *blocks, uint64_t n_table,
+                          const uint32_t *table_at, const uint32_t *pos0, const uint32_t *q_at,
+                          const uint32_t *n_tok, uint32_t n_seg, uint32_t heads,
+                          uint32_t max_pos, uint32_t max_tok, uint64_t q_rows, float *out,
+                          int *err, hipStream_t s);
 hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *pool,
                             uint64_t pool_blocks, const float *q, const uint32_t *blocks,
                             uint64_t n_table, const uint32_t *table_at, const uint32_t *pos,

@@ -477,10 +477,12 @@ struct SoftmaxState {
 // carry the same head (c & 3), and in the P.V step lane c's row holds the scaled
 // probabilities of group 2m + sigma (sigma = (c >> 2) & 1), so one A operand serves two
 // 32-value groups and each lane scales for one group instead of two.
+// n_col: positions this lane's query column sees (causal limit); n_max: the largest n_col
+// of the wave -- rows at or past it may never have been written and are zeroed.
 template <int D, bool Q8, bool PK>
 __device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<D> &st,
-                                             const h4 *qf, uint32_t n, uint32_t qg, bool hi_col,
-                                             uint32_t sigma) {
+                                             const h4 *qf, uint32_t n_col, uint32_t n_max,
+                                             uint32_t qg, bool hi_col, uint32_t sigma) {
     constexpr int NJ = D / 16;
     constexpr int NG = D / 32;
     if (!t.ok) return;
@@ -511,11 +513,11 @@ __device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<
 
     // ---- high + residual columns, mask, online softmax (log2 domain)
     float sc[4];
-    const bool partial = p0 + 16u > n;
+    const bool partial = p0 + 16u > n_max;  // wave-uniform
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         float v2 = s[i] + __shfl_xor(s[i], 8);
-        if (partial && p0 + 4 * qg + i >= n) v2 = -INFINITY;
+        if (p0 + 4 * qg + i >= n_col) v2 = -INFINITY;
         sc[i] = v2;
     }
     float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
@@ -544,7 +546,7 @@ __device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<
         if (partial) {
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                if (p0 + 4 * qg + i >= n)
+                if (p0 + 4 * qg + i >= n_max)
 #pragma unroll
                     for (int x = 0; x < D / 32; x++) vw[i][x] = 0u;
         }
@@ -565,7 +567,7 @@ __device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<
         uint32_t vsw[4][Tile<D, Q8>::VW];  // biased bytes x ^ 0x80
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const bool dead = partial && p0 + 4 * qg + i >= n;
+            const bool dead = partial && p0 + 4 * qg + i >= n_max;
 #pragma unroll
             for (int x = 0; x < Tile<D, Q8>::VW; x++) vsw[i][x] = dead ? 0x80808080u : vw[i][x] ^ 0x80808080u;
         }
@@ -577,7 +579,7 @@ __device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 float x = pr[i] * sc_of_row[i];
-                if (partial && p0 + 4 * qg + i >= n) x = 0.0f;  // a never-written slot's scale
+                if (partial && p0 + 4 * qg + i >= n_max) x = 0.0f;  // a never-written slot's scale
                 const _Float16 u = (_Float16)x;
                 pg[i] = (_Float16)fmaf(-lo_part, (float)u, x);  // u, or the residual x - u
             }
@@ -722,7 +724,7 @@ __device__ __forceinline__ void attn_body(QV_ATTN_PARAMS) {
     for (uint32_t tt = t_begin + w; tt < t_end; tt += 4) {
         Tile<D, Q8> cur;
         load_tile<D, Q8, NT>(cur, tt, pool, pool_blocks, blocks, tab, g, c, qg, geo, err);
-        compute_tile<D, Q8, PK>(cur, st, qf, n, qg, hi_col, sigma);
+        compute_tile<D, Q8, PK>(cur, st, qf, n, n, qg, hi_col, sigma);
     }
     float l = st.l;
     const float m = st.m;
@@ -813,6 +815,126 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ ws
 }
 
 // ---------------------------------------------------------------------------------
+// Paged prefill attention: segment i holds n_tok[i] consecutive tokens of one sequence at
+// positions pos0[i], pos0[i]+1, ... (q / out rows q_at[i] + j); token j attends over
+// positions 0..pos0[i]+j of its table (causal), after all of the segment's rows are stored.
+// Workgroup = (segment, KV head, block of 32 query columns); a query column is one
+// (token, head) pair, column index j * GS + h.  Each wave owns 8 columns (MFMA columns
+// c and c + 8 carry their f16 high parts and residuals, as in decode) and streams every
+// tile up to its last token's position; the 4 waves read the same tiles, so L1/L2 serve
+// the repeats.  Columns see their own causal limit; the wave's outputs need no merge.
+// ---------------------------------------------------------------------------------
+#define QV_PREFILL_PARAMS                                                                       \
+    const uint8_t *__restrict__ pool, uint64_t pool_blocks, const float *__restrict__ q,        \
+        const uint32_t *__restrict__ blocks, uint64_t n_table,                                  \
+        const uint32_t *__restrict__ table_at, const uint32_t *__restrict__ pos0,               \
+        const uint32_t *__restrict__ q_at, const uint32_t *__restrict__ n_tok, uint32_t n_seg,  \
+        uint32_t H, uint32_t max_pos, uint32_t max_tok, uint64_t q_rows, uint32_t n_cb,         \
+        float *__restrict__ out, Geo geo, int *err
+
+template <int D, bool Q8>
+__global__ __launch_bounds__(256) void k_prefill_mfma(QV_PREFILL_PARAMS) {
+    constexpr int NJ = D / 16;
+    const uint32_t G = (uint32_t)geo.G, B = (uint32_t)geo.B;
+    const uint32_t GS = H / G;
+    uint32_t bid = blockIdx.x;
+    if (geo.xcd_map) {  // column blocks of one (segment, KV head) share an XCD's L2
+        const uint32_t nb = gridDim.x, qn = nb / 8, rn = nb % 8;
+        const uint32_t x = bid % 8, i = bid / 8;
+        bid = x < rn ? x * (qn + 1) + i : rn * (qn + 1) + (x - rn) * qn + i;
+    }
+    const uint32_t cb = bid % n_cb;
+    const uint32_t sg = bid / n_cb;
+    const uint32_t g = sg % G;
+    const uint32_t seg = sg / G;
+    if (seg >= n_seg) return;
+    const uint32_t nt = n_tok[seg], p0s = pos0[seg], qa = q_at[seg], tab = table_at[seg];
+    if (nt == 0) return;
+    if (nt > max_tok || (uint64_t)p0s + nt - 1 > max_pos) {
+        if (threadIdx.x == 0 && cb == 0 && g == 0) flag(err, ERR_POS);
+        return;
+    }
+    if ((uint64_t)qa + nt > q_rows) {
+        if (threadIdx.x == 0 && cb == 0 && g == 0) flag(err, ERR_OUT);
+        return;
+    }
+    const uint32_t n_all = p0s + nt;
+    if ((uint64_t)tab + (n_all + B - 1) / B > n_table) {
+        if (threadIdx.x == 0 && cb == 0 && g == 0) flag(err, ERR_TABLE);
+        return;
+    }
+    const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+    const uint32_t c = lane & 15u, qg = lane >> 4;
+    const bool hi_col = c < 8;
+    const uint32_t cc0 = cb * 32u + w * 8u;          // the wave's first column
+    const uint32_t ncols = nt * GS;
+    if (cc0 >= ncols) return;
+    const uint32_t last_tok = min(nt - 1, (cc0 + 7u) / GS);
+    const uint32_t n_max = p0s + last_tok + 1;        // the wave's furthest causal limit
+    const uint32_t cc = cc0 + (c & 7u);
+    const bool valid = cc < ncols;
+    const uint32_t tj = valid ? cc / GS : 0u, hh = valid ? cc % GS : 0u;
+    const uint32_t n_col = valid ? p0s + tj + 1 : n_max;
+
+    h4 qf[NJ];
+    {
+        const float qs = (1.0f / sqrtf((float)D)) * LOG2E_F;
+        const float *qrow = q + ((uint64_t)(qa + tj) * H + (uint64_t)g * GS + hh) * D;
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const int d0 = 32 * (j >> 1) + 8 * (int)qg + 4 * (j & 1);
+            float4 x = valid ? *(const float4 *)(qrow + d0) : make_float4(0.f, 0.f, 0.f, 0.f);
+            qf[j] = h4{split_part(x.x * qs, hi_col), split_part(x.y * qs, hi_col),
+                       split_part(x.z * qs, hi_col), split_part(x.w * qs, hi_col)};
+        }
+    }
+    SoftmaxState<D> st;
+    st.m = -INFINITY;
+    st.l = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) st.acc[j] = f4{0.f, 0.f, 0.f, 0.f};
+    const uint32_t ntiles = (n_max + 15) / 16;
+    for (uint32_t tt = 0; tt < ntiles; tt++) {
+        Tile<D, Q8> cur;
+        load_tile<D, Q8, false>(cur, tt, pool, pool_blocks, blocks, tab, g, c, qg, geo, err);
+        compute_tile<D, Q8, false>(cur, st, qf, n_col, n_max, qg, hi_col, 0u);
+    }
+    // column totals; output rows 4qg + i (qg < 2) after adding the residual rows
+    float l = st.l;
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+#pragma unroll
+    for (int j = 0; j < NJ; j++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) st.acc[j][i] += __shfl_xor(st.acc[j][i], 32);
+    float lr[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) lr[i] = __shfl(l, 4 * (int)(qg & 1u) + i);
+    if (qg >= 2) return;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t ccr = cc0 + 4 * qg + i;
+        if (ccr >= ncols) continue;
+        const uint32_t tr = ccr / GS, hr = ccr % GS;
+        float *orow = out + ((uint64_t)(qa + tr) * H + (uint64_t)g * GS + hr) * D;
+        const float inv = 1.0f / lr[i];
+        if constexpr (!Q8) {
+            float o[NJ];
+#pragma unroll
+            for (int j = 0; j < NJ; j++) o[j] = st.acc[j][i] * inv;
+#pragma unroll
+            for (int j = 0; j < NJ; j += 4)
+                *(float4 *)(orow + c * (D / 16) + j) = make_float4(o[j], o[j + 1], o[j + 2], o[j + 3]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < NJ; j += 2)
+                *(float2 *)(orow + 32 * (j >> 1) + 2 * c) =
+                    make_float2(st.acc[j][i] * inv, st.acc[j + 1][i] * inv);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------
 // Decode attention, generic form (any d that is a multiple of 8 up to 512, any group):
 // one wave per (item, query head); lanes take 64 positions at a time for the scores,
 // then d-columns for P.V.  Used where the MFMA form has no instance.
@@ -843,32 +965,18 @@ __device__ __forceinline__ float wave_sum(float x) {
     return x;
 }
 
+// One wave: query row qrow of KV head g over positions 0..n-1 of table tab -> orow.
 template <bool Q8>
-__global__ __launch_bounds__(64) void k_attn_generic(
-    const uint8_t *__restrict__ pool, uint64_t pool_blocks, const float *__restrict__ q,
-    const uint32_t *__restrict__ blocks, uint64_t n_table, const uint32_t *__restrict__ table_at,
-    const uint32_t *__restrict__ pos, uint32_t n_items, uint32_t H, uint32_t max_pos,
-    float *__restrict__ out, Geo geo, int *err) {
+__device__ __forceinline__ void generic_body(const uint8_t *__restrict__ pool,
+                                             uint64_t pool_blocks,
+                                             const uint32_t *__restrict__ blocks, uint32_t tab,
+                                             uint32_t n, uint32_t g, const float *qrow,
+                                             float *orow, const Geo &geo, int *err) {
     __shared__ float qs[512];
     __shared__ float ps[64];
-    const uint32_t item = blockIdx.x / H, h = blockIdx.x - item * H;
-    if (item >= n_items) return;
-    const uint32_t D = (uint32_t)geo.D, B = (uint32_t)geo.B, G = (uint32_t)geo.G;
-    const uint32_t g = h / (H / G);
+    const uint32_t D = (uint32_t)geo.D, B = (uint32_t)geo.B;
     const uint32_t lane = threadIdx.x;
-    const uint32_t plast = pos[item];
-    if (plast > max_pos) {
-        if (lane == 0) flag(err, ERR_POS);
-        return;
-    }
-    const uint32_t n = plast + 1;
-    const uint32_t tab = table_at[item];
-    if ((uint64_t)tab + (n + B - 1) / B > n_table) {
-        if (lane == 0) flag(err, ERR_TABLE);
-        return;
-    }
     const float scale = (1.0f / sqrtf((float)D)) * LOG2E_F;
-    const float *qrow = q + ((uint64_t)item * H + h) * D;
     for (uint32_t i = lane; i < D; i += 64) qs[i] = qrow[i] * scale;
     __syncthreads();
     float m = -INFINITY, l = 0.0f, acc[8];
@@ -915,12 +1023,64 @@ __global__ __launch_bounds__(64) void k_attn_generic(
         }
         __syncthreads();
     }
-    float *orow = out + ((uint64_t)item * H + h) * D;
 #pragma unroll
     for (int x = 0; x < 8; x++) {
         const uint32_t d = lane + 64u * x;
         if (d < D) orow[d] = acc[x] / l;
     }
+}
+
+template <bool Q8>
+__global__ __launch_bounds__(64) void k_attn_generic(
+    const uint8_t *__restrict__ pool, uint64_t pool_blocks, const float *__restrict__ q,
+    const uint32_t *__restrict__ blocks, uint64_t n_table, const uint32_t *__restrict__ table_at,
+    const uint32_t *__restrict__ pos, uint32_t n_items, uint32_t H, uint32_t max_pos,
+    float *__restrict__ out, Geo geo, int *err) {
+    const uint32_t item = blockIdx.x / H, h = blockIdx.x - item * H;
+    if (item >= n_items) return;
+    const uint32_t B = (uint32_t)geo.B, G = (uint32_t)geo.G, D = (uint32_t)geo.D;
+    const uint32_t plast = pos[item];
+    if (plast > max_pos) {
+        if (threadIdx.x == 0) flag(err, ERR_POS);
+        return;
+    }
+    const uint32_t n = plast + 1;
+    const uint32_t tab = table_at[item];
+    if ((uint64_t)tab + (n + B - 1) / B > n_table) {
+        if (threadIdx.x == 0) flag(err, ERR_TABLE);
+        return;
+    }
+    const uint64_t row = (uint64_t)item * H + h;
+    generic_body<Q8>(pool, pool_blocks, blocks, tab, n, h / (H / G), q + row * D, out + row * D,
+                     geo, err);
+}
+
+// Prefill, generic form: one wave per (segment, token, query head).
+template <bool Q8>
+__global__ __launch_bounds__(64) void k_prefill_generic(QV_PREFILL_PARAMS) {
+    const uint32_t h = blockIdx.x % H;
+    const uint32_t j = (blockIdx.x / H) % max_tok;
+    const uint32_t seg = blockIdx.x / H / max_tok;
+    if (seg >= n_seg) return;
+    const uint32_t B = (uint32_t)geo.B, G = (uint32_t)geo.G, D = (uint32_t)geo.D;
+    const uint32_t nt = n_tok[seg], p0s = pos0[seg], qa = q_at[seg], tab = table_at[seg];
+    if (j >= nt) return;
+    const bool first = threadIdx.x == 0 && j == 0 && h == 0;
+    if (nt > max_tok || (uint64_t)p0s + nt - 1 > max_pos) {
+        if (first) flag(err, ERR_POS);
+        return;
+    }
+    if ((uint64_t)qa + nt > q_rows) {
+        if (first) flag(err, ERR_OUT);
+        return;
+    }
+    if ((uint64_t)tab + (p0s + nt + B - 1) / B > n_table) {
+        if (first) flag(err, ERR_TABLE);
+        return;
+    }
+    const uint64_t row = (uint64_t)(qa + j) * H + h;
+    generic_body<Q8>(pool, pool_blocks, blocks, tab, p0s + j + 1, h / (H / G), q + row * D,
+                     out + row * D, geo, err);
 }
 
 // =================================================================================
@@ -1156,6 +1316,57 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
     if (e != hipSuccess || p.n_chunks == 1) return e;
     hipLaunchKernelGGL(k_attn_merge, dim3(n_items * heads), dim3(g.D), 0, s, (const float *)ws,
                        pos, n_items, heads, max_pos, p.n_chunks, p.tpc, (uint32_t)g.D, out);
+    return hipGetLastError();
+}
+
+int check_prefill(const Geometry &g, uint32_t n_seg, uint32_t heads, uint32_t max_tok,
+                  const char **why) {
+    if (heads == 0 || heads % (uint32_t)g.G != 0) {
+        *why = "query heads must be a positive multiple of kv_heads";
+        return QVKV_E_SHAPE;
+    }
+    const bool mfma = g.D == 64 || g.D == 128 || g.D == 256;
+    const uint64_t cols = (uint64_t)max_tok * (heads / (uint32_t)g.G);
+    const uint64_t grid = mfma ? (uint64_t)n_seg * g.G * ((cols + 31) / 32)
+                               : (uint64_t)n_seg * max_tok * heads;
+    if (grid > 0x7fffffffull) {
+        *why = "batch too large";
+        return QVKV_E_SHAPE;
+    }
+    return QVKV_OK;
+}
+
+hipError_t launch_prefill(const Geometry &g, const void *pool, uint64_t pool_blocks,
+                          const float *q, const uint32_t *blocks, uint64_t n_table,
+                          const uint32_t *table_at, const uint32_t *pos0, const uint32_t *q_at,
+                          const uint32_t *n_tok, uint32_t n_seg, uint32_t heads,
+                          uint32_t max_pos, uint32_t max_tok, uint64_t q_rows, float *out,
+                          int *err, hipStream_t s) {
+    if (n_seg == 0 || max_tok == 0) return hipSuccess;
+    const Geo geo = to_geo(g);
+    const uint8_t *pp = (const uint8_t *)pool;
+    const bool q8 = g.dtype == QVKV_Q8_0;
+    if (!(g.D == 64 || g.D == 128 || g.D == 256)) {
+        const unsigned grid = (unsigned)((uint64_t)n_seg * max_tok * heads);
+#define QV_PG(QQ)                                                                              \
+    hipLaunchKernelGGL(k_prefill_generic<QQ>, dim3(grid), dim3(64), 0, s, pp, pool_blocks, q,   \
+                       blocks, n_table, table_at, pos0, q_at, n_tok, n_seg, heads, max_pos,    \
+                       max_tok, q_rows, 0u, out, geo, err)
+        if (q8) QV_PG(true); else QV_PG(false);
+#undef QV_PG
+        return hipGetLastError();
+    }
+    const uint32_t GS = heads / (uint32_t)g.G;
+    const uint32_t n_cb = (uint32_t)(((uint64_t)max_tok * GS + 31) / 32);
+    const unsigned grid = (unsigned)((uint64_t)n_seg * g.G * n_cb);
+#define QV_PF(DD, QQ)                                                                          \
+    hipLaunchKernelGGL((k_prefill_mfma<DD, QQ>), dim3(grid), dim3(256), 0, s, pp, pool_blocks,  \
+                       q, blocks, n_table, table_at, pos0, q_at, n_tok, n_seg, heads, max_pos, \
+                       max_tok, q_rows, n_cb, out, geo, err)
+    if (g.D == 64) { if (q8) QV_PF(64, true); else QV_PF(64, false); }
+    else if (g.D == 128) { if (q8) QV_PF(128, true); else QV_PF(128, false); }
+    else { if (q8) QV_PF(256, true); else QV_PF(256, false); }
+#undef QV_PF
     return hipGetLastError();
 }
 

@@ -181,6 +181,16 @@ class HipDevice:
                                        _ptr(table_at), _ptr(pos), pos.numel(), heads, max_pos,
                                        _ptr(out), _stream(stream)))
 
+    def prefill_attention(self, layout: KvLayout, pool, pool_blocks, q, blocks, table_at, pos0,
+                          q_at, n_tok, heads, max_pos, max_tok, out, stream=None):
+        """Causal attention of segments of consecutive stored tokens (device tensors):
+        token j of segment i is q/out row q_at[i] + j at position pos0[i] + j."""
+        q_rows = q.numel() // (heads * layout.head_dim)
+        check(lib.qvkv_prefill_attention_async(
+            self.handle, ctypes.byref(layout.c), _ptr(pool), pool_blocks, _ptr(q), q_rows,
+            _ptr(blocks), blocks.numel(), _ptr(table_at), _ptr(pos0), _ptr(q_at), _ptr(n_tok),
+            n_tok.numel(), heads, max_pos, max_tok, _ptr(out), _stream(stream)))
+
     def block_copy(self, layout: KvLayout, pool, pool_blocks, src, dst, stream=None):
         check(lib.qvkv_block_copy_async(self.handle, ctypes.byref(layout.c), _ptr(pool),
                                         pool_blocks, _ptr(src), _ptr(dst), src.numel(),

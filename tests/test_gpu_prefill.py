@@ -1,0 +1,172 @@
+"""Paged prefill attention (qvkv_prefill_attention_async) against the oracle: every token
+of a segment attends causally over positions 0..pos0+j of its sequence, as the
+reference's host prefill runs math::attend per (token, head) after storing the segment
+(crates/qubivex-arch/src/lib.rs:1296-1320).  The oracle expands each segment into one
+decode item per token."""
+import numpy as np
+import pytest
+
+import oracle
+from helpers import F16, MAX_ABS, Q8_0, REL_L2, attn_errors, normal, rng, slots_of
+from test_gpu_kernels import cf32, cu32, fill_items, layout, new_pool
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+
+def expand(table_at, lens, n_tok, q_at):
+    """Per-token (table_at, pos, q row) of the segments; sequence i ends at lens[i]."""
+    ta, pos, rows = [], [], []
+    for i, (n, m) in enumerate(zip(lens, n_tok)):
+        for j in range(m):
+            ta.append(table_at[i])
+            pos.append(n - m + j)
+            rows.append(q_at[i] + j)
+    return (np.array(ta, np.uint32), np.array(pos, np.uint32), np.array(rows, np.int64))
+
+
+PREFILL_CASES = [
+    # dtype, H, G, D, [(sequence length after the segment, tokens in the segment)]
+    (F16, 32, 8, 128, [(512, 512), (300, 37), (17, 1), (1000, 130)]),  # 4 heads per KV head
+    (F16, 32, 4, 128, [(64, 64), (2000, 33), (16, 16)]),  # 8 per KV head
+    (F16, 8, 8, 128, [(100, 100), (45, 9)]),  # 1 per KV head: 8 tokens per wave
+    (F16, 16, 1, 128, [(90, 90)]),  # 16 per KV head
+    (F16, 8, 2, 64, [(200, 200), (77, 5)]),
+    (F16, 12, 4, 128, [(50, 50), (81, 3)]),  # 3 per KV head: waves straddle tokens
+    (F16, 4, 2, 256, [(300, 40)]),
+    (F16, 4, 4, 96, [(60, 60), (129, 7)]),  # generic kernel
+    (Q8_0, 32, 8, 128, [(256, 256), (700, 45)]),
+    (Q8_0, 32, 4, 128, [(300, 300), (33, 2)]),
+    (Q8_0, 8, 2, 64, [(130, 66)]),
+    (Q8_0, 4, 2, 256, [(90, 20)]),
+    (Q8_0, 6, 3, 160, [(70, 12)]),  # generic kernel
+]
+
+
+@pytest.mark.parametrize("dtype,H,G,D,segs", PREFILL_CASES)
+def test_prefill_within_tolerance(hip, dtype, H, G, D, segs):
+    print(f"prefill {dtype} H={H} G={G} D={D} segs={segs}", flush=True)
+    r = rng(900 + H * G + D + len(segs))
+    L = layout(dtype, G, D)
+    lens = [n for n, _ in segs]
+    n_tok = np.array([m for _, m in segs], np.uint32)
+    N = sum((n + 15) // 16 for n in lens) + 5
+    pool = new_pool(L, N, fill=9)
+    blocks, table_at, sim = fill_items(hip, L, pool, N, lens, r,
+                                       outliers=0.01 if dtype == Q8_0 else 0)
+    # segments' q rows in reverse order: q_at is an indirection, not the segment index
+    T = int(n_tok.sum())
+    q_at = np.zeros(len(segs), np.uint32)
+    at = 0
+    for i in reversed(range(len(segs))):
+        q_at[i] = at
+        at += int(n_tok[i])
+    pos0 = (np.array(lens, np.uint32) - n_tok).astype(np.uint32)
+    q = normal(r, (T, H, D))
+    out = torch.full((T * H * D,), float("nan"), dtype=torch.float32, device="cuda")
+    max_pos = int(max(lens)) - 1
+    hip.prefill_attention(L, pool, N, cf32(q), cu32(blocks), cu32(table_at), cu32(pos0),
+                          cu32(q_at), cu32(n_tok), H, max_pos, int(n_tok.max()), out)
+    hip.check()
+    got = out.cpu().numpy().reshape(T, H, D)
+    ta, pos, rows = expand(table_at, lens, n_tok, q_at)
+    want = sim.attention(q[rows], H, blocks, ta, pos)
+    max_abs, rel = attn_errors(got[rows], want)
+    print(f"  max_abs={max_abs:.2e} rel_l2={rel:.2e}", flush=True)
+    assert np.isfinite(got).all()
+    assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)
+
+
+def test_prefill_equals_decode_kernel_per_token(hip):
+    """The prefill kernel and the decode kernel (one item per token) agree to float
+    rounding on the same pool: the same tiles, scores and softmax, another order."""
+    r = rng(31)
+    L = layout(F16, 8, 128)
+    H = 32
+    lens, n_tok = [700], np.array([200], np.uint32)
+    N = 50
+    pool = new_pool(L, N)
+    blocks, table_at, _ = fill_items(hip, L, pool, N, lens, r)
+    q = normal(r, (200, H, 128))
+    pos0 = np.array([500], np.uint32)
+    a = torch.zeros(200 * H * 128, dtype=torch.float32, device="cuda")
+    b = torch.zeros_like(a)
+    hip.prefill_attention(L, pool, N, cf32(q), cu32(blocks), cu32(table_at), cu32(pos0),
+                          cu32(np.zeros(1, np.uint32)), cu32(n_tok), H, 699, 200, a)
+    pos = np.arange(500, 700, dtype=np.uint32)
+    hip.attention(L, pool, N, cf32(q), cu32(blocks), cu32(np.zeros(200, np.uint32)), cu32(pos),
+                  H, 699, b)
+    hip.check()
+    d = (a - b).abs().max().item()
+    assert d < 1e-5, d
+
+
+def test_prefill_rejects_out_of_range_segments(hip):
+    """A segment past max_pos, past max_tok, past q_rows or past its table is a ShapeError
+    and the kernel touches nothing."""
+    from qubivex_amd import ShapeError
+
+    r = rng(32)
+    L = layout(F16, 2, 64)
+    N = 8
+    pool = new_pool(L, N)
+    blocks, table_at, _ = fill_items(hip, L, pool, N, [40], r)
+    q = cf32(normal(r, (10, 4, 64)))
+    out = torch.zeros(10 * 4 * 64, dtype=torch.float32, device="cuda")
+    args = dict(blocks=cu32(blocks), table_at=cu32(table_at))
+    bad = [
+        (np.array([35], np.uint32), np.array([0], np.uint32), np.array([10], np.uint32), 40, 10),  # max_pos
+        (np.array([30], np.uint32), np.array([0], np.uint32), np.array([10], np.uint32), 39, 5),  # max_tok
+        (np.array([30], np.uint32), np.array([5], np.uint32), np.array([10], np.uint32), 39, 10),  # q rows
+        (np.array([40], np.uint32), np.array([0], np.uint32), np.array([10], np.uint32), 60, 10),  # table
+    ]
+    for pos0, q_at, n_tok, max_pos, max_tok in bad:
+        hip.prefill_attention(L, pool, N, q, args["blocks"], args["table_at"], cu32(pos0),
+                              cu32(q_at), cu32(n_tok), 4, max_pos, max_tok, out)
+        with pytest.raises(ShapeError):
+            hip.check()
+    assert float(out.abs().sum()) == 0.0
+
+
+def test_host_entry_routes_a_prefill_chunk_through_segments(hip):
+    """qvkv_decode_attention with a prompt chunk of one sequence, a decode token of
+    another and a second chunk: the runs become prefill segments; the results are those
+    of attending each token on its own."""
+    from qubivex_amd import KvLayout
+
+    r = rng(33)
+    L = KvLayout(F16, 4, 128, 16)
+    H = 16
+    N = 60
+    buf = hip.alloc(N * L.block_bytes)
+    # sequence 0: positions 0..39 new; sequence 1: 1 new token at 300; sequence 2: 100..119
+    lens = [40, 301, 120]
+    blocks = r.permutation(N).astype(np.uint32)[:sum((n + 15) // 16 for n in lens)]
+    need = [(n + 15) // 16 for n in lens]
+    table_at_seq = np.concatenate([[0], np.cumsum(need)[:-1]]).astype(np.uint32)
+    toks = [(0, p) for p in range(40)] + [(1, 300)] + [(2, p) for p in range(100, 120)]
+    s = len(toks)
+    pos = np.array([p for _, p in toks], np.uint32)
+    table_at = np.array([table_at_seq[i] for i, _ in toks], np.uint32)
+    # host rows of everything before the new tokens: synced now
+    sync_rows, sync_to = [], []
+    for i, first_new in ((1, 300), (2, 100)):
+        for j in range(first_new):
+            sync_rows.append(normal(r, (2 * L.kv_out,)))
+            sync_to.append(int(slots_of(blocks, table_at_seq, i, [j], 16)[0]))
+    sync = np.concatenate(sync_rows)
+    sync_to = np.array(sync_to, np.uint32)
+    k_new = normal(r, (s, L.kv_out))
+    v_new = normal(r, (s, L.kv_out))
+    q = normal(r, (s, H, 128))
+    got = hip.decode_attention(L, buf, q, H, pos, blocks, table_at, sync, sync_to, k_new, v_new)
+    sim = oracle.SimPool(N, 4, 128, 16, oracle.F16)
+    sr = sync.reshape(-1, 2 * L.kv_out)
+    sim.store(sr[:, :L.kv_out], sr[:, L.kv_out:], sync_to)
+    new_slots = np.array([slots_of(blocks, table_at_seq, i, [p], 16)[0] for i, p in toks], np.uint32)
+    sim.store(k_new, v_new, new_slots)
+    want = sim.attention(q, H, blocks, table_at, pos)
+    max_abs, rel = attn_errors(got, want)
+    print(f"  max_abs={max_abs:.2e} rel_l2={rel:.2e}", flush=True)
+    assert max_abs <= MAX_ABS and rel <= REL_L2
+    buf.close()
