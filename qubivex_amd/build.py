@@ -15,7 +15,11 @@ OUT_DIR = os.path.join(HERE, "lib")
 LIB = os.path.join(OUT_DIR, "libqvkv.so")
 ARCH = os.environ.get("QVKV_ARCH", "gfx950")
 
-HIP_SOURCES = ["kernels.hip", "prelude.hip", "abi.hip"]
+HIP_SOURCES = ["kernels.hip", "prefill.hip", "prelude.hip", "abi.hip"]
+# Per-file code generation: the prefill kernels keep MFMA accumulators in VGPRs (their
+# online-softmax rescale and P split are VALU work on them); decode attention is faster
+# with the compiler's default (accumulators in AGPRs).
+HIP_FLAGS = {"prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 CXX_SOURCES = ["pool.cpp", "prefix.cpp"]
 
 
@@ -37,6 +41,7 @@ def build(verbose: bool = False, jobs: int = 4) -> str:
         objs.append(obj)
         cmd = ["hipcc", f"--offload-arch={ARCH}", "-c", *common, *inc,
                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+               *HIP_FLAGS.get(src, []), *os.environ.get("QVKV_EXTRA_HIPFLAGS", "").split(),
                "-fno-gpu-rdc", os.path.join(CSRC, src), "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)

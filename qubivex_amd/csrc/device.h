@@ -1,0 +1,427 @@
+// Device-side helpers shared by the kernel translation units (kernels.hip, prefill.hip):
+// kernel-side geometry, error flags, q8_0 byte permutations, the decode attention
+// tile (load, MFMA scores, online softmax, P.V) and the generic per-head attention.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+
+#include "internal.h"
+
+namespace qvkv {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+
+enum : int { ERR_BLOCK = 1, ERR_TABLE = 2, ERR_POS = 4, ERR_OUT = 8 };
+
+struct Geo {  // kernel-side copy of Geometry
+    int dtype, G, D, B;
+    uint32_t kv_out;
+    uint64_t bb, k_off, ks_off, v_off, vs_off;
+    uint32_t xcd_map;  // attention: XCD-aware workgroup order
+};
+
+inline Geo to_geo(const Geometry &g) {
+    return Geo{g.dtype, g.G, g.D, g.B, (uint32_t)g.kv_out, g.block_bytes,
+               g.k_off, g.ks_off, g.v_off, g.vs_off, (uint32_t)tune("QVKV_ATTN_XCD", 1)};
+}
+
+__device__ __forceinline__ void flag(int *err, int bit) { atomicOr(err, bit); }
+
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+    h2 v = {(_Float16)a, (_Float16)b};  // v_cvt_f16_f32: IEEE round to nearest even
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// Position of logical value d inside a stored q8_0 row.
+__device__ __forceinline__ uint32_t kperm(uint32_t d, uint32_t D) {
+    return ((d & 31u) >> 3) * (D >> 2) + (d >> 5) * 8u + (d & 7u);
+}
+__device__ __forceinline__ uint32_t vperm(uint32_t d, uint32_t D) {
+    return ((d & 31u) >> 1) * (D >> 4) + 2u * (d >> 5) + (d & 1u);
+}
+
+// ---------------------------------------------------------------------------------
+// The 16-position attention tile (v_mfma_f32_16x16x16_f16) of decode attention and of
+// the q8_0 / d=256 prefill: loading from the pool, scores, online softmax, P.V.
+// Lane l: c = l % 16 (MFMA column / K row), q = l / 16.
+// ---------------------------------------------------------------------------------
+constexpr float LOG2E_F = 1.4426950408889634f;
+
+__device__ __forceinline__ h4 h4_of(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(h4, make_uint2(a, b));
+}
+
+// 4 int8 (one word) -> 4 f16, exactly: (0x6400 | (x ^ 0x80)) is 1024 + x + 128 in f16.
+__device__ __forceinline__ h4 i8x4_to_h4(uint32_t w) {
+    const uint32_t u = w ^ 0x80808080u;
+    const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const h2 a = __builtin_bit_cast(h2, lo) - bias;
+    const h2 b = __builtin_bit_cast(h2, hi) - bias;
+    return h4{a.x, a.y, b.x, b.y};
+}
+
+// f32 -> (high f16, residual f16); lane columns < 8 take the high part.
+// f32 product rounded once to f32, never fused into a later f16 conversion: the high
+// part and the residual of a split must both come from this one rounded value.  hipcc
+// contracts by default and may fuse the product into a v_fma_mix_f16 for one use (one
+// rounding) but not the other, and then high + residual misses the product by one f16
+// ulp of the high part wherever the two roundings disagree.
+__device__ __forceinline__ float mul_rn(float a, float b) {
+    float y = a * b;
+    asm volatile("" : "+v"(y));  // the rounded f32 value, opaque to later fusion
+    return y;
+}
+
+__device__ __forceinline__ _Float16 split_part(float x, bool hi_part) {
+    const _Float16 hi = (_Float16)x;
+    const _Float16 lo = (_Float16)(x - (float)hi);
+    return hi_part ? hi : lo;
+}
+
+typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+
+// NB bytes (4, 8 or a multiple of 16) into words; NT: non-temporal (streamed once).
+template <int NB, bool NT>
+__device__ __forceinline__ void load_bytes(const uint8_t *p, uint32_t *w) {
+    if constexpr (NB == 4) {
+        w[0] = NT ? __builtin_nontemporal_load((const uint32_t *)p) : *(const uint32_t *)p;
+    } else if constexpr (NB == 8) {
+        const u2v x = NT ? __builtin_nontemporal_load((const u2v *)p) : *(const u2v *)p;
+        w[0] = x.x; w[1] = x.y;
+    } else {
+#pragma unroll
+        for (int i = 0; i < NB / 16; i++) {
+            const u4v x = NT ? __builtin_nontemporal_load((const u4v *)(p + 16 * i))
+                             : *(const u4v *)(p + 16 * i);
+            w[4 * i] = x.x; w[4 * i + 1] = x.y; w[4 * i + 2] = x.z; w[4 * i + 3] = x.w;
+        }
+    }
+}
+
+template <int NB>
+__device__ __forceinline__ void load_bytes(const uint8_t *p, uint32_t *w) {
+    load_bytes<NB, false>(p, w);
+}
+
+// f16 number idx of a packed word array, as f32 (idx is a compile-time constant).
+__device__ __forceinline__ float half_at(const uint32_t *w, int idx) {
+    const uint32_t x = w[idx >> 1];
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)((idx & 1) ? (x >> 16) : (x & 0xffffu)));
+}
+
+// One 16-position tile's operands for one lane, as loaded from the pool.
+template <int D, bool Q8>
+struct Tile {
+    static constexpr int KW = Q8 ? D / 16 : D / 8;                    // key words
+    static constexpr int VW = Q8 ? (D / 64 > 0 ? D / 64 : 1) : D / 32;  // value words per row
+    static constexpr int SW = Q8 ? 2 * (D / 32) : 1;                  // scale words (4 rows)
+    uint32_t k[KW];
+    uint32_t v[4][VW];
+    uint32_t ks[SW], vs[SW];
+    uint32_t p0;
+    bool ok;
+};
+
+template <int D, bool Q8, bool NT>
+__device__ __forceinline__ void load_tile(Tile<D, Q8> &t, uint32_t tt, const uint8_t *pool,
+                                          uint64_t pool_blocks, const uint32_t *blocks,
+                                          uint32_t tab, uint32_t g, uint32_t c, uint32_t qg,
+                                          const Geo &geo, int *err) {
+    const uint32_t B = (uint32_t)geo.B;
+    t.p0 = tt * 16u;
+    const uint32_t blk = blocks[tab + t.p0 / B];
+    t.ok = blk < pool_blocks;
+    if (!t.ok) {
+        if ((threadIdx.x & 63u) == 0) flag(err, ERR_BLOCK);
+        return;
+    }
+    const uint8_t *base = pool + (uint64_t)blk * geo.bb;
+    const uint64_t rows = (uint64_t)g * B + t.p0 % B;  // first (head, position) row of the tile
+    if constexpr (!Q8) {
+        // K row c: 16-byte pieces at d = 32i + 8qg; V rows 4qg..4qg+3 at d = c*D/16
+        const uint8_t *kr = base + geo.k_off + ((rows + c) * D + 8 * qg) * 2u;
+#pragma unroll
+        for (int i = 0; i < D / 32; i++) load_bytes<16, NT>(kr + 64u * i, t.k + 4 * i);
+        const uint8_t *vr = base + geo.v_off + ((rows + 4 * qg) * D + c * (D / 16)) * 2u;
+#pragma unroll
+        for (int i = 0; i < 4; i++) load_bytes<D / 8, NT>(vr + (uint64_t)i * D * 2u, t.v[i]);
+    } else {
+        load_bytes<D / 4, NT>(base + geo.k_off + (rows + c) * D + qg * (D / 4), t.k);
+        load_bytes<8 * (D / 32), NT>(base + geo.ks_off + (rows + 4 * qg) * (D / 32) * 2u, t.ks);
+        load_bytes<8 * (D / 32), NT>(base + geo.vs_off + (rows + 4 * qg) * (D / 32) * 2u, t.vs);
+        const uint8_t *vr = base + geo.v_off + (rows + 4 * qg) * D + c * (D / 16);
+#pragma unroll
+        for (int i = 0; i < 4; i++) load_bytes<D / 16, NT>(vr + (uint64_t)i * D, t.v[i]);
+    }
+}
+
+// Online-softmax state of one lane: running max and partial sum (head c % 8), and the
+// output accumulator (rows 4qg..4qg+3 of the MFMA tile, columns by d mapping).
+template <int D>
+struct SoftmaxState {
+    float m, l;
+    f4 acc[D / 16];
+};
+
+// PK ("packed", q8_0 with at most 4 query heads per KV head): MFMA columns c and c^4
+// carry the same head (c & 3), and in the P.V step lane c's row holds the scaled
+// probabilities of group 2m + sigma (sigma = (c >> 2) & 1), so one A operand serves two
+// 32-value groups and each lane scales for one group instead of two.
+// n_col: positions this lane's query column sees (causal limit); n_max: the largest n_col
+// of the wave -- rows at or past it may never have been written and are zeroed.
+template <int D, bool Q8, bool PK>
+__device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<D> &st,
+                                             const h4 *qf, uint32_t n_col, uint32_t n_max,
+                                             uint32_t qg, bool hi_col, uint32_t sigma) {
+    constexpr int NJ = D / 16;
+    constexpr int NG = D / 32;
+    if (!t.ok) return;
+    const uint32_t p0 = t.p0;
+    // ---- scores S^T[position][column] = K . Q^T
+    f4 s = f4{0.f, 0.f, 0.f, 0.f};
+    uint32_t vw[4][Tile<D, Q8>::VW];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int x = 0; x < Tile<D, Q8>::VW; x++) vw[i][x] = t.v[i][x];
+    if constexpr (!Q8) {
+#pragma unroll
+        for (int i = 0; i < NG; i++) {
+            s = __builtin_amdgcn_mfma_f32_16x16x16f16(h4_of(t.k[4 * i], t.k[4 * i + 1]), qf[2 * i], s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_16x16x16f16(h4_of(t.k[4 * i + 2], t.k[4 * i + 3]), qf[2 * i + 1], s, 0, 0, 0);
+        }
+    } else {
+#pragma unroll
+        for (int gi = 0; gi < NG; gi++) {
+            f4 sg = f4{0.f, 0.f, 0.f, 0.f};
+            sg = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4(t.k[2 * gi]), qf[2 * gi], sg, 0, 0, 0);
+            sg = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4(t.k[2 * gi + 1]), qf[2 * gi + 1], sg, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) s[i] = fmaf(sg[i], half_at(t.ks, i * NG + gi), s[i]);
+        }
+    }
+
+    // ---- high + residual columns, mask, online softmax (log2 domain)
+    float sc[4];
+    const bool partial = p0 + 16u > n_max;  // wave-uniform
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float v2 = s[i] + __shfl_xor(s[i], 8);
+        if (p0 + 4 * qg + i >= n_col) v2 = -INFINITY;
+        sc[i] = v2;
+    }
+    float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float mnew = fmaxf(st.m, tmax);
+    const float msafe = mnew == -INFINITY ? 0.0f : mnew;
+    const float alpha = __builtin_amdgcn_exp2f(st.m - msafe);
+    float pr[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) pr[i] = __builtin_amdgcn_exp2f(sc[i] - msafe);
+    st.l = st.l * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
+    if (__any(mnew > st.m)) {
+        float ar[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) ar[i] = __shfl(alpha, 4 * qg + i);
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) st.acc[j][i] *= ar[i];
+    }
+    st.m = mnew;
+
+    // ---- O += P . V
+    if constexpr (!Q8) {
+        if (partial) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (p0 + 4 * qg + i >= n_max)
+#pragma unroll
+                    for (int x = 0; x < D / 32; x++) vw[i][x] = 0u;
+        }
+        const h4 pa = h4{split_part(pr[0], hi_col), split_part(pr[1], hi_col),
+                         split_part(pr[2], hi_col), split_part(pr[3], hi_col)};
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+            const uint32_t w0 = __builtin_amdgcn_perm(vw[1][j >> 1], vw[0][j >> 1], sel);
+            const uint32_t w1 = __builtin_amdgcn_perm(vw[3][j >> 1], vw[2][j >> 1], sel);
+            st.acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, h4_of(w0, w1), st.acc[j], 0, 0, 0);
+        }
+    } else {
+        // V operand of MFMA j (group j/2): rows 4qg..4qg+3 at byte j of each row's run,
+        // int8 exactly as f16.  The rows' scales of group j/2 fold into the probabilities
+        // (P' = p * scale in f32, then f16 high part + residual: exact to ~2^-22), so the
+        // products the MFMA forms are exact.
+        uint32_t vsw[4][Tile<D, Q8>::VW];  // biased bytes x ^ 0x80
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const bool dead = partial && p0 + 4 * qg + i >= n_max;
+#pragma unroll
+            for (int x = 0; x < Tile<D, Q8>::VW; x++) vsw[i][x] = dead ? 0x80808080u : vw[i][x] ^ 0x80808080u;
+        }
+        const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+        const float lo_part = hi_col ? 0.0f : 1.0f;
+        // The A operand of scaled probabilities for group g (this lane's scale pick).
+        auto scaled = [&](float sc_of_row[4]) {
+            _Float16 pg[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float x = mul_rn(pr[i], sc_of_row[i]);
+                if (partial && p0 + 4 * qg + i >= n_max) x = 0.0f;  // a never-written slot's scale
+                const _Float16 u = (_Float16)x;
+                pg[i] = (_Float16)fmaf(-lo_part, (float)u, x);  // u, or the residual x - u
+            }
+            return h4{pg[0], pg[1], pg[2], pg[3]};
+        };
+        // P'.V for the two MFMAs of group gi (bytes 2gi, 2gi+1 of each row's run).
+        auto pv_group = [&](const h4 &pa, int gi) {
+            const int j = 2 * gi;
+            const uint32_t b = (uint32_t)(j & 3);
+            const uint32_t sel = ((4u + b + 1) << 24) | ((b + 1) << 16) | ((4u + b) << 8) | b;
+            const uint32_t t01 = __builtin_amdgcn_perm(vsw[1][j >> 2], vsw[0][j >> 2], sel);
+            const uint32_t t23 = __builtin_amdgcn_perm(vsw[3][j >> 2], vsw[2][j >> 2], sel);
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const uint32_t spread = u ? 0x04030402u : 0x04010400u;
+                const h2 x01 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, t01, spread)) - bias;
+                const h2 x23 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, t23, spread)) - bias;
+                st.acc[j + u] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, h4{x01.x, x01.y, x23.x, x23.y},
+                                                                      st.acc[j + u], 0, 0, 0);
+            }
+        };
+        if constexpr (PK) {
+            // Groups 2m and 2m+1 share one A operand: the scales of row i are the low and
+            // high f16 of word i*NG/2 + m (row-major [row][group] f16 scales).
+#pragma unroll
+            for (int m = 0; m < NG / 2; m++) {
+                float sc[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t w = t.vs[(i * NG) / 2 + m] >> (16u * sigma);
+                    sc[i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+                }
+                const h4 pa = scaled(sc);
+                pv_group(pa, 2 * m);
+                pv_group(pa, 2 * m + 1);
+            }
+        } else {
+#pragma unroll
+            for (int gi = 0; gi < NG; gi++) {
+                float sc[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) sc[i] = half_at(t.vs, i * NG + gi);
+                pv_group(scaled(sc), gi);
+            }
+        }
+    }
+}
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+// ---------------------------------------------------------------------------------
+// Decode attention, generic form (any d that is a multiple of 8 up to 512, any group):
+// one wave per (item, query head); lanes take 64 positions at a time for the scores,
+// then d-columns for P.V.  Used where the MFMA form has no instance.
+// ---------------------------------------------------------------------------------
+template <bool Q8>
+__device__ __forceinline__ float kv_elem(const uint8_t *base, const Geo &geo, bool isv,
+                                         uint64_t row, uint32_t d) {
+    const uint32_t D = (uint32_t)geo.D;
+    if constexpr (!Q8) {
+        return (float)((const _Float16 *)(base + (isv ? geo.v_off : geo.k_off)))[row * D + d];
+    } else {
+        const int8_t qv = (int8_t)base[(isv ? geo.v_off : geo.k_off) + row * D +
+                                       (isv ? vperm(d, D) : kperm(d, D))];
+        const float sc = (float)((const _Float16 *)(base + (isv ? geo.vs_off : geo.ks_off)))
+            [row * (D >> 5) + (d >> 5)];
+        return (float)qv * sc;
+    }
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+    return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+    return x;
+}
+
+// One wave: query row qrow of KV head g over positions 0..n-1 of table tab -> orow.
+template <bool Q8>
+__device__ __forceinline__ void generic_body(const uint8_t *__restrict__ pool,
+                                             uint64_t pool_blocks,
+                                             const uint32_t *__restrict__ blocks, uint32_t tab,
+                                             uint32_t n, uint32_t g, const float *qrow,
+                                             float *orow, const Geo &geo, int *err) {
+    __shared__ float qs[512];
+    __shared__ float ps[64];
+    const uint32_t D = (uint32_t)geo.D, B = (uint32_t)geo.B;
+    const uint32_t lane = threadIdx.x;
+    const float scale = (1.0f / sqrtf((float)D)) * LOG2E_F;
+    for (uint32_t i = lane; i < D; i += 64) qs[i] = qrow[i] * scale;
+    __syncthreads();
+    float m = -INFINITY, l = 0.0f, acc[8];
+#pragma unroll
+    for (int x = 0; x < 8; x++) acc[x] = 0.0f;
+    for (uint32_t b0 = 0; b0 < n; b0 += 64) {
+        const uint32_t p = b0 + lane;
+        float s = -INFINITY;
+        if (p < n) {
+            const uint32_t blk = blocks[tab + p / B];
+            if (blk < pool_blocks) {
+                const uint8_t *base = pool + (uint64_t)blk * geo.bb;
+                const uint64_t row = (uint64_t)g * B + p % B;
+                float t = 0.0f;
+                for (uint32_t d = 0; d < D; d++) t = fmaf(qs[d], kv_elem<Q8>(base, geo, false, row, d), t);
+                s = t;
+            } else {
+                flag(err, ERR_BLOCK);
+            }
+        }
+        const float mnew = fmaxf(m, wave_max(s));
+        const float msafe = mnew == -INFINITY ? 0.0f : mnew;
+        const float alpha = __builtin_amdgcn_exp2f(m - msafe);
+        const float e = p < n ? __builtin_amdgcn_exp2f(s - msafe) : 0.0f;
+        l = l * alpha + wave_sum(e);
+#pragma unroll
+        for (int x = 0; x < 8; x++) acc[x] *= alpha;
+        m = mnew;
+        ps[lane] = e;
+        __syncthreads();
+        const uint32_t cnt = min(64u, n - b0);
+        for (uint32_t pp = 0; pp < cnt; pp++) {
+            const uint32_t p2 = b0 + pp;
+            const uint32_t blk = blocks[tab + p2 / B];
+            if (blk >= pool_blocks) continue;
+            const uint8_t *base = pool + (uint64_t)blk * geo.bb;
+            const uint64_t row = (uint64_t)g * B + p2 % B;
+            const float wgt = ps[pp];
+#pragma unroll
+            for (int x = 0; x < 8; x++) {
+                const uint32_t d = lane + 64u * x;
+                if (d < D) acc[x] = fmaf(wgt, kv_elem<Q8>(base, geo, true, row, d), acc[x]);
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int x = 0; x < 8; x++) {
+        const uint32_t d = lane + 64u * x;
+        if (d < D) orow[d] = acc[x] / l;
+    }
+}
+
+}  // namespace qvkv

@@ -57,6 +57,9 @@ struct AttnPlan {
 };
 int plan_attention(const Geometry &g, uint32_t n_items, uint32_t heads, uint32_t max_pos,
                    AttnPlan *p, const char **why);
+// Launch-shape knob: the default, or an environment variable of the same name (kernels.hip).
+int tune(const char *name, int def);
+
 // Paged prefill attention over segments of consecutive tokens (kernels.hip).
 int check_prefill(const Geometry &g, uint32_t n_seg, uint32_t heads, uint32_t max_tok,
                   const char **why);

@@ -19,49 +19,9 @@
 // probabilities (again high part + residual) against the V tile.  Accumulation is f32.
 // The score tile produced by the first MFMA is, lane for lane, the A operand of the
 // second, so probabilities never leave registers.
-#include <hip/hip_runtime.h>
-#include <math.h>
-#include <stdint.h>
-#include <stdlib.h>
-
-#include "internal.h"
+#include "device.h"
 
 namespace qvkv {
-
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-typedef float f4 __attribute__((ext_vector_type(4)));
-
-enum : int { ERR_BLOCK = 1, ERR_TABLE = 2, ERR_POS = 4, ERR_OUT = 8 };
-
-struct Geo {  // kernel-side copy of Geometry
-    int dtype, G, D, B;
-    uint32_t kv_out;
-    uint64_t bb, k_off, ks_off, v_off, vs_off;
-    uint32_t xcd_map;  // attention: XCD-aware workgroup order
-};
-
-static int tune(const char *name, int def);
-
-static Geo to_geo(const Geometry &g) {
-    return Geo{g.dtype, g.G, g.D, g.B, (uint32_t)g.kv_out, g.block_bytes,
-               g.k_off, g.ks_off, g.v_off, g.vs_off, (uint32_t)tune("QVKV_ATTN_XCD", 1)};
-}
-
-__device__ __forceinline__ void flag(int *err, int bit) { atomicOr(err, bit); }
-
-__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
-    h2 v = {(_Float16)a, (_Float16)b};  // v_cvt_f16_f32: IEEE round to nearest even
-    return __builtin_bit_cast(uint32_t, v);
-}
-
-// Position of logical value d inside a stored q8_0 row.
-__device__ __forceinline__ uint32_t kperm(uint32_t d, uint32_t D) {
-    return ((d & 31u) >> 3) * (D >> 2) + (d >> 5) * 8u + (d & 7u);
-}
-__device__ __forceinline__ uint32_t vperm(uint32_t d, uint32_t D) {
-    return ((d & 31u) >> 1) * (D >> 4) + 2u * (d >> 5) + (d & 1u);
-}
 
 // ---------------------------------------------------------------------------------
 // Append.  Thread = 8 consecutive values of one row of K or V (two 16-byte loads).
@@ -70,8 +30,6 @@ __device__ __forceinline__ uint32_t vperm(uint32_t d, uint32_t D) {
 // quantizer: d = amax/127 (f32), scale = f16(d) RNE, inv = d > 0 ? 1/d : 0 from the
 // f32 d, q = clamp(round_half_away(x*inv), -127, 127), NaN -> 0.
 // ---------------------------------------------------------------------------------
-typedef float f4v __attribute__((ext_vector_type(4)));
-typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 
 template <bool NT>
 __device__ __forceinline__ float4 load_f4(const float *p) {
@@ -362,272 +320,7 @@ __global__ __launch_bounds__(256) void k_block_copy(uint8_t *__restrict__ pool,
 // ---------------------------------------------------------------------------------
 // Decode attention, MFMA form.  Workgroup = 4 waves on one (item, KV head, head chunk
 // of <= 8 query heads, context chunk); wave w takes the chunk's tiles w, w+4, ...
-// Lane l: c = l % 16 (MFMA column / K row), q = l / 16.
 // ---------------------------------------------------------------------------------
-static constexpr float LOG2E_F = 1.4426950408889634f;
-
-__device__ __forceinline__ h4 h4_of(uint32_t a, uint32_t b) {
-    return __builtin_bit_cast(h4, make_uint2(a, b));
-}
-
-// 4 int8 (one word) -> 4 f16, exactly: (0x6400 | (x ^ 0x80)) is 1024 + x + 128 in f16.
-__device__ __forceinline__ h4 i8x4_to_h4(uint32_t w) {
-    const uint32_t u = w ^ 0x80808080u;
-    const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
-    const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
-    const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
-    const h2 a = __builtin_bit_cast(h2, lo) - bias;
-    const h2 b = __builtin_bit_cast(h2, hi) - bias;
-    return h4{a.x, a.y, b.x, b.y};
-}
-
-// f32 -> (high f16, residual f16); lane columns < 8 take the high part.
-__device__ __forceinline__ _Float16 split_part(float x, bool hi_part) {
-    const _Float16 hi = (_Float16)x;
-    const _Float16 lo = (_Float16)(x - (float)hi);
-    return hi_part ? hi : lo;
-}
-
-typedef uint32_t u2v __attribute__((ext_vector_type(2)));
-
-// NB bytes (4, 8 or a multiple of 16) into words; NT: non-temporal (streamed once).
-template <int NB, bool NT>
-__device__ __forceinline__ void load_bytes(const uint8_t *p, uint32_t *w) {
-    if constexpr (NB == 4) {
-        w[0] = NT ? __builtin_nontemporal_load((const uint32_t *)p) : *(const uint32_t *)p;
-    } else if constexpr (NB == 8) {
-        const u2v x = NT ? __builtin_nontemporal_load((const u2v *)p) : *(const u2v *)p;
-        w[0] = x.x; w[1] = x.y;
-    } else {
-#pragma unroll
-        for (int i = 0; i < NB / 16; i++) {
-            const u4v x = NT ? __builtin_nontemporal_load((const u4v *)(p + 16 * i))
-                             : *(const u4v *)(p + 16 * i);
-            w[4 * i] = x.x; w[4 * i + 1] = x.y; w[4 * i + 2] = x.z; w[4 * i + 3] = x.w;
-        }
-    }
-}
-
-template <int NB>
-__device__ __forceinline__ void load_bytes(const uint8_t *p, uint32_t *w) {
-    load_bytes<NB, false>(p, w);
-}
-
-// f16 number idx of a packed word array, as f32 (idx is a compile-time constant).
-__device__ __forceinline__ float half_at(const uint32_t *w, int idx) {
-    const uint32_t x = w[idx >> 1];
-    return (float)__builtin_bit_cast(_Float16, (uint16_t)((idx & 1) ? (x >> 16) : (x & 0xffffu)));
-}
-
-// One 16-position tile's operands for one lane, as loaded from the pool.
-template <int D, bool Q8>
-struct Tile {
-    static constexpr int KW = Q8 ? D / 16 : D / 8;                    // key words
-    static constexpr int VW = Q8 ? (D / 64 > 0 ? D / 64 : 1) : D / 32;  // value words per row
-    static constexpr int SW = Q8 ? 2 * (D / 32) : 1;                  // scale words (4 rows)
-    uint32_t k[KW];
-    uint32_t v[4][VW];
-    uint32_t ks[SW], vs[SW];
-    uint32_t p0;
-    bool ok;
-};
-
-template <int D, bool Q8, bool NT>
-__device__ __forceinline__ void load_tile(Tile<D, Q8> &t, uint32_t tt, const uint8_t *pool,
-                                          uint64_t pool_blocks, const uint32_t *blocks,
-                                          uint32_t tab, uint32_t g, uint32_t c, uint32_t qg,
-                                          const Geo &geo, int *err) {
-    const uint32_t B = (uint32_t)geo.B;
-    t.p0 = tt * 16u;
-    const uint32_t blk = blocks[tab + t.p0 / B];
-    t.ok = blk < pool_blocks;
-    if (!t.ok) {
-        if ((threadIdx.x & 63u) == 0) flag(err, ERR_BLOCK);
-        return;
-    }
-    const uint8_t *base = pool + (uint64_t)blk * geo.bb;
-    const uint64_t rows = (uint64_t)g * B + t.p0 % B;  // first (head, position) row of the tile
-    if constexpr (!Q8) {
-        // K row c: 16-byte pieces at d = 32i + 8qg; V rows 4qg..4qg+3 at d = c*D/16
-        const uint8_t *kr = base + geo.k_off + ((rows + c) * D + 8 * qg) * 2u;
-#pragma unroll
-        for (int i = 0; i < D / 32; i++) load_bytes<16, NT>(kr + 64u * i, t.k + 4 * i);
-        const uint8_t *vr = base + geo.v_off + ((rows + 4 * qg) * D + c * (D / 16)) * 2u;
-#pragma unroll
-        for (int i = 0; i < 4; i++) load_bytes<D / 8, NT>(vr + (uint64_t)i * D * 2u, t.v[i]);
-    } else {
-        load_bytes<D / 4, NT>(base + geo.k_off + (rows + c) * D + qg * (D / 4), t.k);
-        load_bytes<8 * (D / 32), NT>(base + geo.ks_off + (rows + 4 * qg) * (D / 32) * 2u, t.ks);
-        load_bytes<8 * (D / 32), NT>(base + geo.vs_off + (rows + 4 * qg) * (D / 32) * 2u, t.vs);
-        const uint8_t *vr = base + geo.v_off + (rows + 4 * qg) * D + c * (D / 16);
-#pragma unroll
-        for (int i = 0; i < 4; i++) load_bytes<D / 16, NT>(vr + (uint64_t)i * D, t.v[i]);
-    }
-}
-
-// Online-softmax state of one lane: running max and partial sum (head c % 8), and the
-// output accumulator (rows 4qg..4qg+3 of the MFMA tile, columns by d mapping).
-template <int D>
-struct SoftmaxState {
-    float m, l;
-    f4 acc[D / 16];
-};
-
-// PK ("packed", q8_0 with at most 4 query heads per KV head): MFMA columns c and c^4
-// carry the same head (c & 3), and in the P.V step lane c's row holds the scaled
-// probabilities of group 2m + sigma (sigma = (c >> 2) & 1), so one A operand serves two
-// 32-value groups and each lane scales for one group instead of two.
-// n_col: positions this lane's query column sees (causal limit); n_max: the largest n_col
-// of the wave -- rows at or past it may never have been written and are zeroed.
-template <int D, bool Q8, bool PK>
-__device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<D> &st,
-                                             const h4 *qf, uint32_t n_col, uint32_t n_max,
-                                             uint32_t qg, bool hi_col, uint32_t sigma) {
-    constexpr int NJ = D / 16;
-    constexpr int NG = D / 32;
-    if (!t.ok) return;
-    const uint32_t p0 = t.p0;
-    // ---- scores S^T[position][column] = K . Q^T
-    f4 s = f4{0.f, 0.f, 0.f, 0.f};
-    uint32_t vw[4][Tile<D, Q8>::VW];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int x = 0; x < Tile<D, Q8>::VW; x++) vw[i][x] = t.v[i][x];
-    if constexpr (!Q8) {
-#pragma unroll
-        for (int i = 0; i < NG; i++) {
-            s = __builtin_amdgcn_mfma_f32_16x16x16f16(h4_of(t.k[4 * i], t.k[4 * i + 1]), qf[2 * i], s, 0, 0, 0);
-            s = __builtin_amdgcn_mfma_f32_16x16x16f16(h4_of(t.k[4 * i + 2], t.k[4 * i + 3]), qf[2 * i + 1], s, 0, 0, 0);
-        }
-    } else {
-#pragma unroll
-        for (int gi = 0; gi < NG; gi++) {
-            f4 sg = f4{0.f, 0.f, 0.f, 0.f};
-            sg = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4(t.k[2 * gi]), qf[2 * gi], sg, 0, 0, 0);
-            sg = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4(t.k[2 * gi + 1]), qf[2 * gi + 1], sg, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; i++) s[i] = fmaf(sg[i], half_at(t.ks, i * NG + gi), s[i]);
-        }
-    }
-
-    // ---- high + residual columns, mask, online softmax (log2 domain)
-    float sc[4];
-    const bool partial = p0 + 16u > n_max;  // wave-uniform
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        float v2 = s[i] + __shfl_xor(s[i], 8);
-        if (p0 + 4 * qg + i >= n_col) v2 = -INFINITY;
-        sc[i] = v2;
-    }
-    float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const float mnew = fmaxf(st.m, tmax);
-    const float msafe = mnew == -INFINITY ? 0.0f : mnew;
-    const float alpha = __builtin_amdgcn_exp2f(st.m - msafe);
-    float pr[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) pr[i] = __builtin_amdgcn_exp2f(sc[i] - msafe);
-    st.l = st.l * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
-    if (__any(mnew > st.m)) {
-        float ar[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) ar[i] = __shfl(alpha, 4 * qg + i);
-#pragma unroll
-        for (int j = 0; j < NJ; j++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) st.acc[j][i] *= ar[i];
-    }
-    st.m = mnew;
-
-    // ---- O += P . V
-    if constexpr (!Q8) {
-        if (partial) {
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                if (p0 + 4 * qg + i >= n_max)
-#pragma unroll
-                    for (int x = 0; x < D / 32; x++) vw[i][x] = 0u;
-        }
-        const h4 pa = h4{split_part(pr[0], hi_col), split_part(pr[1], hi_col),
-                         split_part(pr[2], hi_col), split_part(pr[3], hi_col)};
-#pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-            const uint32_t w0 = __builtin_amdgcn_perm(vw[1][j >> 1], vw[0][j >> 1], sel);
-            const uint32_t w1 = __builtin_amdgcn_perm(vw[3][j >> 1], vw[2][j >> 1], sel);
-            st.acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, h4_of(w0, w1), st.acc[j], 0, 0, 0);
-        }
-    } else {
-        // V operand of MFMA j (group j/2): rows 4qg..4qg+3 at byte j of each row's run,
-        // int8 exactly as f16.  The rows' scales of group j/2 fold into the probabilities
-        // (P' = p * scale in f32, then f16 high part + residual: exact to ~2^-22), so the
-        // products the MFMA forms are exact.
-        uint32_t vsw[4][Tile<D, Q8>::VW];  // biased bytes x ^ 0x80
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const bool dead = partial && p0 + 4 * qg + i >= n_max;
-#pragma unroll
-            for (int x = 0; x < Tile<D, Q8>::VW; x++) vsw[i][x] = dead ? 0x80808080u : vw[i][x] ^ 0x80808080u;
-        }
-        const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
-        const float lo_part = hi_col ? 0.0f : 1.0f;
-        // The A operand of scaled probabilities for group g (this lane's scale pick).
-        auto scaled = [&](float sc_of_row[4]) {
-            _Float16 pg[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                float x = pr[i] * sc_of_row[i];
-                if (partial && p0 + 4 * qg + i >= n_max) x = 0.0f;  // a never-written slot's scale
-                const _Float16 u = (_Float16)x;
-                pg[i] = (_Float16)fmaf(-lo_part, (float)u, x);  // u, or the residual x - u
-            }
-            return h4{pg[0], pg[1], pg[2], pg[3]};
-        };
-        // P'.V for the two MFMAs of group gi (bytes 2gi, 2gi+1 of each row's run).
-        auto pv_group = [&](const h4 &pa, int gi) {
-            const int j = 2 * gi;
-            const uint32_t b = (uint32_t)(j & 3);
-            const uint32_t sel = ((4u + b + 1) << 24) | ((b + 1) << 16) | ((4u + b) << 8) | b;
-            const uint32_t t01 = __builtin_amdgcn_perm(vsw[1][j >> 2], vsw[0][j >> 2], sel);
-            const uint32_t t23 = __builtin_amdgcn_perm(vsw[3][j >> 2], vsw[2][j >> 2], sel);
-#pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const uint32_t spread = u ? 0x04030402u : 0x04010400u;
-                const h2 x01 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, t01, spread)) - bias;
-                const h2 x23 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, t23, spread)) - bias;
-                st.acc[j + u] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, h4{x01.x, x01.y, x23.x, x23.y},
-                                                                      st.acc[j + u], 0, 0, 0);
-            }
-        };
-        if constexpr (PK) {
-            // Groups 2m and 2m+1 share one A operand: the scales of row i are the low and
-            // high f16 of word i*NG/2 + m (row-major [row][group] f16 scales).
-#pragma unroll
-            for (int m = 0; m < NG / 2; m++) {
-                float sc[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const uint32_t w = t.vs[(i * NG) / 2 + m] >> (16u * sigma);
-                    sc[i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
-                }
-                const h4 pa = scaled(sc);
-                pv_group(pa, 2 * m);
-                pv_group(pa, 2 * m + 1);
-            }
-        } else {
-#pragma unroll
-            for (int gi = 0; gi < NG; gi++) {
-                float sc[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) sc[i] = half_at(t.vs, i * NG + gi);
-                pv_group(scaled(sc), gi);
-            }
-        }
-    }
-}
-
 #define QV_ATTN_PARAMS                                                                          \
     const uint8_t *__restrict__ pool, uint64_t pool_blocks, const float *__restrict__ q,        \
         const uint32_t *__restrict__ blocks, uint64_t n_table,                                  \
@@ -710,8 +403,8 @@ __device__ __forceinline__ void attn_body(QV_ATTN_PARAMS) {
         for (int j = 0; j < NJ; j++) {
             const int d0 = 32 * (j >> 1) + 8 * (int)qg + 4 * (j & 1);
             float4 x = hvalid ? *(const float4 *)(qrow + d0) : make_float4(0.f, 0.f, 0.f, 0.f);
-            qf[j] = h4{split_part(x.x * qs, hi_col), split_part(x.y * qs, hi_col),
-                       split_part(x.z * qs, hi_col), split_part(x.w * qs, hi_col)};
+            qf[j] = h4{split_part(mul_rn(x.x, qs), hi_col), split_part(mul_rn(x.y, qs), hi_col),
+                       split_part(mul_rn(x.z, qs), hi_col), split_part(mul_rn(x.w, qs), hi_col)};
         }
     }
 
@@ -814,222 +507,6 @@ __global__ __launch_bounds__(256) void k_attn_merge(const float *__restrict__ ws
     }
 }
 
-// ---------------------------------------------------------------------------------
-// Paged prefill attention: segment i holds n_tok[i] consecutive tokens of one sequence at
-// positions pos0[i], pos0[i]+1, ... (q / out rows q_at[i] + j); token j attends over
-// positions 0..pos0[i]+j of its table (causal), after all of the segment's rows are stored.
-// Workgroup = (segment, KV head, block of 32 query columns); a query column is one
-// (token, head) pair, column index j * GS + h.  Each wave owns 8 columns (MFMA columns
-// c and c + 8 carry their f16 high parts and residuals, as in decode) and streams every
-// tile up to its last token's position; the 4 waves read the same tiles, so L1/L2 serve
-// the repeats.  Columns see their own causal limit; the wave's outputs need no merge.
-// ---------------------------------------------------------------------------------
-#define QV_PREFILL_PARAMS                                                                       \
-    const uint8_t *__restrict__ pool, uint64_t pool_blocks, const float *__restrict__ q,        \
-        const uint32_t *__restrict__ blocks, uint64_t n_table,                                  \
-        const uint32_t *__restrict__ table_at, const uint32_t *__restrict__ pos0,               \
-        const uint32_t *__restrict__ q_at, const uint32_t *__restrict__ n_tok, uint32_t n_seg,  \
-        uint32_t H, uint32_t max_pos, uint32_t max_tok, uint64_t q_rows, uint32_t n_cb,         \
-        float *__restrict__ out, Geo geo, int *err
-
-template <int D, bool Q8>
-__global__ __launch_bounds__(256) void k_prefill_mfma(QV_PREFILL_PARAMS) {
-    constexpr int NJ = D / 16;
-    const uint32_t G = (uint32_t)geo.G, B = (uint32_t)geo.B;
-    const uint32_t GS = H / G;
-    uint32_t bid = blockIdx.x;
-    if (geo.xcd_map) {  // column blocks of one (segment, KV head) share an XCD's L2
-        const uint32_t nb = gridDim.x, qn = nb / 8, rn = nb % 8;
-        const uint32_t x = bid % 8, i = bid / 8;
-        bid = x < rn ? x * (qn + 1) + i : rn * (qn + 1) + (x - rn) * qn + i;
-    }
-    const uint32_t cb = bid % n_cb;
-    const uint32_t sg = bid / n_cb;
-    const uint32_t g = sg % G;
-    const uint32_t seg = sg / G;
-    if (seg >= n_seg) return;
-    const uint32_t nt = n_tok[seg], p0s = pos0[seg], qa = q_at[seg], tab = table_at[seg];
-    if (nt == 0) return;
-    if (nt > max_tok || (uint64_t)p0s + nt - 1 > max_pos) {
-        if (threadIdx.x == 0 && cb == 0 && g == 0) flag(err, ERR_POS);
-        return;
-    }
-    if ((uint64_t)qa + nt > q_rows) {
-        if (threadIdx.x == 0 && cb == 0 && g == 0) flag(err, ERR_OUT);
-        return;
-    }
-    const uint32_t n_all = p0s + nt;
-    if ((uint64_t)tab + (n_all + B - 1) / B > n_table) {
-        if (threadIdx.x == 0 && cb == 0 && g == 0) flag(err, ERR_TABLE);
-        return;
-    }
-    const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
-    const uint32_t c = lane & 15u, qg = lane >> 4;
-    const bool hi_col = c < 8;
-    const uint32_t cc0 = cb * 32u + w * 8u;          // the wave's first column
-    const uint32_t ncols = nt * GS;
-    if (cc0 >= ncols) return;
-    const uint32_t last_tok = min(nt - 1, (cc0 + 7u) / GS);
-    const uint32_t n_max = p0s + last_tok + 1;        // the wave's furthest causal limit
-    const uint32_t cc = cc0 + (c & 7u);
-    const bool valid = cc < ncols;
-    const uint32_t tj = valid ? cc / GS : 0u, hh = valid ? cc % GS : 0u;
-    const uint32_t n_col = valid ? p0s + tj + 1 : n_max;
-
-    h4 qf[NJ];
-    {
-        const float qs = (1.0f / sqrtf((float)D)) * LOG2E_F;
-        const float *qrow = q + ((uint64_t)(qa + tj) * H + (uint64_t)g * GS + hh) * D;
-#pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            const int d0 = 32 * (j >> 1) + 8 * (int)qg + 4 * (j & 1);
-            float4 x = valid ? *(const float4 *)(qrow + d0) : make_float4(0.f, 0.f, 0.f, 0.f);
-            qf[j] = h4{split_part(x.x * qs, hi_col), split_part(x.y * qs, hi_col),
-                       split_part(x.z * qs, hi_col), split_part(x.w * qs, hi_col)};
-        }
-    }
-    SoftmaxState<D> st;
-    st.m = -INFINITY;
-    st.l = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NJ; j++) st.acc[j] = f4{0.f, 0.f, 0.f, 0.f};
-    const uint32_t ntiles = (n_max + 15) / 16;
-    for (uint32_t tt = 0; tt < ntiles; tt++) {
-        Tile<D, Q8> cur;
-        load_tile<D, Q8, false>(cur, tt, pool, pool_blocks, blocks, tab, g, c, qg, geo, err);
-        compute_tile<D, Q8, false>(cur, st, qf, n_col, n_max, qg, hi_col, 0u);
-    }
-    // column totals; output rows 4qg + i (qg < 2) after adding the residual rows
-    float l = st.l;
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
-#pragma unroll
-    for (int j = 0; j < NJ; j++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) st.acc[j][i] += __shfl_xor(st.acc[j][i], 32);
-    float lr[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) lr[i] = __shfl(l, 4 * (int)(qg & 1u) + i);
-    if (qg >= 2) return;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const uint32_t ccr = cc0 + 4 * qg + i;
-        if (ccr >= ncols) continue;
-        const uint32_t tr = ccr / GS, hr = ccr % GS;
-        float *orow = out + ((uint64_t)(qa + tr) * H + (uint64_t)g * GS + hr) * D;
-        const float inv = 1.0f / lr[i];
-        if constexpr (!Q8) {
-            float o[NJ];
-#pragma unroll
-            for (int j = 0; j < NJ; j++) o[j] = st.acc[j][i] * inv;
-#pragma unroll
-            for (int j = 0; j < NJ; j += 4)
-                *(float4 *)(orow + c * (D / 16) + j) = make_float4(o[j], o[j + 1], o[j + 2], o[j + 3]);
-        } else {
-#pragma unroll
-            for (int j = 0; j < NJ; j += 2)
-                *(float2 *)(orow + 32 * (j >> 1) + 2 * c) =
-                    make_float2(st.acc[j][i] * inv, st.acc[j + 1][i] * inv);
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------------
-// Decode attention, generic form (any d that is a multiple of 8 up to 512, any group):
-// one wave per (item, query head); lanes take 64 positions at a time for the scores,
-// then d-columns for P.V.  Used where the MFMA form has no instance.
-// ---------------------------------------------------------------------------------
-template <bool Q8>
-__device__ __forceinline__ float kv_elem(const uint8_t *base, const Geo &geo, bool isv,
-                                         uint64_t row, uint32_t d) {
-    const uint32_t D = (uint32_t)geo.D;
-    if constexpr (!Q8) {
-        return (float)((const _Float16 *)(base + (isv ? geo.v_off : geo.k_off)))[row * D + d];
-    } else {
-        const int8_t qv = (int8_t)base[(isv ? geo.v_off : geo.k_off) + row * D +
-                                       (isv ? vperm(d, D) : kperm(d, D))];
-        const float sc = (float)((const _Float16 *)(base + (isv ? geo.vs_off : geo.ks_off)))
-            [row * (D >> 5) + (d >> 5)];
-        return (float)qv * sc;
-    }
-}
-
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-    return x;
-}
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
-    return x;
-}
-
-// One wave: query row qrow of KV head g over positions 0..n-1 of table tab -> orow.
-template <bool Q8>
-__device__ __forceinline__ void generic_body(const uint8_t *__restrict__ pool,
-                                             uint64_t pool_blocks,
-                                             const uint32_t *__restrict__ blocks, uint32_t tab,
-                                             uint32_t n, uint32_t g, const float *qrow,
-                                             float *orow, const Geo &geo, int *err) {
-    __shared__ float qs[512];
-    __shared__ float ps[64];
-    const uint32_t D = (uint32_t)geo.D, B = (uint32_t)geo.B;
-    const uint32_t lane = threadIdx.x;
-    const float scale = (1.0f / sqrtf((float)D)) * LOG2E_F;
-    for (uint32_t i = lane; i < D; i += 64) qs[i] = qrow[i] * scale;
-    __syncthreads();
-    float m = -INFINITY, l = 0.0f, acc[8];
-#pragma unroll
-    for (int x = 0; x < 8; x++) acc[x] = 0.0f;
-    for (uint32_t b0 = 0; b0 < n; b0 += 64) {
-        const uint32_t p = b0 + lane;
-        float s = -INFINITY;
-        if (p < n) {
-            const uint32_t blk = blocks[tab + p / B];
-            if (blk < pool_blocks) {
-                const uint8_t *base = pool + (uint64_t)blk * geo.bb;
-                const uint64_t row = (uint64_t)g * B + p % B;
-                float t = 0.0f;
-                for (uint32_t d = 0; d < D; d++) t = fmaf(qs[d], kv_elem<Q8>(base, geo, false, row, d), t);
-                s = t;
-            } else {
-                flag(err, ERR_BLOCK);
-            }
-        }
-        const float mnew = fmaxf(m, wave_max(s));
-        const float msafe = mnew == -INFINITY ? 0.0f : mnew;
-        const float alpha = __builtin_amdgcn_exp2f(m - msafe);
-        const float e = p < n ? __builtin_amdgcn_exp2f(s - msafe) : 0.0f;
-        l = l * alpha + wave_sum(e);
-#pragma unroll
-        for (int x = 0; x < 8; x++) acc[x] *= alpha;
-        m = mnew;
-        ps[lane] = e;
-        __syncthreads();
-        const uint32_t cnt = min(64u, n - b0);
-        for (uint32_t pp = 0; pp < cnt; pp++) {
-            const uint32_t p2 = b0 + pp;
-            const uint32_t blk = blocks[tab + p2 / B];
-            if (blk >= pool_blocks) continue;
-            const uint8_t *base = pool + (uint64_t)blk * geo.bb;
-            const uint64_t row = (uint64_t)g * B + p2 % B;
-            const float wgt = ps[pp];
-#pragma unroll
-            for (int x = 0; x < 8; x++) {
-                const uint32_t d = lane + 64u * x;
-                if (d < D) acc[x] = fmaf(wgt, kv_elem<Q8>(base, geo, true, row, d), acc[x]);
-            }
-        }
-        __syncthreads();
-    }
-#pragma unroll
-    for (int x = 0; x < 8; x++) {
-        const uint32_t d = lane + 64u * x;
-        if (d < D) orow[d] = acc[x] / l;
-    }
-}
-
 template <bool Q8>
 __global__ __launch_bounds__(64) void k_attn_generic(
     const uint8_t *__restrict__ pool, uint64_t pool_blocks, const float *__restrict__ q,
@@ -1053,34 +530,6 @@ __global__ __launch_bounds__(64) void k_attn_generic(
     const uint64_t row = (uint64_t)item * H + h;
     generic_body<Q8>(pool, pool_blocks, blocks, tab, n, h / (H / G), q + row * D, out + row * D,
                      geo, err);
-}
-
-// Prefill, generic form: one wave per (segment, token, query head).
-template <bool Q8>
-__global__ __launch_bounds__(64) void k_prefill_generic(QV_PREFILL_PARAMS) {
-    const uint32_t h = blockIdx.x % H;
-    const uint32_t j = (blockIdx.x / H) % max_tok;
-    const uint32_t seg = blockIdx.x / H / max_tok;
-    if (seg >= n_seg) return;
-    const uint32_t B = (uint32_t)geo.B, G = (uint32_t)geo.G, D = (uint32_t)geo.D;
-    const uint32_t nt = n_tok[seg], p0s = pos0[seg], qa = q_at[seg], tab = table_at[seg];
-    if (j >= nt) return;
-    const bool first = threadIdx.x == 0 && j == 0 && h == 0;
-    if (nt > max_tok || (uint64_t)p0s + nt - 1 > max_pos) {
-        if (first) flag(err, ERR_POS);
-        return;
-    }
-    if ((uint64_t)qa + nt > q_rows) {
-        if (first) flag(err, ERR_OUT);
-        return;
-    }
-    if ((uint64_t)tab + (p0s + nt + B - 1) / B > n_table) {
-        if (first) flag(err, ERR_TABLE);
-        return;
-    }
-    const uint64_t row = (uint64_t)(qa + j) * H + h;
-    generic_body<Q8>(pool, pool_blocks, blocks, tab, p0s + j + 1, h / (H / G), q + row * D,
-                     out + row * D, geo, err);
 }
 
 // =================================================================================
@@ -1134,7 +583,7 @@ int make_geometry(const qvkv_layout *l, Geometry *g, const char **why) {
 
 // Launch-shape knobs (defaults are the measured best); an environment variable of the
 // same name overrides one for measurement.
-static int tune(const char *name, int def) {
+int tune(const char *name, int def) {
     const char *s = getenv(name);
     return s && *s ? atoi(s) : def;
 }
@@ -1316,57 +765,6 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
     if (e != hipSuccess || p.n_chunks == 1) return e;
     hipLaunchKernelGGL(k_attn_merge, dim3(n_items * heads), dim3(g.D), 0, s, (const float *)ws,
                        pos, n_items, heads, max_pos, p.n_chunks, p.tpc, (uint32_t)g.D, out);
-    return hipGetLastError();
-}
-
-int check_prefill(const Geometry &g, uint32_t n_seg, uint32_t heads, uint32_t max_tok,
-                  const char **why) {
-    if (heads == 0 || heads % (uint32_t)g.G != 0) {
-        *why = "query heads must be a positive multiple of kv_heads";
-        return QVKV_E_SHAPE;
-    }
-    const bool mfma = g.D == 64 || g.D == 128 || g.D == 256;
-    const uint64_t cols = (uint64_t)max_tok * (heads / (uint32_t)g.G);
-    const uint64_t grid = mfma ? (uint64_t)n_seg * g.G * ((cols + 31) / 32)
-                               : (uint64_t)n_seg * max_tok * heads;
-    if (grid > 0x7fffffffull) {
-        *why = "batch too large";
-        return QVKV_E_SHAPE;
-    }
-    return QVKV_OK;
-}
-
-hipError_t launch_prefill(const Geometry &g, const void *pool, uint64_t pool_blocks,
-                          const float *q, const uint32_t *blocks, uint64_t n_table,
-                          const uint32_t *table_at, const uint32_t *pos0, const uint32_t *q_at,
-                          const uint32_t *n_tok, uint32_t n_seg, uint32_t heads,
-                          uint32_t max_pos, uint32_t max_tok, uint64_t q_rows, float *out,
-                          int *err, hipStream_t s) {
-    if (n_seg == 0 || max_tok == 0) return hipSuccess;
-    const Geo geo = to_geo(g);
-    const uint8_t *pp = (const uint8_t *)pool;
-    const bool q8 = g.dtype == QVKV_Q8_0;
-    if (!(g.D == 64 || g.D == 128 || g.D == 256)) {
-        const unsigned grid = (unsigned)((uint64_t)n_seg * max_tok * heads);
-#define QV_PG(QQ)                                                                              \
-    hipLaunchKernelGGL(k_prefill_generic<QQ>, dim3(grid), dim3(64), 0, s, pp, pool_blocks, q,   \
-                       blocks, n_table, table_at, pos0, q_at, n_tok, n_seg, heads, max_pos,    \
-                       max_tok, q_rows, 0u, out, geo, err)
-        if (q8) QV_PG(true); else QV_PG(false);
-#undef QV_PG
-        return hipGetLastError();
-    }
-    const uint32_t GS = heads / (uint32_t)g.G;
-    const uint32_t n_cb = (uint32_t)(((uint64_t)max_tok * GS + 31) / 32);
-    const unsigned grid = (unsigned)((uint64_t)n_seg * g.G * n_cb);
-#define QV_PF(DD, QQ)                                                                          \
-    hipLaunchKernelGGL((k_prefill_mfma<DD, QQ>), dim3(grid), dim3(256), 0, s, pp, pool_blocks,  \
-                       q, blocks, n_table, table_at, pos0, q_at, n_tok, n_seg, heads, max_pos, \
-                       max_tok, q_rows, n_cb, out, geo, err)
-    if (g.D == 64) { if (q8) QV_PF(64, true); else QV_PF(64, false); }
-    else if (g.D == 128) { if (q8) QV_PF(128, true); else QV_PF(128, false); }
-    else { if (q8) QV_PF(256, true); else QV_PF(256, false); }
-#undef QV_PF
     return hipGetLastError();
 }
 

@@ -1,0 +1,513 @@
+// Paged prefill attention kernels (gfx950): causal attention of segments of
+// consecutive stored tokens over the paged pool.  Built with MFMA operands in VGPRs
+// (-mllvm -amdgpu-mfma-vgpr-form): the online-softmax rescale and the P split work on
+// the accumulators with plain VALU ops instead of copying them to and from AGPRs.
+#include "device.h"
+
+namespace qvkv {
+
+// ---------------------------------------------------------------------------------
+// Paged prefill attention: segment i holds n_tok[i] consecutive tokens of one sequence at
+// positions pos0[i], pos0[i]+1, ... (q / out rows q_at[i] + j); token j attends over
+// positions 0..pos0[i]+j of its table (causal), after all of the segment's rows are stored.
+// Workgroup = (segment, KV head, block of 32 query columns); a query column is one
+// (token, head) pair, column index j * GS + h.  Each wave owns 8 columns (MFMA columns
+// c and c + 8 carry their f16 high parts and residuals, as in decode) and streams every
+// tile up to its last token's position; the 4 waves read the same tiles, so L1/L2 serve
+// the repeats.  Columns see their own causal limit; the wave's outputs need no merge.
+// ---------------------------------------------------------------------------------
+#define QV_PREFILL_PARAMS                                                                       \
+    const uint8_t *__restrict__ pool, uint64_t pool_blocks, const float *__restrict__ q,        \
+        const uint32_t *__restrict__ blocks, uint64_t n_table,                                  \
+        const uint32_t *__restrict__ table_at, const uint32_t *__restrict__ pos0,               \
+        const uint32_t *__restrict__ q_at, const uint32_t *__restrict__ n_tok, uint32_t n_seg,  \
+        uint32_t H, uint32_t max_pos, uint32_t max_tok, uint64_t q_rows, uint32_t n_cb,         \
+        float *__restrict__ out, Geo geo, int *err
+
+template <int D, bool Q8>
+__global__ __launch_bounds__(256) void k_prefill_mfma(QV_PREFILL_PARAMS) {
+    constexpr int NJ = D / 16;
+    const uint32_t G = (uint32_t)geo.G, B = (uint32_t)geo.B;
+    const uint32_t GS = H / G;
+    uint32_t bid = blockIdx.x;
+    if (geo.xcd_map) {  // column blocks of one (segment, KV head) share an XCD's L2
+        const uint32_t nb = gridDim.x, qn = nb / 8, rn = nb % 8;
+        const uint32_t x = bid % 8, i = bid / 8;
+        bid = x < rn ? x * (qn + 1) + i : rn * (qn + 1) + (x - rn) * qn + i;
+    }
+    const uint32_t cb = bid % n_cb;
+    const uint32_t sg = bid / n_cb;
+    const uint32_t g = sg % G;
+    const uint32_t seg = sg / G;
+    if (seg >= n_seg) return;
+    const uint32_t nt = n_tok[seg], p0s = pos0[seg], qa = q_at[seg], tab = table_at[seg];
+    if (nt == 0) return;
+    if (nt > max_tok || (uint64_t)p0s + nt - 1 > max_pos) {
+        if (threadIdx.x == 0 && cb == 0 && g == 0) flag(err, ERR_POS);
+        return;
+    }
+    if ((uint64_t)qa + nt > q_rows) {
+        if (threadIdx.x == 0 && cb == 0 && g == 0) flag(err, ERR_OUT);
+        return;
+    }
+    const uint32_t n_all = p0s + nt;
+    if ((uint64_t)tab + (n_all + B - 1) / B > n_table) {
+        if (threadIdx.x == 0 && cb == 0 && g == 0) flag(err, ERR_TABLE);
+        return;
+    }
+    const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+    const uint32_t c = lane & 15u, qg = lane >> 4;
+    const bool hi_col = c < 8;
+    const uint32_t cc0 = cb * 32u + w * 8u;          // the wave's first column
+    const uint32_t ncols = nt * GS;
+    if (cc0 >= ncols) return;
+    const uint32_t last_tok = min(nt - 1, (cc0 + 7u) / GS);
+    const uint32_t n_max = p0s + last_tok + 1;        // the wave's furthest causal limit
+    const uint32_t cc = cc0 + (c & 7u);
+    const bool valid = cc < ncols;
+    const uint32_t tj = valid ? cc / GS : 0u, hh = valid ? cc % GS : 0u;
+    const uint32_t n_col = valid ? p0s + tj + 1 : n_max;
+
+    h4 qf[NJ];
+    {
+        const float qs = (1.0f / sqrtf((float)D)) * LOG2E_F;
+        const float *qrow = q + ((uint64_t)(qa + tj) * H + (uint64_t)g * GS + hh) * D;
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const int d0 = 32 * (j >> 1) + 8 * (int)qg + 4 * (j & 1);
+            float4 x = valid ? *(const float4 *)(qrow + d0) : make_float4(0.f, 0.f, 0.f, 0.f);
+            qf[j] = h4{split_part(mul_rn(x.x, qs), hi_col), split_part(mul_rn(x.y, qs), hi_col),
+                       split_part(mul_rn(x.z, qs), hi_col), split_part(mul_rn(x.w, qs), hi_col)};
+        }
+    }
+    SoftmaxState<D> st;
+    st.m = -INFINITY;
+    st.l = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) st.acc[j] = f4{0.f, 0.f, 0.f, 0.f};
+    const uint32_t ntiles = (n_max + 15) / 16;
+    for (uint32_t tt = 0; tt < ntiles; tt++) {
+        Tile<D, Q8> cur;
+        load_tile<D, Q8, false>(cur, tt, pool, pool_blocks, blocks, tab, g, c, qg, geo, err);
+        compute_tile<D, Q8, false>(cur, st, qf, n_col, n_max, qg, hi_col, 0u);
+    }
+    // column totals; output rows 4qg + i (qg < 2) after adding the residual rows
+    float l = st.l;
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+#pragma unroll
+    for (int j = 0; j < NJ; j++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) st.acc[j][i] += __shfl_xor(st.acc[j][i], 32);
+    float lr[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) lr[i] = __shfl(l, 4 * (int)(qg & 1u) + i);
+    if (qg >= 2) return;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t ccr = cc0 + 4 * qg + i;
+        if (ccr >= ncols) continue;
+        const uint32_t tr = ccr / GS, hr = ccr % GS;
+        float *orow = out + ((uint64_t)(qa + tr) * H + (uint64_t)g * GS + hr) * D;
+        const float inv = 1.0f / lr[i];
+        if constexpr (!Q8) {
+            float o[NJ];
+#pragma unroll
+            for (int j = 0; j < NJ; j++) o[j] = st.acc[j][i] * inv;
+#pragma unroll
+            for (int j = 0; j < NJ; j += 4)
+                *(float4 *)(orow + c * (D / 16) + j) = make_float4(o[j], o[j + 1], o[j + 2], o[j + 3]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < NJ; j += 2)
+                *(float2 *)(orow + 32 * (j >> 1) + 2 * c) =
+                    make_float2(st.acc[j][i] * inv, st.acc[j + 1][i] * inv);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// Paged prefill attention, f16 pools, d = 64 or 128: the MFMA-throughput form.
+// Workgroup = (segment, KV head, block of 64 query rows); row r = token j * GS + head h.
+// The 4 waves stage 32-position K/V tiles once in LDS (K row-major, V transposed,
+// double-buffered: the next tile's global loads are in flight during this tile's math)
+// and each wave computes 16 query rows with v_mfma_f32_16x16x32_f16:
+//   S^T[pos][row] = K . Q^T: A = K rows from LDS (MFMA h, row i <-> position
+//     8(i/4) + 4h + i%4, so lane l ends up holding positions 8(l/16)..8(l/16)+7 of row
+//     l%16), B = q's f16 high part, then its residual (two accumulating MFMAs);
+//   O[row][d] += P . V: A = this lane's 8 probabilities (positions 8(l/16)+t), high part
+//     then residual; B = 8 consecutive positions of one d from the transposed V tile.
+// The k index of both MFMAs pairs the same logical element in A and B, so the products
+// are exact f16 x f16 in f32 accumulators as in decode.
+// ---------------------------------------------------------------------------------
+
+template <int D>
+struct PrefillLds {
+    static constexpr int TP = 32;          // positions per tile
+    static constexpr int KR = D + 8;       // K row stride (halves): spreads LDS banks
+    static constexpr int VR = TP + 8;      // V^T row stride (halves)
+    _Float16 k[2][TP][KR];
+    _Float16 v[2][D][VR];
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void k_prefill_f16(QV_PREFILL_PARAMS) {
+    constexpr int TP = PrefillLds<D>::TP;
+    constexpr int KS = D / 32;                 // QK k-steps
+    constexpr int NDB = D / 16;                // PV d blocks
+    constexpr int CPR = D / 8;                 // 16-byte chunks per K (or V) row
+    constexpr int LPT = 2 * TP * CPR / 256;    // chunks per thread per tile (K and V)
+    static_assert(LPT >= 1 && (2 * TP * CPR) % 256 == 0, "tile / thread mismatch");
+    __shared__ PrefillLds<D> lds;
+
+    const uint32_t G = (uint32_t)geo.G, B = (uint32_t)geo.B;
+    const uint32_t GS = H / G;
+    uint32_t bid = blockIdx.x;
+    if (geo.xcd_map) {
+        const uint32_t nb = gridDim.x, qn = nb / 8, rn = nb % 8;
+        const uint32_t x = bid % 8, i = bid / 8;
+        bid = x < rn ? x * (qn + 1) + i : rn * (qn + 1) + (x - rn) * qn + i;
+    }
+    const uint32_t qb = bid % n_cb;
+    const uint32_t sg = bid / n_cb;
+    const uint32_t g = sg % G;
+    const uint32_t seg = sg / G;
+    if (seg >= n_seg) return;
+    const uint32_t nt = n_tok[seg], p0s = pos0[seg], qa = q_at[seg], tab = table_at[seg];
+    if (nt == 0) return;
+    const bool lead = threadIdx.x == 0 && qb == 0 && g == 0;
+    if (nt > max_tok || (uint64_t)p0s + nt - 1 > max_pos) {
+        if (lead) flag(err, ERR_POS);
+        return;
+    }
+    if ((uint64_t)qa + nt > q_rows) {
+        if (lead) flag(err, ERR_OUT);
+        return;
+    }
+    const uint32_t n_all = p0s + nt;
+    if ((uint64_t)tab + (n_all + B - 1) / B > n_table) {
+        if (lead) flag(err, ERR_TABLE);
+        return;
+    }
+    const uint32_t nrows = nt * GS;
+    const uint32_t r0 = qb * 64u;
+    if (r0 >= nrows) return;  // the whole workgroup: no barrier has run yet
+    const uint32_t wg_last = min(nt - 1, (r0 + 63u) / GS);
+    const uint32_t n_wg = p0s + wg_last + 1;   // positions the workgroup's rows see
+    const uint32_t ntiles = (n_wg + TP - 1) / TP;
+
+    const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+    const uint32_t col = lane & 15u, grp = lane >> 4;
+    const uint32_t rw0 = r0 + w * 16u;                      // the wave's first row
+    const bool wave_live = rw0 < nrows;
+    const uint32_t n_wave = wave_live ? p0s + min(nt - 1, (rw0 + 15u) / GS) + 1 : 0u;
+    const uint32_t n_wave_min = wave_live ? p0s + rw0 / GS + 1 : 0u;  // first row's limit
+    const uint32_t row = rw0 + col;
+    const bool rvalid = row < nrows;
+    const uint32_t tj = rvalid ? row / GS : 0u, hh = rvalid ? row % GS : 0u;
+    const uint32_t n_row = rvalid ? p0s + tj + 1 : 0u;
+
+    // Q fragments: k-step ks, lane group grp holds d = 32 ks + 8 grp .. +7 (high, residual)
+    h8 qh[KS], ql[KS];
+    {
+        const float qs = (1.0f / sqrtf((float)D)) * LOG2E_F;
+        const float *qrow = q + ((uint64_t)(qa + tj) * H + (uint64_t)g * GS + hh) * D;
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            float x[8];
+            if (rvalid) {
+                const float4 a = *(const float4 *)(qrow + 32 * ks + 8 * grp);
+                const float4 b = *(const float4 *)(qrow + 32 * ks + 8 * grp + 4);
+                x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+                x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++) x[e] = 0.0f;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float y = mul_rn(x[e], qs);
+                const _Float16 hi = (_Float16)y;
+                qh[ks][e] = hi;
+                ql[ks][e] = (_Float16)(y - (float)hi);
+            }
+        }
+    }
+
+    // ---- tile loader.  The first VW waves move V: lane (q, piece) loads the 4x8 block of
+    // positions 4q..4q+3 x d = 8 piece..+7, transposes it in registers and writes 4
+    // positions of 8 rows of V^T (8 bytes each).  The other waves move K: 16-byte pieces,
+    // position p stored at LDS row 16 ((p >> 2) & 1) + 4 (p >> 3) + (p & 3), the A-operand
+    // row order of the scores MFMAs (their reads then walk consecutive rows).
+    constexpr int VW = CPR * 8 / 64;               // waves moving V (1 at d 64, 2 at d 128)
+    constexpr int KT = 256 - 64 * VW;              // threads moving K
+    constexpr int KCH = TP * CPR;                  // K chunks per tile
+    constexpr int KPT = (KCH + KT - 1) / KT;       // per K thread
+    constexpr int NST = KPT > 4 ? KPT : 4;
+    static_assert(VW >= 1 && VW <= 2 && CPR * 8 == 64 * VW, "V blocks fill whole waves");
+    u4v stage[NST];
+    const bool vwave = w < (uint32_t)VW;
+    const uint32_t vq = lane & 7u, vpiece = (lane >> 3) + 8u * w;   // V lanes
+    const uint32_t kt = threadIdx.x - 64u * VW;                      // K lanes
+    // Block bases of a tile's two 16-position halves (uniform across the workgroup: each
+    // half lies inside one block since B is a multiple of 16); positions past n_wg read
+    // as zero.
+    auto half_base = [&](uint32_t ph) -> const uint8_t * {
+        if (ph >= n_wg) return nullptr;
+        const uint32_t blk = blocks[tab + ph / B];
+        if (blk >= pool_blocks) {
+            if (threadIdx.x == 0) flag(err, ERR_BLOCK);
+            return nullptr;
+        }
+        return pool + (uint64_t)blk * geo.bb + ((uint64_t)g * B + ph % B) * D * 2u;
+    };
+    // Row r (0..31) of the tile from the bases of its two 16-position halves; positions
+    // past n_wg (r >= valid) and bad blocks read as zero.
+    auto fetch = [](const uint8_t *b0, const uint8_t *b1, uint32_t valid, uint32_t r,
+                    uint32_t off) -> u4v {
+        const uint8_t *b = (r & 16u) ? b1 : b0;
+        if (b == nullptr || r >= valid) return u4v{0u, 0u, 0u, 0u};
+        return *(const u4v *)(b + off);
+    };
+    auto load = [&](uint32_t t) {
+        const uint32_t p0 = t * TP;
+        const uint8_t *b0 = half_base(p0), *b1 = half_base(p0 + 16u);
+        const uint32_t valid = n_wg - p0 < (uint32_t)TP ? n_wg - p0 : (uint32_t)TP;
+        const bool full = valid == (uint32_t)TP && b0 != nullptr && b1 != nullptr;  // uniform
+        if (vwave) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const uint32_t row = 4 * vq + r;
+                const uint32_t off = (uint32_t)geo.v_off + ((row & 15u) * D + vpiece * 8) * 2u;
+                stage[r] = full ? *(const u4v *)(((row & 16u) ? b1 : b0) + off)
+                                : fetch(b0, b1, valid, row, off);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < KPT; u++) {
+                const uint32_t c = kt + (uint32_t)KT * u;
+                const uint32_t row = c / CPR;
+                const uint32_t off = (uint32_t)geo.k_off + ((row & 15u) * D + (c % CPR) * 8) * 2u;
+                if (c < (uint32_t)KCH)
+                    stage[u] = full ? *(const u4v *)(((row & 16u) ? b1 : b0) + off)
+                                    : fetch(b0, b1, valid, row, off);
+            }
+        }
+    };
+    auto store = [&](int buf) {
+        if (vwave) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+                u2v o;
+                o[0] = __builtin_amdgcn_perm(stage[1][e >> 1], stage[0][e >> 1], sel);
+                o[1] = __builtin_amdgcn_perm(stage[3][e >> 1], stage[2][e >> 1], sel);
+                *(u2v *)&lds.v[buf][vpiece * 8 + e][4 * vq] = o;
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < KPT; u++) {
+                const uint32_t c = kt + (uint32_t)KT * u;
+                if (c < (uint32_t)KCH) {
+                    const uint32_t p = c / CPR, piece = c % CPR;
+                    const uint32_t lr = 16u * ((p >> 2) & 1u) + 4u * (p >> 3) + (p & 3u);
+                    *(u4v *)&lds.k[buf][lr][piece * 8] = stage[u];
+                }
+            }
+        }
+    };
+
+    float m = -INFINITY, l = 0.0f;
+    f4 acc[NDB];
+#pragma unroll
+    for (int j = 0; j < NDB; j++) acc[j] = f4{0.f, 0.f, 0.f, 0.f};
+
+    load(0);
+    store(0);
+    __syncthreads();
+    for (uint32_t t = 0; t < ntiles; t++) {
+        const int buf = (int)(t & 1u);
+        if (t + 1 < ntiles) load(t + 1);
+        const uint32_t tp0 = t * TP;
+        if (tp0 < n_wave) {
+            // ---- scores: lane holds positions tp0 + 8 grp + (4h + i) of row `col`
+            f4 s[2];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                s[h] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++) {
+                    const h8 a = *(const h8 *)&lds.k[buf][16 * h + col][32 * ks + 8 * grp];
+                    s[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[ks], s[h], 0, 0, 0);
+                    s[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[ks], s[h], 0, 0, 0);
+                }
+            }
+            float sc[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) sc[e] = s[e >> 2][e & 3];
+            if (tp0 + TP > n_wave_min) {  // the tile reaches some row's causal limit
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    if (tp0 + 8u * grp + (uint32_t)e >= n_row) sc[e] = -INFINITY;
+            }
+            float tmax = sc[0];
+#pragma unroll
+            for (int e = 1; e < 8; e++) tmax = fmaxf(tmax, sc[e]);
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+            // Lazy rescale: the reference max m moves only when a row's scores exceed it by
+            // more than 2^8, so probabilities stay <= 256 (exact under the f16 high +
+            // residual split) and the O rescale runs on few tiles.
+            if (__any(tmax > m + 8.0f)) {
+                const float mnew = fmaxf(m, tmax);
+                const float alpha = __builtin_amdgcn_exp2f(m - (mnew == -INFINITY ? 0.0f : mnew));
+                l *= alpha;
+                float ar[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) ar[i] = __shfl(alpha, 4 * (int)grp + i);
+#pragma unroll
+                for (int j = 0; j < NDB; j++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[j][i] *= ar[i];
+                m = mnew;
+            }
+            const float msafe = m == -INFINITY ? 0.0f : m;
+            float pr[8];
+            float psum = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                pr[e] = __builtin_amdgcn_exp2f(sc[e] - msafe);
+                psum += pr[e];
+            }
+            l += psum;
+            h8 ph, pl;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const _Float16 hi = (_Float16)pr[e];
+                ph[e] = hi;
+                pl[e] = (_Float16)fmaf(-1.0f, (float)hi, pr[e]);  // exact residual, one rounding
+            }
+#pragma unroll
+            for (int j = 0; j < NDB; j++) {
+                const h8 b = *(const h8 *)&lds.v[buf][16 * j + col][8 * grp];
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, b, acc[j], 0, 0, 0);
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, b, acc[j], 0, 0, 0);
+            }
+        }
+        if (t + 1 < ntiles) store(buf ^ 1);
+        __syncthreads();
+    }
+    if (!wave_live) return;
+    // ---- row totals; lane (col, grp) holds O rows 4 grp + i at d = 16 j + col
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    float lr[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) lr[i] = __shfl(l, 4 * (int)grp + i);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t rr = rw0 + 4 * grp + i;
+        if (rr >= nrows) continue;
+        const uint32_t tr = rr / GS, hr = rr % GS;
+        float *orow = out + ((uint64_t)(qa + tr) * H + (uint64_t)g * GS + hr) * D;
+        const float inv = 1.0f / lr[i];
+#pragma unroll
+        for (int j = 0; j < NDB; j++) orow[16 * j + col] = acc[j][i] * inv;
+    }
+}
+
+// Prefill, generic form: one wave per (segment, token, query head).
+template <bool Q8>
+__global__ __launch_bounds__(64) void k_prefill_generic(QV_PREFILL_PARAMS) {
+    const uint32_t h = blockIdx.x % H;
+    const uint32_t j = (blockIdx.x / H) % max_tok;
+    const uint32_t seg = blockIdx.x / H / max_tok;
+    if (seg >= n_seg) return;
+    const uint32_t B = (uint32_t)geo.B, G = (uint32_t)geo.G, D = (uint32_t)geo.D;
+    const uint32_t nt = n_tok[seg], p0s = pos0[seg], qa = q_at[seg], tab = table_at[seg];
+    if (j >= nt) return;
+    const bool first = threadIdx.x == 0 && j == 0 && h == 0;
+    if (nt > max_tok || (uint64_t)p0s + nt - 1 > max_pos) {
+        if (first) flag(err, ERR_POS);
+        return;
+    }
+    if ((uint64_t)qa + nt > q_rows) {
+        if (first) flag(err, ERR_OUT);
+        return;
+    }
+    if ((uint64_t)tab + (p0s + nt + B - 1) / B > n_table) {
+        if (first) flag(err, ERR_TABLE);
+        return;
+    }
+    const uint64_t row = (uint64_t)(qa + j) * H + h;
+    generic_body<Q8>(pool, pool_blocks, blocks, tab, p0s + j + 1, h / (H / G), q + row * D,
+                     out + row * D, geo, err);
+}
+
+// =================================================================================
+// Host side.
+// =================================================================================
+
+int check_prefill(const Geometry &g, uint32_t n_seg, uint32_t heads, uint32_t max_tok,
+                  const char **why) {
+    if (heads == 0 || heads % (uint32_t)g.G != 0) {
+        *why = "query heads must be a positive multiple of kv_heads";
+        return QVKV_E_SHAPE;
+    }
+    const bool mfma = g.D == 64 || g.D == 128 || g.D == 256;
+    const uint64_t cols = (uint64_t)max_tok * (heads / (uint32_t)g.G);
+    const uint64_t grid = mfma ? (uint64_t)n_seg * g.G * ((cols + 31) / 32)
+                               : (uint64_t)n_seg * max_tok * heads;
+    if (grid > 0x7fffffffull) {
+        *why = "batch too large";
+        return QVKV_E_SHAPE;
+    }
+    return QVKV_OK;
+}
+
+hipError_t launch_prefill(const Geometry &g, const void *pool, uint64_t pool_blocks,
+                          const float *q, const uint32_t *blocks, uint64_t n_table,
+                          const uint32_t *table_at, const uint32_t *pos0, const uint32_t *q_at,
+                          const uint32_t *n_tok, uint32_t n_seg, uint32_t heads,
+                          uint32_t max_pos, uint32_t max_tok, uint64_t q_rows, float *out,
+                          int *err, hipStream_t s) {
+    if (n_seg == 0 || max_tok == 0) return hipSuccess;
+    const Geo geo = to_geo(g);
+    const uint8_t *pp = (const uint8_t *)pool;
+    const bool q8 = g.dtype == QVKV_Q8_0;
+    if (!(g.D == 64 || g.D == 128 || g.D == 256)) {
+        const unsigned grid = (unsigned)((uint64_t)n_seg * max_tok * heads);
+#define QV_PG(QQ)                                                                              \
+    hipLaunchKernelGGL(k_prefill_generic<QQ>, dim3(grid), dim3(64), 0, s, pp, pool_blocks, q,   \
+                       blocks, n_table, table_at, pos0, q_at, n_tok, n_seg, heads, max_pos,    \
+                       max_tok, q_rows, 0u, out, geo, err)
+        if (q8) QV_PG(true); else QV_PG(false);
+#undef QV_PG
+        return hipGetLastError();
+    }
+    const uint32_t GS = heads / (uint32_t)g.G;
+    if (!q8 && (g.D == 64 || g.D == 128) && tune("QVKV_PREFILL_V2", 1)) {
+        const uint32_t n_qb = (uint32_t)(((uint64_t)max_tok * GS + 63) / 64);
+        const unsigned grid2 = (unsigned)((uint64_t)n_seg * g.G * n_qb);
+#define QV_PF2(DD)                                                                             \
+    hipLaunchKernelGGL((k_prefill_f16<DD>), dim3(grid2), dim3(256), 0, s, pp, pool_blocks, q,   \
+                       blocks, n_table, table_at, pos0, q_at, n_tok, n_seg, heads, max_pos,    \
+                       max_tok, q_rows, n_qb, out, geo, err)
+        if (g.D == 64) { QV_PF2(64); } else { QV_PF2(128); }
+#undef QV_PF2
+        return hipGetLastError();
+    }
+    const uint32_t n_cb = (uint32_t)(((uint64_t)max_tok * GS + 31) / 32);
+    const unsigned grid = (unsigned)((uint64_t)n_seg * g.G * n_cb);
+#define QV_PF(DD, QQ)                                                                          \
+    hipLaunchKernelGGL((k_prefill_mfma<DD, QQ>), dim3(grid), dim3(256), 0, s, pp, pool_blocks,  \
+                       q, blocks, n_table, table_at, pos0, q_at, n_tok, n_seg, heads, max_pos, \
+                       max_tok, q_rows, n_cb, out, geo, err)
+    if (g.D == 64) { if (q8) QV_PF(64, true); else QV_PF(64, false); }
+    else if (g.D == 128) { if (q8) QV_PF(128, true); else QV_PF(128, false); }
+    else { if (q8) QV_PF(256, true); else QV_PF(256, false); }
+#undef QV_PF
+    return hipGetLastError();
+}
+
+}  // namespace qvkv
