@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 import oracle
-from helpers import F16, MAX_ABS, Q8_0, REL_L2, attn_errors, normal, rng, slots_of
+from helpers import F16, MAX_ABS, Q8_0, REL_L2, attn_errors, decode_pool, normal, rng, slots_of
 from test_gpu_kernels import cf32, cu32, fill_items, layout, new_pool
 
 pytestmark = pytest.mark.gpu
@@ -170,3 +170,51 @@ def test_host_entry_routes_a_prefill_chunk_through_segments(hip):
     print(f"  max_abs={max_abs:.2e} rel_l2={rel:.2e}", flush=True)
     assert max_abs <= MAX_ABS and rel <= REL_L2
     buf.close()
+
+
+def _f64_attention(k16, v16, q, g_of, npos):
+    """Exact attention of one query over positions 0..npos-1 (float64)."""
+    s = k16[:npos, g_of] @ q.astype(np.float64) / np.sqrt(q.size)
+    p = np.exp(s - s.max())
+    return p @ v16[:npos, g_of] / p.sum()
+
+
+@pytest.mark.parametrize("kind", ["prefill", "decode"])
+def test_f16_paths_track_float64_closely(hip, kind):
+    """With f16 K/V the products q.k and p.v are exact in the MFMAs (q and p carried as
+    f16 high part + residual), so both attention paths sit within ~1e-6 of float64.
+    Pins the split: a high part and residual taken from two different roundings of
+    the same product (a contraction into v_fma_mix for one of them) leaves one-ulp
+    errors that show up here as ~1e-5, far inside the reference tolerance."""
+    r = rng(77)
+    G, D, H = 4, 128, 32
+    L = layout(F16, G, D)
+    n, nt = 1500, 40
+    N = (n + 15) // 16 + 2
+    pool = new_pool(L, N)
+    blocks, table_at, _ = fill_items(hip, L, pool, N, [n], r)
+    raw = pool.cpu().numpy()
+    dec = decode_pool(raw, L, N)
+    k16 = np.zeros((n, G, D)); v16 = np.zeros((n, G, D))
+    for p in range(n):
+        b, o = blocks[p // 16], p % 16
+        k16[p] = dec["k"][b, :, o].view(np.float16).astype(np.float64)
+        v16[p] = dec["v"][b, :, o].view(np.float16).astype(np.float64)
+    q = normal(r, (nt, H, D))
+    out = torch.zeros(nt * H * D, dtype=torch.float32, device="cuda")
+    if kind == "prefill":
+        hip.prefill_attention(L, pool, N, cf32(q), cu32(blocks), cu32(table_at),
+                              cu32([n - nt]), cu32([0]), cu32([nt]), H, n - 1, nt, out)
+    else:
+        pos = np.arange(n - nt, n, dtype=np.uint32)
+        hip.attention(L, pool, N, cf32(q), cu32(blocks), cu32(np.zeros(nt, np.uint32)),
+                      cu32(pos), H, n - 1, out)
+    hip.check()
+    got = out.cpu().numpy().reshape(nt, H, D)
+    worst = 0.0
+    for j in range(nt):
+        for h in range(H):
+            worst = max(worst, np.abs(got[j, h] - _f64_attention(k16, v16, q[j, h], h // (H // G),
+                                                                 n - nt + j + 1)).max())
+    print(f"  {kind}: max |got - f64| = {worst:.2e}", flush=True)
+    assert worst < 1e-5, worst
