@@ -483,6 +483,7 @@ int qvkv_append(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *pool, const 
     uint64_t held;
     if (int rc = pool_of(dev, pool, g, &held)) return rc;
     if (n == 0) return QVKV_OK;
+    if (!k || !v || !slots) return fail(QVKV_E_SHAPE, "shape mismatch in append: null pointer");
     for (uint32_t r = 0; r < n; r++)
         if (slots[r] / g.B >= held)
             return fail(QVKV_E_SHAPE, "shape mismatch in append: slot %u is in a block past the pool's %llu",
@@ -514,6 +515,8 @@ int qvkv_gather(qvkv_dev *dev, const qvkv_layout *layout, const qvkv_buf *pool,
     if (out_dtype != QVKV_F32 && !(out_dtype == QVKV_F16 && g.dtype == QVKV_F16))
         return fail(QVKV_E_UNSUPPORTED, "hip backend has no gather kernel for this output dtype");
     if (n_items == 0) return QVKV_OK;
+    if (!blocks || !table_at || !lens || !out_at || !out_k || !out_v)
+        return fail(QVKV_E_SHAPE, "shape mismatch in gather: null pointer");
     uint32_t max_len = 0;
     for (uint32_t t = 0; t < n_items; t++) {
         max_len = std::max(max_len, lens[t]);
@@ -557,6 +560,7 @@ int qvkv_block_copy(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *pool,
     if (int rc = geometry(layout, &g)) return rc;
     uint64_t held;
     if (int rc = pool_of(dev, pool, g, &held)) return rc;
+    if (n && (!src || !dst)) return fail(QVKV_E_SHAPE, "shape mismatch in block copy: null pointer");
     for (uint32_t i = 0; i < n; i++)
         if (src[i] >= held || dst[i] >= held)
             return fail(QVKV_E_SHAPE, "shape mismatch in block copy: a block past the pool's %llu",
@@ -649,6 +653,9 @@ int qvkv_decode_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *po
     if (int rc = pool_of(dev, pool, g, &held)) return rc;
     qvkv::AttnPlan p;
     const char *why = "";
+    if (s && (!q || !pos || !blocks || !table_at || !out || (n_sync && (!sync || !sync_to)) ||
+              !k_new || !v_new))
+        return fail(QVKV_E_SHAPE, "shape mismatch in routed moe attention: null pointer");
     uint32_t max_pos = 0;
     for (uint32_t t = 0; t < s; t++) max_pos = std::max(max_pos, pos[t]);
     if (int rc = qvkv::plan_attention(g, s, heads, max_pos, &p, &why))
@@ -762,6 +769,9 @@ int qvkv_prelude_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *p
     const uint32_t heads = p->heads;
     qvkv::AttnPlan plan;
     const char *why = "";
+    if (s && (!q || !k || !v || !pos || !blocks || !table_at || !out ||
+              (n_sync && (!sync || !sync_to))))
+        return fail(QVKV_E_SHAPE, "shape mismatch in routed moe attention: null pointer");
     uint32_t max_pos = 0;
     for (uint32_t t = 0; t < s; t++) max_pos = std::max(max_pos, pos[t]);
     if (int rc = qvkv::plan_attention(g, s, heads, max_pos, &plan, &why))

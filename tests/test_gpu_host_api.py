@@ -185,3 +185,25 @@ def test_concurrent_callers_on_one_device(hip):
     for t in threads:
         t.join()
     assert not errors, errors
+
+
+def test_host_entry_points_reject_null_arrays(hip):
+    """A null array with a non-zero count is a ShapeError, not a host crash."""
+    import ctypes
+
+    from qubivex_amd import KvLayout, ShapeError, _lib
+
+    L = KvLayout("f16", 2, 64, 16)
+    buf = hip.alloc(4 * L.block_bytes)
+    lib, lay, dev, pool = _lib.lib, ctypes.byref(L.c), hip.handle, buf.handle
+    calls = [
+        lambda: lib.qvkv_append(dev, lay, pool, None, None, None, 3),
+        lambda: lib.qvkv_gather(dev, lay, pool, None, 4, None, None, None, 2, _lib.F32, 8, None, None),
+        lambda: lib.qvkv_block_copy(dev, lay, pool, None, None, 2),
+        lambda: lib.qvkv_decode_attention(dev, lay, pool, None, 4, None, 1, None, 1, None, None,
+                                          None, 0, None, None, None),
+    ]
+    for call in calls:
+        with pytest.raises(ShapeError):
+            _lib.check(call())
+    buf.close()
