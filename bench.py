@@ -27,6 +27,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
+PEAK_F16_TFLOPS = 2500.0  # dense f16 MFMA, MI355X
 
 CONFIGS = {
     # layers, kv heads, head dim, q heads, sequences, context (int or (lo, hi)), dtype, outliers
@@ -168,6 +169,10 @@ def main():
     kv_bytes_step = positions * kv_out * 2 * bytes_per_value
     attn_bytes = kv_bytes_step + q.numel() * 4 * 2 + blocks.size * 4 + items * 8
     flops = 4.0 * H * D * positions
+    # MFMA work the decode kernel issues: per 16-position tile of one (item, KV head, chunk
+    # of <= 8 query heads) 2*d/16 v_mfma_f32_16x16x16_f16 (QK^T and PV), 4096 FMA each.
+    hc = (H // G + 7) // 8
+    mfma_flops = float(np.sum((pos.astype(np.float64) + 16) // 16)) * G * hc * (2 * D / 16) * 8192
 
     def step(ev=None):
         dev.append(L, mem, n_blocks, kn, vn, d_slots)
@@ -196,7 +201,8 @@ def main():
         ms_step = wall * 1e3 / args.steps
         result.update(ms_per_step=ms_step, tokens_per_s=S / (ms_step / 1e3), attn_ms=attn_ms,
                       attn_gbs=attn_bytes / (attn_ms / 1e3) / 1e9,
-                      attn_tflops=flops / (attn_ms / 1e3) / 1e12)
+                      attn_tflops=flops / (attn_ms / 1e3) / 1e12,
+                      attn_mfma_tflops=mfma_flops / (attn_ms / 1e3) / 1e12)
         log(f"[bench] decode step {ms_step:.3f} ms ({S / (ms_step / 1e3):.0f} tok/s); attention "
             f"{attn_ms:.3f} ms = {result['attn_gbs']:.0f} GB/s")
 
@@ -283,8 +289,19 @@ def main():
         p_ms = e0.elapsed_time(e1) / reps
         seen = float(np.sum([PF * (int(p) + 1) + PF * (PF - 1) / 2 for p in seg_pos0]))
         p_flops = 4.0 * H * D * seen
+        # MFMA work the f16 prefill kernel issues: per wave (16 query rows) and 32-position
+        # tile up to its last row's position, 2*(d/32)*2 + (d/16)*2 v_mfma_f32_16x16x32_f16
+        # (q and p as f16 high part + residual), 8192 FMA each.
+        GS = H // G
+        rows = PF * GS
+        w_first = np.arange(0, rows, 16)
+        last_tok = np.minimum(PF - 1, (w_first + 15) // GS)
+        tiles = sum(float(np.sum((int(p0) + last_tok + 1 + 31) // 32)) for p0 in seg_pos0) * G
+        p_mfma = tiles * (4 * (D // 32) + 2 * (D // 16)) * 16384.0
         result.update(prefill_ms=p_ms, prefill_tok_s=S * PF / (p_ms / 1e3),
                       prefill_tflops=p_flops / (p_ms / 1e3) / 1e12)
+        if dtype == "f16" and D in (64, 128):  # the LDS-staged 16x16x32 kernel
+            result.update(prefill_mfma_tflops=p_mfma / (p_ms / 1e3) / 1e12)
         log(f"[bench] prefill {S} x {PF} tokens (1 layer, ctx {int(ctx.min())}..{int(ctx.max())}): "
             f"{p_ms:.3f} ms = {result['prefill_tok_s']:.0f} tok/s, {result['prefill_tflops']:.1f} TFLOP/s")
         del qp, op
@@ -348,6 +365,13 @@ def main():
             "append": round(result.get("append_gbs", 0) / PEAK_HBM_GBS, 4),
             "gather": round(result.get("gather_gbs", 0) / PEAK_HBM_GBS, 4),
             "block_copy": round(result.get("copy_gbs", 0) / PEAK_HBM_GBS, 4),
+        }
+        # MFMA issue rate against the dense f16 peak (2.5 PFLOP/s): decode attention is
+        # HBM-bound and uses the matrix cores only for the GQA group contraction.
+        line["mfma_utilisation"] = {
+            "peak_tflops": PEAK_F16_TFLOPS,
+            "attention": round(result["attn_mfma_tflops"] / PEAK_F16_TFLOPS, 4),
+            "prefill": round(result.get("prefill_mfma_tflops", 0) / PEAK_F16_TFLOPS, 4),
         }
     print(json.dumps(line), flush=True)
     pool.close()
