@@ -129,14 +129,20 @@ __global__ __launch_bounds__(256) void k_prefill_mfma(QV_PREFILL_PARAMS) {
 // ---------------------------------------------------------------------------------
 // Paged prefill attention, f16 pools, d = 64 or 128: the MFMA-throughput form.
 // Workgroup = (segment, KV head, block of 64 query rows); row r = token j * GS + head h.
-// The 4 waves stage 32-position K/V tiles once in LDS (K row-major, V transposed,
-// double-buffered: the next tile's global loads are in flight during this tile's math)
-// and each wave computes 16 query rows with v_mfma_f32_16x16x32_f16:
+// The 4 waves stage 32-position K/V tiles once in LDS and each wave computes 16 query
+// rows with v_mfma_f32_16x16x32_f16.  Two ways to stage (the math is shared):
+//   DMA (d = 128, the default): global_load_lds_dwordx4 streams tiles into three slots
+//     two tiles ahead, no staging registers; V stays row-major and the P.V operand comes
+//     from ds_read_b64_tr_b16 (a transposed LDS read); XOR swizzles keep every read
+//     conflict-free;
+//   registers (d = 64): the next tile is loaded into registers during this tile's math
+//     and stored double-buffered, V transposed in registers (v_perm).
+// The MFMAs:
 //   S^T[pos][row] = K . Q^T: A = K rows from LDS (MFMA h, row i <-> position
 //     8(i/4) + 4h + i%4, so lane l ends up holding positions 8(l/16)..8(l/16)+7 of row
 //     l%16), B = q's f16 high part, then its residual (two accumulating MFMAs);
 //   O[row][d] += P . V: A = this lane's 8 probabilities (positions 8(l/16)+t), high part
-//     then residual; B = 8 consecutive positions of one d from the transposed V tile.
+//     then residual; B = 8 consecutive positions of one d.
 // The k index of both MFMAs pairs the same logical element in A and B, so the products
 // are exact f16 x f16 in f32 accumulators as in decode.
 // ---------------------------------------------------------------------------------
@@ -150,8 +156,32 @@ struct PrefillLds {
     _Float16 v[2][D][VR];
 };
 
+// The DMA form's LDS: three tile slots, each K and V for 32 positions, row-major with
+// 16-byte pieces XOR-swizzled inside a row (the DMA writes 1 KiB contiguous per
+// instruction, so rows cannot be padded): K row lr holds piece p at p ^ kswz(lr); V row r
+// at p ^ vswz(r).  The swizzles make the scores' A-operand reads (16 rows, one piece) and
+// the transposed V reads (ds_read_b64_tr_b16: 4 rows x 32 bytes per 16 lanes) hit
+// distinct banks.
 template <int D>
-__global__ __launch_bounds__(256) void k_prefill_f16(QV_PREFILL_PARAMS) {
+struct DmaSlot {
+    _Float16 k[32 * D];
+    _Float16 v[32 * D];
+};
+template <int D>
+__device__ __forceinline__ uint32_t kswz(uint32_t lr) {
+    return (lr / (16u / (D / 8))) % (D / 8);
+}
+template <int D>
+__device__ __forceinline__ uint32_t vswz(uint32_t r) {
+    return D / 8 == 16 ? 2u * ((r & 3u) + 4u * ((r >> 3) & 1u))
+                       : 2u * (((r >> 1) & 1u) + 2u * ((r >> 3) & 1u));
+}
+
+// DMA: the register budget of 3 waves/SIMD (170 VGPRs; the DMA form holds no staging
+// registers): 392 vs 369 TFLOP/s at 2 waves (cfg5).
+template <int D, bool DMA>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DMA ? 3 : 1)))
+void k_prefill_f16(QV_PREFILL_PARAMS) {
     constexpr int TP = PrefillLds<D>::TP;
     constexpr int KS = D / 32;                 // QK k-steps
     constexpr int NDB = D / 16;                // PV d blocks
@@ -159,6 +189,8 @@ __global__ __launch_bounds__(256) void k_prefill_f16(QV_PREFILL_PARAMS) {
     constexpr int LPT = 2 * TP * CPR / 256;    // chunks per thread per tile (K and V)
     static_assert(LPT >= 1 && (2 * TP * CPR) % 256 == 0, "tile / thread mismatch");
     __shared__ PrefillLds<D> lds;
+    __shared__ __attribute__((aligned(16))) DmaSlot<D> s0, s1, s2;
+    if constexpr (!DMA) (void)s0, (void)s1, (void)s2;
 
     const uint32_t G = (uint32_t)geo.G, B = (uint32_t)geo.B;
     const uint32_t GS = H / G;
@@ -254,7 +286,9 @@ __global__ __launch_bounds__(256) void k_prefill_f16(QV_PREFILL_PARAMS) {
     // as zero.
     auto half_base = [&](uint32_t ph) -> const uint8_t * {
         if (ph >= n_wg) return nullptr;
-        const uint32_t blk = blocks[tab + ph / B];
+        // a scalar load (constant address space): it counts on lgkmcnt, so it never waits
+        // behind the vmcnt of tiles still streaming into LDS
+        const uint32_t blk = ((const __attribute__((address_space(4))) uint32_t *)blocks)[tab + ph / B];
         if (blk >= pool_blocks) {
             if (threadIdx.x == 0) flag(err, ERR_BLOCK);
             return nullptr;
@@ -322,80 +356,195 @@ __global__ __launch_bounds__(256) void k_prefill_f16(QV_PREFILL_PARAMS) {
 #pragma unroll
     for (int j = 0; j < NDB; j++) acc[j] = f4{0.f, 0.f, 0.f, 0.f};
 
-    load(0);
-    store(0);
-    __syncthreads();
-    for (uint32_t t = 0; t < ntiles; t++) {
-        const int buf = (int)(t & 1u);
-        if (t + 1 < ntiles) load(t + 1);
-        const uint32_t tp0 = t * TP;
-        if (tp0 < n_wave) {
-            // ---- scores: lane holds positions tp0 + 8 grp + (4h + i) of row `col`
-            f4 s[2];
+    // One tile for this wave's 16 rows.  kread(h, ks): the scores' A operand (K rows 16h +
+    // col, d = 32 ks + 8 grp ..); vread(j): the P.V B operand (positions 8 grp + t of
+    // d = 16 j + col).
+    auto tile = [&](uint32_t tp0, auto kread, auto vread) {
+        if (tp0 >= n_wave) return;
+        // ---- scores: lane holds positions tp0 + 8 grp + (4h + i) of row `col`
+        f4 s[2];
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                s[h] = f4{0.f, 0.f, 0.f, 0.f};
+        for (int h = 0; h < 2; h++) {
+            s[h] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int ks = 0; ks < KS; ks++) {
-                    const h8 a = *(const h8 *)&lds.k[buf][16 * h + col][32 * ks + 8 * grp];
-                    s[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[ks], s[h], 0, 0, 0);
-                    s[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[ks], s[h], 0, 0, 0);
-                }
-            }
-            float sc[8];
-#pragma unroll
-            for (int e = 0; e < 8; e++) sc[e] = s[e >> 2][e & 3];
-            if (tp0 + TP > n_wave_min) {  // the tile reaches some row's causal limit
-#pragma unroll
-                for (int e = 0; e < 8; e++)
-                    if (tp0 + 8u * grp + (uint32_t)e >= n_row) sc[e] = -INFINITY;
-            }
-            float tmax = sc[0];
-#pragma unroll
-            for (int e = 1; e < 8; e++) tmax = fmaxf(tmax, sc[e]);
-            tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-            // Lazy rescale: the reference max m moves only when a row's scores exceed it by
-            // more than 2^8, so probabilities stay <= 256 (exact under the f16 high +
-            // residual split) and the O rescale runs on few tiles.
-            if (__any(tmax > m + 8.0f)) {
-                const float mnew = fmaxf(m, tmax);
-                const float alpha = __builtin_amdgcn_exp2f(m - (mnew == -INFINITY ? 0.0f : mnew));
-                l *= alpha;
-                float ar[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) ar[i] = __shfl(alpha, 4 * (int)grp + i);
-#pragma unroll
-                for (int j = 0; j < NDB; j++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) acc[j][i] *= ar[i];
-                m = mnew;
-            }
-            const float msafe = m == -INFINITY ? 0.0f : m;
-            float pr[8];
-            float psum = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                pr[e] = __builtin_amdgcn_exp2f(sc[e] - msafe);
-                psum += pr[e];
-            }
-            l += psum;
-            h8 ph, pl;
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const _Float16 hi = (_Float16)pr[e];
-                ph[e] = hi;
-                pl[e] = (_Float16)fmaf(-1.0f, (float)hi, pr[e]);  // exact residual, one rounding
-            }
-#pragma unroll
-            for (int j = 0; j < NDB; j++) {
-                const h8 b = *(const h8 *)&lds.v[buf][16 * j + col][8 * grp];
-                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, b, acc[j], 0, 0, 0);
-                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, b, acc[j], 0, 0, 0);
+            for (int ks = 0; ks < KS; ks++) {
+                const h8 a = kread(h, ks);
+                s[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[ks], s[h], 0, 0, 0);
+                s[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[ks], s[h], 0, 0, 0);
             }
         }
-        if (t + 1 < ntiles) store(buf ^ 1);
+        float sc[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) sc[e] = s[e >> 2][e & 3];
+        if (tp0 + TP > n_wave_min) {  // the tile reaches some row's causal limit
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                if (tp0 + 8u * grp + (uint32_t)e >= n_row) sc[e] = -INFINITY;
+        }
+        float tmax = sc[0];
+#pragma unroll
+        for (int e = 1; e < 8; e++) tmax = fmaxf(tmax, sc[e]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        // Lazy rescale: the reference max m moves only when a row's scores exceed it by
+        // more than 2^8, so probabilities stay <= 256 (exact under the f16 high +
+        // residual split) and the O rescale runs on few tiles.
+        if (__any(tmax > m + 8.0f)) {
+            const float mnew = fmaxf(m, tmax);
+            const float alpha = __builtin_amdgcn_exp2f(m - (mnew == -INFINITY ? 0.0f : mnew));
+            l *= alpha;
+            float ar[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) ar[i] = __shfl(alpha, 4 * (int)grp + i);
+#pragma unroll
+            for (int j = 0; j < NDB; j++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[j][i] *= ar[i];
+            m = mnew;
+        }
+        const float msafe = m == -INFINITY ? 0.0f : m;
+        float pr[8];
+        float psum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            pr[e] = __builtin_amdgcn_exp2f(sc[e] - msafe);
+            psum += pr[e];
+        }
+        l += psum;
+        h8 ph, pl;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const _Float16 hi = (_Float16)pr[e];
+            ph[e] = hi;
+            pl[e] = (_Float16)fmaf(-1.0f, (float)hi, pr[e]);  // exact residual, one rounding
+        }
+#pragma unroll
+        for (int j = 0; j < NDB; j++) {
+            const h8 b = vread(j);
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, b, acc[j], 0, 0, 0);
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, b, acc[j], 0, 0, 0);
+        }
+    };
+
+    if constexpr (!DMA) {
+        load(0);
+        store(0);
         __syncthreads();
+        for (uint32_t t = 0; t < ntiles; t++) {
+            const int buf = (int)(t & 1u);
+            if (t + 1 < ntiles) load(t + 1);
+            tile(
+                t * TP,
+                [&](int h, int ks) {
+                    return *(const h8 *)&lds.k[buf][16 * h + col][32 * ks + 8 * grp];
+                },
+                [&](int j) { return *(const h8 *)&lds.v[buf][16 * j + col][8 * grp]; });
+            if (t + 1 < ntiles) store(buf ^ 1);
+            __syncthreads();
+        }
+    } else {
+        // Tiles stream into three LDS slots two tiles ahead with global_load_lds_dwordx4
+        // (each lane's 16 bytes land at slot + 16 * chunk, chunk = thread + 256 u); a tile
+        // with positions past n_wg or a bad block takes the register path and zeros.
+        constexpr int CH = TP * CPR;           // chunks per K (or V) tile
+        constexpr int CPT = 2 * CH / 256;      // chunks per thread per tile
+        static_assert(CH % 64 == 0, "a wave's chunks are all K or all V");
+        auto chunk = [&](uint32_t c, uint32_t &pos, uint32_t &piece, bool &isv) {
+            isv = c >= (uint32_t)CH;
+            const uint32_t cc = isv ? c - CH : c;
+            const uint32_t r = cc / CPR, sp = cc % CPR;
+            if (!isv) {  // LDS row r = 16h + i holds position 8 (i / 4) + 4h + i % 4
+                pos = 8u * ((r & 15u) >> 2) + 4u * (r >> 4) + (r & 3u);
+                piece = sp ^ kswz<D>(r);
+            } else {
+                pos = r;
+                piece = sp ^ vswz<D>(r);
+            }
+        };
+        // pool offsets of the K and V parts of a block, as values (a per-lane choice
+        // between two kernel-argument fields would otherwise load through a vector address)
+        const uint32_t koff = (uint32_t)geo.k_off, voff = (uint32_t)geo.v_off;
+        auto issue = [&](uint32_t t, DmaSlot<D> &sl) {
+            const uint32_t p0 = t * TP;
+            const uint8_t *b0 = half_base(p0), *b1 = half_base(p0 + 16u);
+            const uint32_t valid = n_wg - p0 < (uint32_t)TP ? n_wg - p0 : (uint32_t)TP;
+            const bool full = valid == (uint32_t)TP && b0 != nullptr && b1 != nullptr;  // uniform
+#pragma unroll
+            for (int u = 0; u < CPT; u++) {
+                const uint32_t c = threadIdx.x + 256u * u;
+                uint32_t pos, piece;
+                bool isv;
+                chunk(c, pos, piece, isv);
+                const uint32_t off = (isv ? voff : koff) + ((pos & 15u) * D + piece * 8) * 2u;
+                _Float16 *dst = isv ? sl.v : sl.k;
+                const uint32_t cc = isv ? c - CH : c;
+                if (full) {
+                    // the LDS address is the wave's first chunk; lanes follow at 16 bytes
+                    __builtin_amdgcn_global_load_lds(((pos & 16u) ? b1 : b0) + off,
+                                                     dst + (cc - lane) * 8, 16, 0, 2);
+                } else {
+                    const u4v x = fetch(b0, b1, valid, pos, off);
+                    *(u4v *)(dst + cc * 8) = x;
+                }
+            }
+        };
+        auto kread = [&](DmaSlot<D> &sl) {
+            return [&sl, col = col, grp = grp](int h, int ks) {
+                const uint32_t r = 16u * h + col, p = 4u * ks + grp;
+                return *(const h8 *)(sl.k + (r * CPR + (p ^ kswz<D>(r))) * 8);
+            };
+        };
+        auto vread = [&](DmaSlot<D> &sl) {
+            // lane s of a 16-lane group addresses position 8 grp + 4 hf + s / 4, d = 16 j +
+            // 4 (s % 4): the transposed read hands lane col those 4 positions at d = 16 j + col
+            return [&sl, lane = lane, grp = grp](int j) {
+                const uint32_t sidx = lane & 15u;
+                u2v w[2];
+#pragma unroll
+                for (int hf = 0; hf < 2; hf++) {
+                    const uint32_t r = 8u * grp + 4u * hf + (sidx >> 2);
+                    const uint32_t d = 16u * j + 4u * (sidx & 3u);
+                    const uint32_t p = d >> 3;
+                    const _Float16 *a = sl.v + (r * CPR + (p ^ vswz<D>(r))) * 8 + (d & 7u);
+                    // whole registers only (element-wise copies of the 4 x 16-bit result
+                    // miscompile); the compiler waits for all DMA in flight before this read
+                    // (it cannot prove the slots apart), which measured faster than an asm
+                    // form that avoids the wait but spills
+                    typedef short s4 __attribute__((ext_vector_type(4)));
+                    w[hf] = __builtin_bit_cast(u2v, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                        (__attribute__((address_space(3))) s4 *)a));
+                }
+                return __builtin_bit_cast(h8, u4v{w[0][0], w[0][1], w[1][0], w[1][1]});
+            };
+        };
+        // waits: this thread's chunks of tile t have landed when at most `ahead` tiles'
+        // chunks (CPT instructions each) are still outstanding
+        auto wait_tile = [&](uint32_t t) {
+            if (t + 1 < ntiles) {
+                if constexpr (CPT == 4) __builtin_amdgcn_s_waitcnt(0x0f74);  // vmcnt(4)
+                else __builtin_amdgcn_s_waitcnt(0x0f72);                    // vmcnt(2)
+            } else {
+                __builtin_amdgcn_s_waitcnt(0x0f70);                         // vmcnt(0)
+            }
+        };
+        auto step = [&](uint32_t t, DmaSlot<D> &cur, DmaSlot<D> &nxt) {
+            // Tile t landed everywhere and every wave is past tile t - 1.  A bare barrier:
+            // __syncthreads' fence would also wait for the tiles still in flight.
+            wait_tile(t);
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): register-path LDS stores
+            asm volatile("" ::: "memory");       // no LDS access moves across the barrier
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            if (t + 2 < ntiles) issue(t + 2, nxt);  // into tile t - 1's slot
+            tile(t * TP, kread(cur), vread(cur));
+        };
+        issue(0, s0);
+        if (ntiles > 1) issue(1, s1);
+        for (uint32_t t = 0; t < ntiles; t += 3) {
+            step(t, s0, s2);
+            if (t + 1 < ntiles) step(t + 1, s1, s0);
+            if (t + 2 < ntiles) step(t + 2, s2, s1);
+        }
     }
     if (!wave_live) return;
     // ---- row totals; lane (col, grp) holds O rows 4 grp + i at d = 16 j + col
@@ -489,11 +638,13 @@ hipError_t launch_prefill(const Geometry &g, const void *pool, uint64_t pool_blo
     if (!q8 && (g.D == 64 || g.D == 128) && tune("QVKV_PREFILL_V2", 1)) {
         const uint32_t n_qb = (uint32_t)(((uint64_t)max_tok * GS + 63) / 64);
         const unsigned grid2 = (unsigned)((uint64_t)n_seg * g.G * n_qb);
-#define QV_PF2(DD)                                                                             \
-    hipLaunchKernelGGL((k_prefill_f16<DD>), dim3(grid2), dim3(256), 0, s, pp, pool_blocks, q,   \
-                       blocks, n_table, table_at, pos0, q_at, n_tok, n_seg, heads, max_pos,    \
+#define QV_PF2(DD, DMA)                                                                        \
+    hipLaunchKernelGGL((k_prefill_f16<DD, DMA>), dim3(grid2), dim3(256), 0, s, pp, pool_blocks, \
+                       q, blocks, n_table, table_at, pos0, q_at, n_tok, n_seg, heads, max_pos, \
                        max_tok, q_rows, n_qb, out, geo, err)
-        if (g.D == 64) { QV_PF2(64); } else { QV_PF2(128); }
+        if (g.D == 64) { QV_PF2(64, false); }
+        else if (tune("QVKV_PREFILL_DMA", 1)) { QV_PF2(128, true); }
+        else { QV_PF2(128, false); }
 #undef QV_PF2
         return hipGetLastError();
     }
