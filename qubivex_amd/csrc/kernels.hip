@@ -163,6 +163,13 @@ __global__ __launch_bounds__(256) void k_append(uint8_t *__restrict__ pool, uint
 // ---------------------------------------------------------------------------------
 // Gather.  Workgroup = one 16-position tile of one item, every head, K and V.
 // ---------------------------------------------------------------------------------
+// Output rows are written with non-temporal stores (a pure stream the kernel never reads
+// back): 5.9-6.2 vs 5.6-5.7 TB/s with plain stores at cfg5.
+__device__ __forceinline__ void store_f8(float *dst, const float *y) {
+    __builtin_nontemporal_store(f4v{y[0], y[1], y[2], y[3]}, (f4v *)dst);
+    __builtin_nontemporal_store(f4v{y[4], y[5], y[6], y[7]}, (f4v *)(dst + 4));
+}
+
 template <int DT, int OUT>
 __global__ __launch_bounds__(256) void k_gather(const uint8_t *__restrict__ pool,
                                                 uint64_t pool_blocks,
@@ -226,7 +233,7 @@ __global__ __launch_bounds__(256) void k_gather(const uint8_t *__restrict__ pool
             }
 #pragma unroll
             for (int u = 0; u < U; u++)
-                if (dst[u]) *(u4v *)dst[u] = x[u];
+                if (dst[u]) __builtin_nontemporal_store(x[u], (u4v *)dst[u]);
         }
         return;
     }
@@ -246,13 +253,14 @@ __global__ __launch_bounds__(256) void k_gather(const uint8_t *__restrict__ pool
             const uint4 x = *(const uint4 *)(base + (isv ? geo.v_off : geo.k_off) +
                                               (rowidx * D + e) * 2u);
             if (OUT == QVKV_F16) {
-                *(uint4 *)((uint16_t *)(isv ? out_v : out_k) + o) = x;
+                __builtin_nontemporal_store(u4v{x.x, x.y, x.z, x.w},
+                                            (u4v *)((uint16_t *)(isv ? out_v : out_k) + o));
             } else {
                 h2 a = __builtin_bit_cast(h2, x.x), b = __builtin_bit_cast(h2, x.y);
                 h2 c = __builtin_bit_cast(h2, x.z), d2 = __builtin_bit_cast(h2, x.w);
-                float *dst = (float *)(isv ? out_v : out_k) + o;
-                *(float4 *)dst = make_float4((float)a.x, (float)a.y, (float)b.x, (float)b.y);
-                *(float4 *)(dst + 4) = make_float4((float)c.x, (float)c.y, (float)d2.x, (float)d2.y);
+                const float y[8] = {(float)a.x, (float)a.y, (float)b.x, (float)b.y,
+                                    (float)c.x, (float)c.y, (float)d2.x, (float)d2.y};
+                store_f8((float *)(isv ? out_v : out_k) + o, y);
             }
         } else {  // q8_0 -> f32: y = f32(q) * f32(scale), one multiply (the reference dequant)
             const uint8_t *rowp = base + (isv ? geo.v_off : geo.k_off) + rowidx * D;
@@ -275,9 +283,7 @@ __global__ __launch_bounds__(256) void k_gather(const uint8_t *__restrict__ pool
                     y[t + 1] = (float)(int8_t)(pr >> 8) * sc;
                 }
             }
-            float *dst = (float *)(isv ? out_v : out_k) + o;
-            *(float4 *)dst = make_float4(y[0], y[1], y[2], y[3]);
-            *(float4 *)(dst + 4) = make_float4(y[4], y[5], y[6], y[7]);
+            store_f8((float *)(isv ? out_v : out_k) + o, y);
         }
     }
 }
