@@ -130,14 +130,14 @@ struct Tile {
     bool ok;
 };
 
+// Tile tt (positions 16tt..16tt+15) of block blk (the table entry of position 16tt).
 template <int D, bool Q8, bool NT>
-__device__ __forceinline__ void load_tile(Tile<D, Q8> &t, uint32_t tt, const uint8_t *pool,
-                                          uint64_t pool_blocks, const uint32_t *blocks,
-                                          uint32_t tab, uint32_t g, uint32_t c, uint32_t qg,
-                                          const Geo &geo, int *err) {
+__device__ __forceinline__ void load_tile_of(Tile<D, Q8> &t, uint32_t tt, uint32_t blk,
+                                             const uint8_t *pool, uint64_t pool_blocks,
+                                             uint32_t g, uint32_t c, uint32_t qg,
+                                             const Geo &geo, int *err) {
     const uint32_t B = (uint32_t)geo.B;
     t.p0 = tt * 16u;
-    const uint32_t blk = blocks[tab + t.p0 / B];
     t.ok = blk < pool_blocks;
     if (!t.ok) {
         if ((threadIdx.x & 63u) == 0) flag(err, ERR_BLOCK);
@@ -161,6 +161,15 @@ __device__ __forceinline__ void load_tile(Tile<D, Q8> &t, uint32_t tt, const uin
 #pragma unroll
         for (int i = 0; i < 4; i++) load_bytes<D / 16, NT>(vr + (uint64_t)i * D, t.v[i]);
     }
+}
+
+template <int D, bool Q8, bool NT>
+__device__ __forceinline__ void load_tile(Tile<D, Q8> &t, uint32_t tt, const uint8_t *pool,
+                                          uint64_t pool_blocks, const uint32_t *blocks,
+                                          uint32_t tab, uint32_t g, uint32_t c, uint32_t qg,
+                                          const Geo &geo, int *err) {
+    load_tile_of<D, Q8, NT>(t, tt, blocks[tab + tt * 16u / (uint32_t)geo.B], pool, pool_blocks,
+                            g, c, qg, geo, err);
 }
 
 // Online-softmax state of one lane: running max and partial sum (head c % 8), and the

@@ -393,7 +393,12 @@ __device__ __forceinline__ void attn_body(QV_ATTN_PARAMS) {
     const uint32_t t_end = min(ntiles, t_begin + tpc);
     if (t_begin >= t_end) return;
 
-    const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+    const uint32_t lane = threadIdx.x & 63u;
+    // q8_0: the wave index is made scalar so the tile loop and its address arithmetic run
+    // on the scalar unit, leaving the vector ALUs to the dequantisation (cfg3 +8 %).  The
+    // f16 kernel is faster in its vector-loop form (the scalar loop moved its accumulators
+    // between AGPRs and VGPRs on every tile).
+    const uint32_t w = Q8 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : threadIdx.x >> 6;
     const uint32_t c = lane & 15u, qg = lane >> 4;
     const bool hi_col = c < 8;
     const uint32_t hidx = PK ? (c & 3u) : hc * 8 + (c & 7u);  // query head within the group
@@ -420,10 +425,26 @@ __device__ __forceinline__ void attn_body(QV_ATTN_PARAMS) {
 #pragma unroll
     for (int j = 0; j < NJ; j++) st.acc[j] = f4{0.f, 0.f, 0.f, 0.f};
 
-    for (uint32_t tt = t_begin + w; tt < t_end; tt += 4) {
-        Tile<D, Q8> cur;
-        load_tile<D, Q8, NT>(cur, tt, pool, pool_blocks, blocks, tab, g, c, qg, geo, err);
-        compute_tile<D, Q8, PK>(cur, st, qf, n, n, qg, hi_col, sigma);
+    if constexpr (Q8) {
+        // The table entries of the wave's next 64 tiles are fetched one per lane ahead of
+        // the tiles; a tile's block id is then a lane read into a scalar register.
+        uint32_t ids = 0;
+        for (uint32_t tt = t_begin + w, k = 0; tt < t_end; tt += 4, k = (k + 1) & 63u) {
+            if (k == 0) {
+                const uint32_t tl = tt + 4u * lane;
+                ids = tl < t_end ? blocks[tab + tl * 16u / B] : 0u;
+            }
+            Tile<D, Q8> cur;
+            load_tile_of<D, Q8, NT>(cur, tt, __builtin_amdgcn_readlane(ids, k), pool, pool_blocks,
+                                    g, c, qg, geo, err);
+            compute_tile<D, Q8, PK>(cur, st, qf, n, n, qg, hi_col, sigma);
+        }
+    } else {
+        for (uint32_t tt = t_begin + w; tt < t_end; tt += 4) {
+            Tile<D, Q8> cur;
+            load_tile<D, Q8, NT>(cur, tt, pool, pool_blocks, blocks, tab, g, c, qg, geo, err);
+            compute_tile<D, Q8, PK>(cur, st, qf, n, n, qg, hi_col, sigma);
+        }
     }
     float l = st.l;
     const float m = st.m;
