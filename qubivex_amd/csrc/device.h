@@ -68,6 +68,25 @@ __device__ __forceinline__ h4 i8x4_to_h4(uint32_t w) {
     return h4{a.x, a.y, b.x, b.y};
 }
 
+// x + x of lane l ^ 8: within each row of 16 lanes, a DPP rotate by 8.
+__device__ __forceinline__ float add_xor8(float x) {
+    return x + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x),
+                                                                  0x128 /* row_ror:8 */, 0xf,
+                                                                  0xf, false));
+}
+
+// max of x over lanes l, l ^ 16, l ^ 32, l ^ 48.  v_permlane16_swap (vdst, vsrc both x)
+// leaves x of rows (0, 0, 2, 2) in one result and (1, 1, 3, 3) in the other; the max of
+// the two is the max over l and l ^ 16.  v_permlane32_swap does the same for halves.
+__device__ __forceinline__ float max_xor16_32(float x) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    x = fmaxf(__builtin_bit_cast(float, a[0]), __builtin_bit_cast(float, a[1]));
+    const uint32_t v = __builtin_bit_cast(uint32_t, x);
+    const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return fmaxf(__builtin_bit_cast(float, b[0]), __builtin_bit_cast(float, b[1]));
+}
+
 // f32 -> (high f16, residual f16); lane columns < 8 take the high part.
 // f32 product rounded once to f32, never fused into a later f16 conversion: the high
 // part and the residual of a split must both come from this one rounded value.  hipcc
@@ -77,6 +96,14 @@ __device__ __forceinline__ h4 i8x4_to_h4(uint32_t w) {
 __device__ __forceinline__ float mul_rn(float a, float b) {
     float y = a * b;
     asm volatile("" : "+v"(y));  // the rounded f32 value, opaque to later fusion
+    return y;
+}
+
+// a * b rounded once, with 0 * x = 0 for every x (NaN and inf included): v_mul_legacy_f32.
+// Opaque to the compiler, so never contracted into a later operation either.
+__device__ __forceinline__ float mul_legacy(float a, float b) {
+    float y;
+    asm("v_mul_legacy_f32 %0, %1, %2" : "=v"(y) : "v"(a), "v"(b));
     return y;
 }
 
@@ -222,14 +249,13 @@ __device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<
     float sc[4];
     const bool partial = p0 + 16u > n_max;  // wave-uniform
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        float v2 = s[i] + __shfl_xor(s[i], 8);
-        if (p0 + 4 * qg + i >= n_col) v2 = -INFINITY;
-        sc[i] = v2;
+    for (int i = 0; i < 4; i++) sc[i] = add_xor8(s[i]);
+    if (__any(p0 + 16u > n_col)) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (p0 + 4 * qg + i >= n_col) sc[i] = -INFINITY;
     }
-    float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float tmax = max_xor16_32(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
     const float mnew = fmaxf(st.m, tmax);
     const float msafe = mnew == -INFINITY ? 0.0f : mnew;
     const float alpha = __builtin_amdgcn_exp2f(st.m - msafe);
@@ -271,13 +297,15 @@ __device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<
         // int8 exactly as f16.  The rows' scales of group j/2 fold into the probabilities
         // (P' = p * scale in f32, then f16 high part + residual: exact to ~2^-22), so the
         // products the MFMA forms are exact.
+        // Rows at or past n_max (a partial tile only) have p = 0 exactly (score -inf).  Their
+        // int8 values are finite whatever the slot holds, so 0 * value = 0 in the MFMA; their
+        // scales may be any f16 bits (NaN, inf) and are folded in with v_mul_legacy_f32,
+        // whose 0 * x is 0 for every x.  No row needs masking.
         uint32_t vsw[4][Tile<D, Q8>::VW];  // biased bytes x ^ 0x80
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const bool dead = partial && p0 + 4 * qg + i >= n_max;
+        for (int i = 0; i < 4; i++)
 #pragma unroll
-            for (int x = 0; x < Tile<D, Q8>::VW; x++) vsw[i][x] = dead ? 0x80808080u : vw[i][x] ^ 0x80808080u;
-        }
+            for (int x = 0; x < Tile<D, Q8>::VW; x++) vsw[i][x] = vw[i][x] ^ 0x80808080u;
         const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
         const float lo_part = hi_col ? 0.0f : 1.0f;
         // The A operand of scaled probabilities for group g (this lane's scale pick).
@@ -285,8 +313,7 @@ __device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<
             _Float16 pg[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                float x = mul_rn(pr[i], sc_of_row[i]);
-                if (partial && p0 + 4 * qg + i >= n_max) x = 0.0f;  // a never-written slot's scale
+                const float x = mul_legacy(pr[i], sc_of_row[i]);
                 const _Float16 u = (_Float16)x;
                 pg[i] = (_Float16)fmaf(-lo_part, (float)u, x);  // u, or the residual x - u
             }
