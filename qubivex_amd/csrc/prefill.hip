@@ -384,8 +384,7 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
         float tmax = sc[0];
 #pragma unroll
         for (int e = 1; e < 8; e++) tmax = fmaxf(tmax, sc[e]);
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        tmax = max_xor16_32(tmax);
         // Lazy rescale: the reference max m moves only when a row's scores exceed it by
         // more than 2^8, so probabilities stay <= 256 (exact under the f16 high +
         // residual split) and the O rescale runs on few tiles.
