@@ -478,9 +478,11 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
                 _Float16 *dst = isv ? sl.v : sl.k;
                 const uint32_t cc = isv ? c - CH : c;
                 if (full) {
-                    // the LDS address is the wave's first chunk; lanes follow at 16 bytes
+                    // the LDS address is the wave's first chunk; lanes follow at 16 bytes.
+                    // Cached loads (aux 0): the n_cb workgroups of a (segment, KV head) read
+                    // the same tiles and share them through the XCD's L2.
                     __builtin_amdgcn_global_load_lds(((pos & 16u) ? b1 : b0) + off,
-                                                     dst + (cc - lane) * 8, 16, 0, 2);
+                                                     dst + (cc - lane) * 8, 16, 0, 0);
                 } else {
                     const u4v x = fetch(b0, b1, valid, pos, off);
                     *(u4v *)(dst + cc * 8) = x;

@@ -230,6 +230,45 @@ def test_attention_within_tolerance(hip, dtype, H, G, D, lens):
     assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)
 
 
+@pytest.mark.parametrize("dtype", [F16, Q8_0])
+def test_attention_ignores_nan_in_unwritten_slots(hip, dtype):
+    """Slots past each item's last position hold 0xFF bytes: NaN f16 values and NaN q8_0
+    scales.  Partial tiles read them; decode and prefill must mask them exactly (q8_0 folds
+    the V scale into p with a multiply whose 0 * NaN is 0)."""
+    r = rng(410 + (dtype == Q8_0))
+    G, D, H = 4, 128, 16
+    L = layout(dtype, G, D)
+    lens = [1, 7, 17, 250]
+    N = sum((n + 15) // 16 for n in lens) + 2
+    pool = torch.full((N * L.block_bytes,), 0xFF, dtype=torch.uint8, device="cuda")
+    blocks, table_at, sim = fill_items(hip, L, pool, N, lens, r)
+    q = normal(r, (len(lens), H, D))
+    pos = np.array(lens, np.uint32) - 1
+    out = torch.full((len(lens) * H * D,), float("nan"), dtype=torch.float32, device="cuda")
+    hip.attention(L, pool, N, cf32(q), cu32(blocks), cu32(table_at), cu32(pos), H, int(pos.max()), out)
+    hip.check()
+    got = out.cpu().numpy().reshape(len(lens), H, D)
+    assert np.isfinite(got).all()
+    e = attn_errors(got, sim.attention(q, H, blocks, table_at, pos))
+    assert e[0] <= MAX_ABS and e[1] <= REL_L2, e
+    # prefill of every item's last min(n, 9) tokens
+    n_tok = np.minimum(np.array(lens), 9).astype(np.uint32)
+    pos0 = (np.array(lens) - n_tok).astype(np.uint32)
+    q_at = np.concatenate([[0], np.cumsum(n_tok)[:-1]]).astype(np.uint32)
+    T = int(n_tok.sum())
+    qp = normal(r, (T, H, D))
+    outp = torch.full((T * H * D,), float("nan"), dtype=torch.float32, device="cuda")
+    hip.prefill_attention(L, pool, N, cf32(qp), cu32(blocks), cu32(table_at), cu32(pos0),
+                          cu32(q_at), cu32(n_tok), H, int(max(lens)) - 1, int(n_tok.max()), outp)
+    hip.check()
+    gp = outp.cpu().numpy().reshape(T, H, D)
+    assert np.isfinite(gp).all()
+    ta = np.repeat(table_at, n_tok).astype(np.uint32)
+    pt = np.concatenate([np.arange(p, p + m) for p, m in zip(pos0, n_tok)]).astype(np.uint32)
+    e = attn_errors(gp, sim.attention(qp, H, blocks, ta, pt))
+    assert e[0] <= MAX_ABS and e[1] <= REL_L2, e
+
+
 def test_attention_split_context_8k(hip):
     """One long item alone: the launch splits the context and merges the partials."""
     r = rng(7)
