@@ -127,13 +127,25 @@ __global__ __launch_bounds__(256) void k_append(uint8_t *__restrict__ pool, uint
             amax = fmaxf(amax, __shfl_xor(amax, 2));
             const float d = amax / 127.0f;
             const float inv = d > 0.0f ? 1.0f / d : 0.0f;
-            uint32_t qb[2] = {0, 0};
+            // roundf (half away from zero), NaN -> 0, clamp to +-127, as three instructions
+            // per value: for |y| < 2^23, trunc(y + copysign(0.49999997, y)) equals roundf(y)
+            // for every f32 (checked exhaustively); v_cvt_i32_f32 truncates, maps NaN to 0
+            // and saturates +-inf; the clamp is then integer.  y is one rounded product.
+            int qi[8];
 #pragma unroll
             for (int t = 0; t < 8; t++) {
-                float r = roundf(xs[t] * inv);
-                r = (r != r) ? 0.0f : fminf(fmaxf(r, -127.0f), 127.0f);
-                const uint32_t b = (uint32_t)(uint8_t)(int8_t)(int)r;
-                qb[t >> 2] |= b << (8 * (t & 3));
+                const float y = mul_rn(xs[t], inv);
+                const float yr = y + __builtin_copysignf(0.49999997f, y);
+                int ri;
+                asm("v_cvt_i32_f32 %0, %1" : "=v"(ri) : "v"(yr));
+                qi[t] = min(max(ri, -127), 127);
+            }
+            uint32_t qb[2];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const uint32_t lo = __builtin_amdgcn_perm((uint32_t)qi[4 * h + 1], (uint32_t)qi[4 * h], 0x0c0c0400u);
+                const uint32_t hi = __builtin_amdgcn_perm((uint32_t)qi[4 * h + 3], (uint32_t)qi[4 * h + 2], 0x0c0c0400u);
+                qb[h] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
             }
             const uint32_t grp = i >> 5;
             if (!isv) {
@@ -145,10 +157,30 @@ __global__ __launch_bounds__(256) void k_append(uint8_t *__restrict__ pool, uint
                 }
             } else {
                 uint8_t *dst = base + geo.v_off + rowidx * D;
+                if (D == 128u) {
+                    // V bytes sit at vperm(d) = 8 (d % 32 / 2) + 2 (d / 32) + d % 2: the 8-byte
+                    // chunk m holds value pair m of all four 32-groups.  The lanes 4g + o
+                    // (g = group, o = i % 32 / 8) of a head row hold pairs 4o..4o+3 of group g;
+                    // a 4 x 4 exchange over lanes ^ 4, ^ 8, ^ 12 hands lane 4g + o chunk
+                    // 4o + g whole, and the row's 16 lanes write its 128 bytes contiguously.
+                    const uint32_t gl = (threadIdx.x >> 2) & 3u;  // this lane's group g
+                    auto pair_of = [&](uint32_t m) { return (qb[m >> 1] >> (16u * (m & 1u))) & 0xffffu; };
+                    uint32_t part[4];
+                    part[gl] = pair_of(gl);
 #pragma unroll
-                for (int t = 0; t < 8; t += 2) {
-                    const uint32_t pair = (qb[t >> 2] >> (8 * (t & 3))) & 0xffffu;
-                    *(uint16_t *)(dst + vperm(i + t, D)) = (uint16_t)pair;
+                    for (uint32_t r = 1; r < 4; r++) {
+                        // lane g sends its pair g ^ r to lane g ^ r, which wants pair g ^ r
+                        const uint32_t got = (uint32_t)__shfl_xor((int)pair_of(gl ^ r), (int)(4u * r));
+                        part[gl ^ r] = got;
+                    }
+                    const uint32_t m = (i & 31u) / 2u + gl;  // this lane's chunk
+                    *(uint2 *)(dst + 8u * m) = make_uint2(part[0] | (part[1] << 16), part[2] | (part[3] << 16));
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 8; t += 2) {
+                        const uint32_t pair = (qb[t >> 2] >> (8 * (t & 3))) & 0xffffu;
+                        *(uint16_t *)(dst + vperm(i + t, D)) = (uint16_t)pair;
+                    }
                 }
                 if ((i & 31u) == 0) {
                     _Float16 sh = (_Float16)d;

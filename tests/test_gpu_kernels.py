@@ -94,6 +94,10 @@ def q8_case(r, n, G, D):
     grp[2, 5] = 40.0
     if grp.shape[0] > 3:
         grp[3, 7] = np.nan
+    if grp.shape[0] > 5:
+        grp[4] = np.float32(3e-39)  # subnormal amax: 1 / d overflows to inf
+        grp[4, 1] = np.float32(-1e-40)
+        grp[5] = np.float32(0.5) * np.arange(-16, 16, dtype=np.float32) * np.float32(127 / 15.5)
     gv = v[0].reshape(-1, 32)
     gv[0] = 1e-30  # scale underflows f16 (subnormal / zero)
     gv[1, 3] = np.inf
