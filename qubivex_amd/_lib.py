@@ -2,7 +2,7 @@
 
 The library is required: importing this module without a built library raises, so no
 caller can silently fall back to anything else.  Build it with
-``python -m qubivex_amd.build`` (or ``__graft_entry__.build()``).
+``python qubivex_amd/build.py`` (or ``__graft_entry__.build()``).
 """
 import ctypes
 import os
@@ -77,7 +77,7 @@ class PrefixStats(ctypes.Structure):
 def _load():
     if not os.path.exists(LIB):
         raise ImportError(
-            f"libqvkv.so is not built ({LIB}); run `python -m qubivex_amd.build` first")
+            f"libqvkv.so is not built ({LIB}); run `python qubivex_amd/build.py` (or __graft_entry__.build()) first")
     return ctypes.CDLL(LIB)
 
 
