@@ -7,6 +7,7 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include "fastdiv.h"
 #include "internal.h"
 
 namespace qvkv {
@@ -15,6 +16,7 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef float f4v __attribute__((ext_vector_type(4)));
+typedef float f2v __attribute__((ext_vector_type(2)));
 typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 
 enum : int { ERR_BLOCK = 1, ERR_TABLE = 2, ERR_POS = 4, ERR_OUT = 8 };
@@ -24,11 +26,13 @@ struct Geo {  // kernel-side copy of Geometry
     uint32_t kv_out;
     uint64_t bb, k_off, ks_off, v_off, vs_off;
     uint32_t xcd_map;  // attention: XCD-aware workgroup order
+    FastDiv fd_b;      // division by B
 };
 
 inline Geo to_geo(const Geometry &g) {
     return Geo{g.dtype, g.G, g.D, g.B, (uint32_t)g.kv_out, g.block_bytes,
-               g.k_off, g.ks_off, g.v_off, g.vs_off, (uint32_t)tune("QVKV_ATTN_XCD", 1)};
+               g.k_off, g.ks_off, g.v_off, g.vs_off, (uint32_t)tune("QVKV_ATTN_XCD", 1),
+               FastDiv((uint32_t)g.B)};
 }
 
 __device__ __forceinline__ void flag(int *err, int bit) { atomicOr(err, bit); }

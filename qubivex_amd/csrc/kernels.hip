@@ -41,60 +41,99 @@ __device__ __forceinline__ float4 load_f4(const float *p) {
     }
 }
 
-// One 8-value chunk: where it comes from and where it goes.
+// One 8-value chunk: where it comes from and where it goes.  Work item w of a launch is
+// chunk w % (2 cpr) of row w / (2 cpr): K chunks first, then V.  The divisions by 2 cpr and
+// by B are invariant multiplications; DD is the head dim when known at compile time.
 struct AppendItem {
     const float *src;
     uint8_t *base;     // its block
-    uint64_t rowidx;   // (head, position) row inside the K or V region
+    uint32_t rowidx;   // (head, position) row inside the K or V region
     uint32_t i;        // first value's index along d
     bool isv, ok;
 };
 
-__device__ __forceinline__ AppendItem append_item(uint32_t w, uint32_t total, uint32_t cpr,
-                                                  uint8_t *pool, uint64_t pool_blocks,
-                                                  const float *k, const float *v,
-                                                  const uint32_t *slots, const Geo &geo,
-                                                  int *err) {
+// Tile order (d known at compile time): work items run over tiles of 16 consecutive rows;
+// inside a tile, K heads then V heads, and for each head its 16 rows of D/8 lanes.  A
+// workgroup thus covers 16 rows of one head (d = 128), and when the rows are consecutive
+// positions of a block (a prefill chunk) its stores fill one contiguous block tile instead
+// of short pieces of many.  fd_row divides by 16 * 2 * cpr; items past row n are padding.
+struct RowChunk {
+    uint32_t row, g, m;  // row, head, 8-value chunk within the head's row
+    bool isv;
+};
+template <int DD>
+__device__ __forceinline__ RowChunk row_tile_order(uint32_t w, uint32_t cpr, FastDiv fd_tile) {
+    constexpr uint32_t LPR = DD / 8, PER_HEAD = 16u * LPR;
+    RowChunk rc;
+    const uint32_t tile = fd_tile.div(w);
+    const uint32_t rem = w - tile * 32u * cpr;
+    const uint32_t hv = rem / PER_HEAD;     // K heads 0..G-1, then V heads
+    const uint32_t G = cpr / LPR;
+    rc.isv = hv >= G;
+    rc.g = rc.isv ? hv - G : hv;
+    const uint32_t inh = rem % PER_HEAD;
+    rc.row = tile * 16u + inh / LPR;
+    rc.m = inh % LPR;
+    return rc;
+}
+
+template <int DD>
+__device__ __forceinline__ AppendItem append_item(uint32_t w, uint32_t total, uint32_t n,
+                                                  uint32_t cpr,
+                                                  FastDiv fd_row, uint8_t *pool,
+                                                  uint64_t pool_blocks, const float *k,
+                                                  const float *v, const uint32_t *slots,
+                                                  const Geo &geo, int *err) {
     AppendItem it{};
     it.ok = false;
     if (w >= total) return it;
-    const uint32_t D = (uint32_t)geo.D, B = (uint32_t)geo.B;
-    const uint32_t row = w / (2u * cpr);
-    const uint32_t rem = w - row * 2u * cpr;
-    it.isv = rem >= cpr;
-    const uint32_t e = (it.isv ? rem - cpr : rem) * 8u;
-    const uint32_t g = e / D;
-    it.i = e - g * D;
+    const uint32_t D = DD ? (uint32_t)DD : (uint32_t)geo.D;
+    uint32_t row, g;
+    if constexpr (DD != 0) {
+        const RowChunk rc = row_tile_order<DD>(w, cpr, fd_row);
+        if (rc.row >= n) return it;
+        row = rc.row;
+        it.isv = rc.isv;
+        g = rc.g;
+        it.i = rc.m * 8u;
+    } else {
+        row = fd_row.div(w);
+        const uint32_t rem = w - row * 2u * cpr;
+        it.isv = rem >= cpr;
+        const uint32_t e = (it.isv ? rem - cpr : rem) * 8u;
+        g = e / D;
+        it.i = e - g * D;
+    }
     const uint32_t slot = slots[row];
-    const uint32_t blk = slot / B;
+    const uint32_t blk = geo.fd_b.div(slot);
     if (blk >= pool_blocks) {  // whole rows: every lane of a q8_0 group agrees
         flag(err, ERR_BLOCK);
         return it;
     }
-    it.src = (it.isv ? v : k) + (uint64_t)row * geo.kv_out + e;
+    it.src = (it.isv ? v : k) + (uint64_t)row * geo.kv_out + g * D + it.i;
     it.base = pool + (uint64_t)blk * geo.bb;
-    it.rowidx = (uint64_t)g * B + (slot - blk * B);
+    it.rowidx = g * (uint32_t)geo.B + (slot - blk * (uint32_t)geo.B);
     it.ok = true;
     return it;
 }
 
 // U chunks per thread per round, all loads issued before any store.
-template <int DT, int U, bool NT>
+template <int DT, int U, bool NT, int DD>
 __global__ __launch_bounds__(256) void k_append(uint8_t *__restrict__ pool, uint64_t pool_blocks,
                                                 const float *__restrict__ k,
                                                 const float *__restrict__ v,
                                                 const uint32_t *__restrict__ slots, uint32_t n,
-                                                Geo geo, int *err) {
+                                                FastDiv fd_row, Geo geo, int *err) {
     const uint32_t cpr = geo.kv_out >> 3;  // 8-value chunks per K (or V) row
-    const uint32_t total = n * 2u * cpr;
-    const uint32_t D = (uint32_t)geo.D;
+    const uint32_t total = (DD ? (n + 15u) / 16u * 16u : n) * 2u * cpr;
+    const uint32_t D = DD ? (uint32_t)DD : (uint32_t)geo.D;
     for (uint32_t b0 = blockIdx.x * 256u * U; b0 < total; b0 += gridDim.x * 256u * U) {
         AppendItem its[U];
         float4 xa[U], xb[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            its[u] = append_item(b0 + u * 256u + threadIdx.x, total, cpr, pool, pool_blocks, k, v,
-                                 slots, geo, err);
+            its[u] = append_item<DD>(b0 + u * 256u + threadIdx.x, total, n, cpr, fd_row, pool,
+                                     pool_blocks, k, v, slots, geo, err);
             if (its[u].ok) {
                 xa[u] = load_f4<NT>(its[u].src);
                 xb[u] = load_f4<NT>(its[u].src + 4);
@@ -105,7 +144,7 @@ __global__ __launch_bounds__(256) void k_append(uint8_t *__restrict__ pool, uint
         if (!its[u].ok) continue;
         const float4 x0 = xa[u], x1 = xb[u];
         uint8_t *base = its[u].base;
-        const uint64_t rowidx = its[u].rowidx;
+        const uint64_t rowidx = its[u].rowidx;  // < 2^32: G * B rows per block
         const uint32_t i = its[u].i;
         const bool isv = its[u].isv;
         if (DT == QVKV_F16) {
@@ -188,6 +227,198 @@ __global__ __launch_bounds__(256) void k_append(uint8_t *__restrict__ pool, uint
                 }
             }
         }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// q8_0 append for d = 64, 128, 256.  A (head, position) row of K or V is D/8 lanes; lane
+// m of a row produces the 8 stored bytes at 8m of its K or V row, so every lane stores
+// one aligned 8-byte piece and no bytes change lanes:
+//   K: the piece at q*(D/4) + 8i holds logical d = 32i + 8q .. +7, so lane m loads
+//      values 8m .. 8m+7 (i = m/4, q = m%4): its group is its quad;
+//   V: byte c*(D/16) + 2g + u holds d = 32g + 2c + u, so lane m loads the 4 value pairs
+//      of bytes 8m + 2j, j = 0..3; a group's pairs lie in lanes of one row.
+// Group maxima are all-reduced over the lanes that hold the group with DPP row moves.
+// Each lane divides for one group (amax / 127, then 1 / d, correctly rounded like the
+// reference's f32 arithmetic) and a quad-broadcast hands the others their inverse.
+// ---------------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+    // every lane read is in the executing set (rows are whole); bound_ctrl lets the move
+    // fold into the consuming instruction as a DPP operand
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL,
+                                                              0xF, 0xF, true));
+}
+enum : int { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_ROR4 = 0x124, DPP_ROR8 = 0x128,
+             DPP_HALF_MIRROR = 0x141 };
+template <int S>  // quad_perm [S, S, S, S]: every lane of a quad reads quad lane S
+__device__ __forceinline__ float quad_bcast(float x) { return dpp_f<S * 0x55>(x); }
+
+// roundf (half away from zero), NaN -> 0, clamp to +-127, as four instructions per value:
+// for |y| < 2^23, trunc(y + copysign(0.49999997, y)) equals roundf(y) for every f32;
+// v_cvt_i32_f32 truncates, maps NaN to 0 and saturates +-inf; the clamp is integer.
+// y is one rounded product (as the reference's x * inv).
+__device__ __forceinline__ int quant_q8(float x, float inv) {
+    const float y = mul_rn(x, inv);
+    const float yr = y + __builtin_copysignf(0.49999997f, y);
+    int ri;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(ri) : "v"(yr));
+    return min(max(ri, -127), 127);
+}
+__device__ __forceinline__ uint32_t pack_q4(int a, int b, int c, int d) {
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x0c0c0400u);
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+template <bool NTS>
+__device__ __forceinline__ void st_u2(uint8_t *p, uint32_t a, uint32_t b) {
+    if constexpr (NTS) __builtin_nontemporal_store(u2v{a, b}, (u2v *)p);
+    else *(u2v *)p = u2v{a, b};
+}
+__device__ __forceinline__ void q8_scale(float amax, float &d, float &inv) {
+    d = amax / 127.0f;
+    inv = d > 0.0f ? 1.0f / d : 0.0f;
+}
+
+template <int U, int MODE, int D>
+__global__ __launch_bounds__(256) void k_append_q8(uint8_t *__restrict__ pool,
+                                                   uint64_t pool_blocks,
+                                                   const float *__restrict__ k,
+                                                   const float *__restrict__ v,
+                                                   const uint32_t *__restrict__ slots,
+                                                   uint32_t n, FastDiv fd_row, Geo geo,
+                                                   int *err) {
+    static_assert(D == 64 || D == 128 || D == 256, "d");
+    constexpr bool NT = MODE & 1, NTS = MODE & 2;  // non-temporal loads / stores
+    constexpr uint32_t P16 = D / 16;   // V: bytes per c
+    const uint32_t cpr = geo.kv_out >> 3;
+    const uint32_t total = (n + 15u) / 16u * 16u * 2u * cpr;
+    const uint32_t B = (uint32_t)geo.B;
+    for (uint32_t b0 = blockIdx.x * 256u * U; b0 < total; b0 += gridDim.x * 256u * U) {
+        float x[U][8];
+        uint8_t *rowk[U];   // the row's first byte in the K or V region
+        uint8_t *rows[U];   // the row's first scale
+        bool isv[U];
+        uint32_t mm[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            rowk[u] = nullptr;
+            const uint32_t w = b0 + u * 256u + threadIdx.x;
+            if (w >= total) continue;
+            const RowChunk rc = row_tile_order<D>(w, cpr, fd_row);
+            if (rc.row >= n) continue;
+            const uint32_t row = rc.row, g = rc.g, m = rc.m;
+            isv[u] = rc.isv;
+            mm[u] = m;
+            const uint32_t slot = slots[row];
+            const uint32_t blk = geo.fd_b.div(slot);
+            if (blk >= pool_blocks) {  // whole rows: every lane of a group agrees
+                flag(err, ERR_BLOCK);
+                continue;
+            }
+            const uint32_t rowidx = g * B + (slot - blk * B);
+            uint8_t *base = pool + (uint64_t)blk * geo.bb;
+            rowk[u] = base + (isv[u] ? geo.v_off : geo.k_off) + (uint64_t)rowidx * D;
+            rows[u] = base + (isv[u] ? geo.vs_off : geo.ks_off) + (uint64_t)rowidx * (D / 16);
+            const float *src = (isv[u] ? v : k) + (uint64_t)row * geo.kv_out + g * D;
+            if (!isv[u]) {
+                const float4 a = load_f4<NT>(src + 8u * m), b = load_f4<NT>(src + 8u * m + 4);
+                x[u][0] = a.x; x[u][1] = a.y; x[u][2] = a.z; x[u][3] = a.w;
+                x[u][4] = b.x; x[u][5] = b.y; x[u][6] = b.z; x[u][7] = b.w;
+            } else {
+#pragma unroll
+                for (uint32_t j = 0; j < 4; j++) {
+                    const uint32_t by = 8u * m + 2u * j;
+                    const uint32_t dd = 32u * ((by % P16) / 2u) + 2u * (by / P16);
+                    const float2 p = *(const float2 *)(src + dd);
+                    x[u][2 * j] = p.x;
+                    x[u][2 * j + 1] = p.y;
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (!rowk[u]) continue;
+            const uint32_t m = mm[u];
+            int qi[8];
+            if (!isv[u]) {
+                float amax = 0.0f;
+#pragma unroll
+                for (int t = 0; t < 8; t++) amax = fmaxf(amax, fabsf(x[u][t]));
+                amax = fmaxf(amax, dpp_f<DPP_XOR1>(amax));
+                amax = fmaxf(amax, dpp_f<DPP_XOR2>(amax));
+                float d, inv;
+                q8_scale(amax, d, inv);
+#pragma unroll
+                for (int t = 0; t < 8; t++) qi[t] = quant_q8(x[u][t], inv);
+                st_u2<NTS>(rowk[u] + (m & 3u) * (D / 4) + (m >> 2) * 8u,
+                           pack_q4(qi[0], qi[1], qi[2], qi[3]), pack_q4(qi[4], qi[5], qi[6], qi[7]));
+                if ((m & 3u) == 0) *(_Float16 *)(rows[u] + (m >> 2) * 2u) = (_Float16)d;
+            } else {
+                float pm[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) pm[j] = fmaxf(fabsf(x[u][2 * j]), fabsf(x[u][2 * j + 1]));
+                float inv[4], dsc;
+                if constexpr (D == 128) {
+                    // pair j is group j; the group spans the row's 16 lanes
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        pm[j] = fmaxf(pm[j], dpp_f<DPP_XOR1>(pm[j]));
+                        pm[j] = fmaxf(pm[j], dpp_f<DPP_XOR2>(pm[j]));
+                        pm[j] = fmaxf(pm[j], dpp_f<DPP_ROR4>(pm[j]));
+                        pm[j] = fmaxf(pm[j], dpp_f<DPP_ROR8>(pm[j]));
+                    }
+                    const uint32_t sel = m & 3u;
+                    const float a = sel == 0 ? pm[0] : sel == 1 ? pm[1] : sel == 2 ? pm[2] : pm[3];
+                    float is;
+                    q8_scale(a, dsc, is);
+                    inv[0] = quad_bcast<0>(is);
+                    inv[1] = quad_bcast<1>(is);
+                    inv[2] = quad_bcast<2>(is);
+                    inv[3] = quad_bcast<3>(is);
+                } else if constexpr (D == 64) {
+                    // pairs 0, 2 are group 0 and 1, 3 group 1; a group spans the row's 8 lanes
+                    float g0 = fmaxf(pm[0], pm[2]), g1 = fmaxf(pm[1], pm[3]);
+                    g0 = fmaxf(g0, dpp_f<DPP_XOR1>(g0));
+                    g0 = fmaxf(g0, dpp_f<DPP_XOR2>(g0));
+                    g0 = fmaxf(g0, dpp_f<DPP_HALF_MIRROR>(g0));
+                    g1 = fmaxf(g1, dpp_f<DPP_XOR1>(g1));
+                    g1 = fmaxf(g1, dpp_f<DPP_XOR2>(g1));
+                    g1 = fmaxf(g1, dpp_f<DPP_HALF_MIRROR>(g1));
+                    float is;
+                    q8_scale((m & 1u) ? g1 : g0, dsc, is);
+                    const float i0 = quad_bcast<0>(is), i1 = quad_bcast<1>(is);
+                    inv[0] = i0; inv[1] = i1; inv[2] = i0; inv[3] = i1;
+                } else {
+                    // pair j is group 4 (m % 2) + j; the group spans the row's 16 lanes of
+                    // m's parity (lanes ^ 2, ^ 4, ^ 8, ^ 16)
+                    float ds[4];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        pm[j] = fmaxf(pm[j], dpp_f<DPP_XOR2>(pm[j]));
+                        pm[j] = fmaxf(pm[j], dpp_f<DPP_ROR4>(pm[j]));
+                        pm[j] = fmaxf(pm[j], dpp_f<DPP_ROR8>(pm[j]));
+                        pm[j] = fmaxf(pm[j], __shfl_xor(pm[j], 16));
+                        q8_scale(pm[j], ds[j], inv[j]);
+                    }
+                    const uint32_t sel = (m >> 1) & 3u;
+                    dsc = sel == 0 ? ds[0] : sel == 1 ? ds[1] : sel == 2 ? ds[2] : ds[3];
+                }
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    qi[2 * j] = quant_q8(x[u][2 * j], inv[j]);
+                    qi[2 * j + 1] = quant_q8(x[u][2 * j + 1], inv[j]);
+                }
+                st_u2<NTS>(rowk[u] + 8u * m, pack_q4(qi[0], qi[1], qi[2], qi[3]),
+                           pack_q4(qi[4], qi[5], qi[6], qi[7]));
+                // scale writers: D = 64, 128: lane m < D/32 holds group m's d;
+                // D = 256: lane m < 8 holds group 4 (m % 2) + m / 2
+                if (m < D / 32) {
+                    const uint32_t grp = D == 256 ? 4u * (m & 1u) + (m >> 1) : m;
+                    *(_Float16 *)(rows[u] + grp * 2u) = (_Float16)dsc;
+                }
+            }
         }
     }
 }
@@ -316,6 +547,124 @@ __global__ __launch_bounds__(256) void k_gather(const uint8_t *__restrict__ pool
                 }
             }
             store_f8((float *)(isv ? out_v : out_k) + o, y);
+        }
+    }
+}
+
+// q8_0 -> f32 gather for d = 64, 128, 256.  Thread = one 16-byte piece of a stored row
+// (one load), dequantized and written as the contiguous logical runs it holds:
+//   K (byte q*(D/4) + 8i + t holds d = 32i + 8q + t): a piece holds two 8-value runs,
+//     d = 32i + 8q .. +7 and 32(i+1) + 8q .. +7;
+//   V (byte c*(D/16) + 2g + u holds d = 32g + 2c + u): a piece holds NC = 256/D (>= 1)
+//     consecutive c of NG = 8/NC groups, i.e. 2*NC consecutive values of each group.
+// The row's D/32 f16 scales come in with one load.  8 pieces in flight per thread.
+template <int D>
+__device__ __forceinline__ void store_run(float *dst, const float *y, int n) {
+    if (n == 8) store_f8(dst, y);
+    else if (n == 4) __builtin_nontemporal_store(f4v{y[0], y[1], y[2], y[3]}, (f4v *)dst);
+    else __builtin_nontemporal_store(f2v{y[0], y[1]}, (f2v *)dst);
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void k_gather_q8(const uint8_t *__restrict__ pool,
+                                                   uint64_t pool_blocks,
+                                                   const uint32_t *__restrict__ blocks,
+                                                   uint64_t n_table,
+                                                   const uint32_t *__restrict__ table_at,
+                                                   const uint32_t *__restrict__ lens,
+                                                   const uint64_t *__restrict__ out_at,
+                                                   uint32_t n_items, uint32_t tiles_max,
+                                                   uint64_t out_positions, float *out_k,
+                                                   float *out_v, Geo geo, int *err) {
+    const uint32_t item = blockIdx.x / tiles_max;
+    const uint32_t tile = blockIdx.x - item * tiles_max;
+    if (item >= n_items) return;
+    const uint32_t len = lens[item];
+    const uint32_t p0 = tile * 16u;
+    if (p0 >= len) return;
+    const uint32_t B = (uint32_t)geo.B, G = (uint32_t)geo.G;
+    const uint32_t tab = table_at[item];
+    const uint32_t nblk = (len + B - 1) / B;
+    if ((uint64_t)tab + nblk > n_table) {
+        if (threadIdx.x == 0) flag(err, ERR_TABLE);
+        return;
+    }
+    const uint64_t oat = out_at[item];
+    if (oat + len > out_positions) {
+        if (threadIdx.x == 0) flag(err, ERR_OUT);
+        return;
+    }
+    const uint32_t blk = blocks[tab + p0 / B];
+    if (blk >= pool_blocks) {
+        if (threadIdx.x == 0) flag(err, ERR_BLOCK);
+        return;
+    }
+    const uint32_t r0 = p0 % B;
+    const uint8_t *base = pool + (uint64_t)blk * geo.bb;
+    constexpr uint32_t PR = D / 16;           // pieces per row
+    constexpr uint32_t NS = D / 32;           // scales per row
+    constexpr uint32_t NC = D >= 256 ? 1 : 256 / D, NG = 8 / NC;
+    const uint32_t per_kv = G * 16u * PR;
+    constexpr int U = 8;
+    for (uint32_t b0 = 0; b0 < 2u * per_kv; b0 += 256u * U) {
+        u4v x[U];
+        u4v sc[U];
+        float *dst[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            dst[u] = nullptr;
+            const uint32_t idx = b0 + u * 256u + threadIdx.x;
+            if (idx >= 2u * per_kv) continue;
+            const bool isv = idx >= per_kv;
+            const uint32_t r = isv ? idx - per_kv : idx;
+            const uint32_t j = r % PR, row = (r / PR) & 15u, g = r / (PR * 16u);
+            const uint32_t p = p0 + row;
+            if (p >= len) continue;
+            const uint64_t rowidx = (uint64_t)g * B + r0 + row;
+            x[u] = __builtin_nontemporal_load(
+                (const u4v *)(base + (isv ? geo.v_off : geo.k_off) + rowidx * D + 16u * j));
+            const uint8_t *sp = base + (isv ? geo.vs_off : geo.ks_off) + rowidx * NS * 2u;
+            if constexpr (NS == 2) sc[u] = u4v{*(const uint32_t *)sp, 0u, 0u, 0u};
+            else if constexpr (NS == 4) { const u2v t = *(const u2v *)sp; sc[u] = u4v{t.x, t.y, 0u, 0u}; }
+            else sc[u] = *(const u4v *)sp;
+            dst[u] = (isv ? out_v : out_k) + oat * (uint64_t)G * D + ((uint64_t)g * len + p) * D;
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (!dst[u]) continue;
+            const uint32_t idx = b0 + u * 256u + threadIdx.x;
+            const bool isv = idx >= per_kv;
+            const uint32_t j = (isv ? idx - per_kv : idx) % PR;
+            const uint32_t w[4] = {x[u].x, x[u].y, x[u].z, x[u].w};
+            auto qv = [&](uint32_t b) { return (float)(int8_t)(w[b >> 2] >> (8u * (b & 3u))); };
+            auto scale = [&](uint32_t grp) {
+                const uint32_t word = sc[u][grp >> 1];
+                return (float)__builtin_bit_cast(_Float16, (uint16_t)(word >> (16u * (grp & 1u))));
+            };
+            if (!isv) {
+                const uint32_t qq = (16u * j) / (D / 4), i0 = ((16u * j) % (D / 4)) / 8u;
+#pragma unroll
+                for (uint32_t h = 0; h < 2; h++) {
+                    const float s = scale(i0 + h);
+                    float y[8];
+#pragma unroll
+                    for (uint32_t t = 0; t < 8; t++) y[t] = qv(8u * h + t) * s;
+                    store_f8(dst[u] + 32u * (i0 + h) + 8u * qq, y);
+                }
+            } else {
+                const uint32_t c0 = (16u * j) / PR, g0 = ((16u * j) % PR) / 2u;
+#pragma unroll
+                for (uint32_t gi = 0; gi < NG; gi++) {
+                    const float s = scale(g0 + gi);
+                    float y[2 * NC];
+#pragma unroll
+                    for (uint32_t ci = 0; ci < NC; ci++) {
+                        y[2 * ci] = qv(ci * PR + 2u * gi) * s;
+                        y[2 * ci + 1] = qv(ci * PR + 2u * gi + 1u) * s;
+                    }
+                    store_run<D>(dst[u] + 32u * (g0 + gi) + 2u * c0, y, 2 * NC);
+                }
+            }
         }
     }
 }
@@ -667,26 +1016,53 @@ hipError_t launch_append(const Geometry &g, void *pool, uint64_t pool_blocks, co
     // f16: non-temporal f32 loads and f16 stores (a pure stream); q8_0 is faster with
     // cached loads (measured at cfg3: 4.78 vs 4.40 TB/s).
     const bool NT = tune("QVKV_APPEND_NT", g.dtype == QVKV_F16 ? 1 : 0) != 0;
-    // keep the flat index inside 32 bits: launch in row batches
-    const uint32_t max_rows = (uint32_t)((0x7fffffffull / per_row));
+    // keep the flat index inside 32 bits: launch in batches of whole 16-row tiles
+    const uint32_t max_rows = (uint32_t)((0x7fffffffull / per_row)) & ~15u;
+    const bool tiled = g.D == 64 || g.D == 128 || g.D == 256;
+    const FastDiv fd_row((uint32_t)(tiled ? 16 * per_row : per_row));
     for (uint32_t r0 = 0; r0 < n; r0 += max_rows) {
         const uint32_t nr = n - r0 < max_rows ? n - r0 : max_rows;
-        const unsigned grid = grid_for(((uint64_t)nr * per_row + U - 1) / U, per_cu);
+        const uint64_t items = (tiled ? (uint64_t)(nr + 15) / 16 * 16 : nr) * per_row;
+        const unsigned grid = grid_for((items + U - 1) / U, per_cu);
         const float *kk = k + (uint64_t)r0 * g.kv_out, *vv = v + (uint64_t)r0 * g.kv_out;
-#define QV_APPEND(DT, UU, NN)                                                                  \
-    hipLaunchKernelGGL((k_append<DT, UU, NN>), dim3(grid), dim3(256), 0, s, (uint8_t *)pool,   \
-                       pool_blocks, kk, vv, slots + r0, nr, geo, err)
+#define QV_APPEND(DT, UU, NN, DD)                                                              \
+    hipLaunchKernelGGL((k_append<DT, UU, NN, DD>), dim3(grid), dim3(256), 0, s, (uint8_t *)pool,   \
+                       pool_blocks, kk, vv, slots + r0, nr, fd_row, geo, err)
+#define QV_APPEND_D(DT, UU, NN)                                                                \
+    if (g.D == 64) QV_APPEND(DT, UU, NN, 64);                                                  \
+    else if (g.D == 128) QV_APPEND(DT, UU, NN, 128);                                           \
+    else if (g.D == 256) QV_APPEND(DT, UU, NN, 256);                                           \
+    else QV_APPEND(DT, UU, NN, 0);
 #define QV_APPEND_U(DT)                                                                        \
-    if (U <= 1) { if (NT) QV_APPEND(DT, 1, true); else QV_APPEND(DT, 1, false); }              \
-    else if (U == 2) { if (NT) QV_APPEND(DT, 2, true); else QV_APPEND(DT, 2, false); }         \
-    else if (U == 4) { if (NT) QV_APPEND(DT, 4, true); else QV_APPEND(DT, 4, false); }         \
-    else { if (NT) QV_APPEND(DT, 8, true); else QV_APPEND(DT, 8, false); }
-        if (g.dtype == QVKV_F16) {
+    if (U <= 2) { if (NT) { QV_APPEND_D(DT, 2, true) } else { QV_APPEND_D(DT, 2, false) } }    \
+    else { if (NT) { QV_APPEND_D(DT, 4, true) } else { QV_APPEND_D(DT, 4, false) } }
+#define QV_APPEND_Q8(UU, NN, DD)                                                               \
+    hipLaunchKernelGGL((k_append_q8<UU, NN, DD>), dim3(grid), dim3(256), 0, s, (uint8_t *)pool, \
+                       pool_blocks, kk, vv, slots + r0, nr, fd_row, geo, err)
+#define QV_APPEND_Q8_D(UU, NN)                                                                 \
+    if (g.D == 64) QV_APPEND_Q8(UU, NN, 64);                                                   \
+    else if (g.D == 128) QV_APPEND_Q8(UU, NN, 128);                                            \
+    else QV_APPEND_Q8(UU, NN, 256);
+        const bool q8fast = (g.D == 64 || g.D == 128 || g.D == 256) &&
+                            tune("QVKV_APPEND_Q8_FAST", 1) != 0;
+        if (g.dtype == QVKV_Q8_0 && q8fast) {
+            // cached loads, non-temporal stores (measured at cfg3: 5.50 / 5.57 TB/s with cached
+            // / non-temporal stores, 5.3 with non-temporal loads; 2 chunks per thread ahead of 4)
+            const int mode = (NT ? 1 : 0) | (tune("QVKV_APPEND_NTS", 1) ? 2 : 0);
+#define QV_APPEND_Q8_M(UU)                                                                     \
+    if (mode == 0) { QV_APPEND_Q8_D(UU, 0) } else if (mode == 1) { QV_APPEND_Q8_D(UU, 1) }     \
+    else if (mode == 2) { QV_APPEND_Q8_D(UU, 2) } else { QV_APPEND_Q8_D(UU, 3) }
+            if (U <= 2) { QV_APPEND_Q8_M(2) } else { QV_APPEND_Q8_M(4) }
+#undef QV_APPEND_Q8_M
+        } else if (g.dtype == QVKV_F16) {
             QV_APPEND_U(QVKV_F16)
         } else {
             QV_APPEND_U(QVKV_Q8_0)
         }
+#undef QV_APPEND_Q8_D
+#undef QV_APPEND_Q8
 #undef QV_APPEND_U
+#undef QV_APPEND_D
 #undef QV_APPEND
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
@@ -709,9 +1085,18 @@ hipError_t launch_gather(const Geometry &g, const void *pool, uint64_t pool_bloc
     hipLaunchKernelGGL((k_gather<DT, OT>), dim3((unsigned)grid), dim3(256), 0, s, p,           \
                        pool_blocks, blocks, n_table, table_at, lens, out_at, n_items, tiles,   \
                        out_positions, out_k, out_v, geo, err)
-    if (g.dtype == QVKV_F16 && out_dtype == QVKV_F16) QV_GATHER(QVKV_F16, QVKV_F16);
+#define QV_GATHER_Q8(DD)                                                                       \
+    hipLaunchKernelGGL((k_gather_q8<DD>), dim3((unsigned)grid), dim3(256), 0, s, p,            \
+                       pool_blocks, blocks, n_table, table_at, lens, out_at, n_items, tiles,   \
+                       out_positions, (float *)out_k, (float *)out_v, geo, err)
+    const bool q8fast = tune("QVKV_GATHER_Q8_FAST", 1) != 0;
+    if (g.dtype == QVKV_Q8_0 && q8fast && g.D == 64) QV_GATHER_Q8(64);
+    else if (g.dtype == QVKV_Q8_0 && q8fast && g.D == 128) QV_GATHER_Q8(128);
+    else if (g.dtype == QVKV_Q8_0 && q8fast && g.D == 256) QV_GATHER_Q8(256);
+    else if (g.dtype == QVKV_F16 && out_dtype == QVKV_F16) QV_GATHER(QVKV_F16, QVKV_F16);
     else if (g.dtype == QVKV_F16) QV_GATHER(QVKV_F16, QVKV_F32);
     else QV_GATHER(QVKV_Q8_0, QVKV_F32);
+#undef QV_GATHER_Q8
 #undef QV_GATHER
     return hipGetLastError();
 }

@@ -106,7 +106,7 @@ def q8_case(r, n, G, D):
     return k, v
 
 
-@pytest.mark.parametrize("G,D", [(8, 128), (4, 64), (2, 256)])
+@pytest.mark.parametrize("G,D", [(8, 128), (4, 64), (2, 256), (3, 96), (5, 128)])
 def test_append_q8_0_bit_exact(hip, G, D):
     print(f"append q8_0 G={G} D={D}", flush=True)
     r = rng(200 + G * D)
@@ -147,6 +147,7 @@ def fill_items(hip, L, pool, N, lens, r, outliers=0.0):
 
 
 @pytest.mark.parametrize("dtype,G,D", [(F16, 8, 128), (F16, 4, 64), (Q8_0, 8, 128), (Q8_0, 2, 64),
+                                       (Q8_0, 3, 256), (Q8_0, 2, 96), (Q8_0, 1, 160),
                                        (F16, 2, 96)])
 def test_gather_bit_exact(hip, dtype, G, D):
     print(f"gather {dtype} G={G} D={D}", flush=True)
