@@ -61,16 +61,47 @@ __device__ __forceinline__ h4 h4_of(uint32_t a, uint32_t b) {
     return __builtin_bit_cast(h4, make_uint2(a, b));
 }
 
-// 4 int8 (one word) -> 4 f16, exactly: (0x6400 | (x ^ 0x80)) is 1024 + x + 128 in f16.
+// Four signed bytes -> four f16 (exact), one v_cvt_f16_i16 per value: SDWA selects and
+// sign-extends the byte on the way in and writes one half of the result.  Each block
+// defines one MFMA operand (two registers) and ends in s_nop 1: an MFMA reading a VGPR
+// that a VALU instruction wrote needs 2 wait states in between, which the compiler's
+// hazard recognizer does not provide after inline asm.
+//   i8x4_to_h4(w): bytes 0..3 of w;  bytes_to_h4<BY>(w0..w3): byte BY of w0, w1, w2, w3.
+#define QV_CVT(DST, SRC, WORD, UNUSED, BYTE)                                                    \
+    "v_cvt_f16_i16_sdwa " DST ", sext(" SRC ") dst_sel:" WORD " dst_unused:" UNUSED             \
+    " src0_sel:" BYTE "\n"
+#define QV_CVT4(B0, B1, B2, B3)                                                                 \
+    QV_CVT("%0", "%2", "WORD_0", "UNUSED_PAD", B0)                                              \
+    QV_CVT("%0", "%3", "WORD_1", "UNUSED_PRESERVE", B1)                                         \
+    QV_CVT("%1", "%4", "WORD_0", "UNUSED_PAD", B2)                                              \
+    QV_CVT("%1", "%5", "WORD_1", "UNUSED_PRESERVE", B3) "s_nop 1"
+
 __device__ __forceinline__ h4 i8x4_to_h4(uint32_t w) {
-    const uint32_t u = w ^ 0x80808080u;
-    const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
-    const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
-    const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
-    const h2 a = __builtin_bit_cast(h2, lo) - bias;
-    const h2 b = __builtin_bit_cast(h2, hi) - bias;
-    return h4{a.x, a.y, b.x, b.y};
+    uint32_t a, b;
+    asm(QV_CVT4("BYTE_0", "BYTE_1", "BYTE_2", "BYTE_3")
+        : "=&v"(a), "=&v"(b) : "v"(w), "v"(w), "v"(w), "v"(w));
+    return h4_of(a, b);
 }
+
+template <int BY>
+__device__ __forceinline__ h4 bytes_to_h4(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
+    uint32_t a, b;
+    if constexpr (BY == 0)
+        asm(QV_CVT4("BYTE_0", "BYTE_0", "BYTE_0", "BYTE_0")
+            : "=&v"(a), "=&v"(b) : "v"(w0), "v"(w1), "v"(w2), "v"(w3));
+    else if constexpr (BY == 1)
+        asm(QV_CVT4("BYTE_1", "BYTE_1", "BYTE_1", "BYTE_1")
+            : "=&v"(a), "=&v"(b) : "v"(w0), "v"(w1), "v"(w2), "v"(w3));
+    else if constexpr (BY == 2)
+        asm(QV_CVT4("BYTE_2", "BYTE_2", "BYTE_2", "BYTE_2")
+            : "=&v"(a), "=&v"(b) : "v"(w0), "v"(w1), "v"(w2), "v"(w3));
+    else
+        asm(QV_CVT4("BYTE_3", "BYTE_3", "BYTE_3", "BYTE_3")
+            : "=&v"(a), "=&v"(b) : "v"(w0), "v"(w1), "v"(w2), "v"(w3));
+    return h4_of(a, b);
+}
+#undef QV_CVT4
+#undef QV_CVT
 
 // x + x of lane l ^ 8: within each row of 16 lanes, a DPP rotate by 8.
 __device__ __forceinline__ float add_xor8(float x) {
@@ -305,12 +336,6 @@ __device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<
         // int8 values are finite whatever the slot holds, so 0 * value = 0 in the MFMA; their
         // scales may be any f16 bits (NaN, inf) and are folded in with v_mul_legacy_f32,
         // whose 0 * x is 0 for every x.  No row needs masking.
-        uint32_t vsw[4][Tile<D, Q8>::VW];  // biased bytes x ^ 0x80
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int x = 0; x < Tile<D, Q8>::VW; x++) vsw[i][x] = vw[i][x] ^ 0x80808080u;
-        const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
         const float lo_part = hi_col ? 0.0f : 1.0f;
         // The A operand of scaled probabilities for group g (this lane's scale pick).
         auto scaled = [&](float sc_of_row[4]) {
@@ -323,20 +348,21 @@ __device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<
             }
             return h4{pg[0], pg[1], pg[2], pg[3]};
         };
-        // P'.V for the two MFMAs of group gi (bytes 2gi, 2gi+1 of each row's run).
+        // P'.V for the two MFMAs of group gi (bytes 2gi, 2gi+1 of each row's run): the B
+        // operand of MFMA j is byte j % 4 of word j / 4 of rows 0..3, converted by SDWA.
         auto pv_group = [&](const h4 &pa, int gi) {
-            const int j = 2 * gi;
-            const uint32_t b = (uint32_t)(j & 3);
-            const uint32_t sel = ((4u + b + 1) << 24) | ((b + 1) << 16) | ((4u + b) << 8) | b;
-            const uint32_t t01 = __builtin_amdgcn_perm(vsw[1][j >> 2], vsw[0][j >> 2], sel);
-            const uint32_t t23 = __builtin_amdgcn_perm(vsw[3][j >> 2], vsw[2][j >> 2], sel);
 #pragma unroll
             for (int u = 0; u < 2; u++) {
-                const uint32_t spread = u ? 0x04030402u : 0x04010400u;
-                const h2 x01 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, t01, spread)) - bias;
-                const h2 x23 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, t23, spread)) - bias;
-                st.acc[j + u] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, h4{x01.x, x01.y, x23.x, x23.y},
-                                                                      st.acc[j + u], 0, 0, 0);
+                const int j = 2 * gi + u;
+                const int wd = j >> 2;
+                h4 bop;
+                switch (j & 3) {
+                    case 0: bop = bytes_to_h4<0>(vw[0][wd], vw[1][wd], vw[2][wd], vw[3][wd]); break;
+                    case 1: bop = bytes_to_h4<1>(vw[0][wd], vw[1][wd], vw[2][wd], vw[3][wd]); break;
+                    case 2: bop = bytes_to_h4<2>(vw[0][wd], vw[1][wd], vw[2][wd], vw[3][wd]); break;
+                    default: bop = bytes_to_h4<3>(vw[0][wd], vw[1][wd], vw[2][wd], vw[3][wd]); break;
+                }
+                st.acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, bop, st.acc[j], 0, 0, 0);
             }
         };
         if constexpr (PK) {
