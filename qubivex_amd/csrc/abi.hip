@@ -195,6 +195,11 @@ int finish(qvkv_dev *dev, hipStream_t s) {
         int zero = 0;
         e = hipMemcpy(dev->d_err, &zero, sizeof zero, hipMemcpyHostToDevice);
         if (e != hipSuccess) return hip_fail(e, "hipMemcpy (error flag reset)");
+        if (bits == 16)
+            return fail(QVKV_E_UNSUPPORTED,
+                        "q8_0 prefill: a value scale above 512 (dequantised values past the f16 "
+                        "range of the MFMA prefill; QVKV_PREFILL_Q8_FAST=0 selects the form "
+                        "without that limit)");
         return fail(QVKV_E_SHAPE,
                     "shape mismatch in kv kernel: %s%s%s%s",
                     (bits & 1) ? "a block id past the pool; " : "",

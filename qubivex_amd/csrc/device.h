@@ -19,7 +19,7 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 typedef float f2v __attribute__((ext_vector_type(2)));
 typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 
-enum : int { ERR_BLOCK = 1, ERR_TABLE = 2, ERR_POS = 4, ERR_OUT = 8 };
+enum : int { ERR_BLOCK = 1, ERR_TABLE = 2, ERR_POS = 4, ERR_OUT = 8, ERR_RANGE = 16 };
 
 struct Geo {  // kernel-side copy of Geometry
     int dtype, G, D, B;
@@ -83,6 +83,30 @@ __device__ __forceinline__ h4 i8x4_to_h4(uint32_t w) {
     return h4_of(a, b);
 }
 
+// The same four conversions for a consumer that is not an MFMA (no padding).
+__device__ __forceinline__ h4 i8x4_to_h4_vals(uint32_t w) {
+    uint32_t a, b;
+    asm(QV_CVT("%0", "%2", "WORD_0", "UNUSED_PAD", "BYTE_0")
+        QV_CVT("%0", "%2", "WORD_1", "UNUSED_PRESERVE", "BYTE_1")
+        QV_CVT("%1", "%2", "WORD_0", "UNUSED_PAD", "BYTE_2")
+        QV_CVT("%1", "%2", "WORD_1", "UNUSED_PRESERVE", "BYTE_3")
+        : "=&v"(a), "=&v"(b) : "v"(w));
+    return h4_of(a, b);
+}
+
+// Bytes BY and BY + 1 of w -> two f16 (low, high half); for a non-MFMA consumer.
+template <int BY>
+__device__ __forceinline__ uint32_t i8x2_to_h2(uint32_t w) {
+    uint32_t a;
+    if constexpr (BY == 0)
+        asm(QV_CVT("%0", "%1", "WORD_0", "UNUSED_PAD", "BYTE_0")
+            QV_CVT("%0", "%1", "WORD_1", "UNUSED_PRESERVE", "BYTE_1") : "=&v"(a) : "v"(w));
+    else
+        asm(QV_CVT("%0", "%1", "WORD_0", "UNUSED_PAD", "BYTE_2")
+            QV_CVT("%0", "%1", "WORD_1", "UNUSED_PRESERVE", "BYTE_3") : "=&v"(a) : "v"(w));
+    return a;
+}
+
 template <int BY>
 __device__ __forceinline__ h4 bytes_to_h4(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
     uint32_t a, b;
@@ -113,13 +137,18 @@ __device__ __forceinline__ float add_xor8(float x) {
 // max of x over lanes l, l ^ 16, l ^ 32, l ^ 48.  v_permlane16_swap (vdst, vsrc both x)
 // leaves x of rows (0, 0, 2, 2) in one result and (1, 1, 3, 3) in the other; the max of
 // the two is the max over l and l ^ 16.  v_permlane32_swap does the same for halves.
+// Each result element is copied to a scalar before its bit_cast: hipcc's
+// __builtin_bit_cast of a vector element (a[1]) reads element 0, which had turned this
+// into the max of row group 0 alone.
 __device__ __forceinline__ float max_xor16_32(float x) {
     const uint32_t u = __builtin_bit_cast(uint32_t, x);
     const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-    x = fmaxf(__builtin_bit_cast(float, a[0]), __builtin_bit_cast(float, a[1]));
+    const uint32_t a0 = a[0], a1 = a[1];
+    x = fmaxf(__builtin_bit_cast(float, a0), __builtin_bit_cast(float, a1));
     const uint32_t v = __builtin_bit_cast(uint32_t, x);
     const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-    return fmaxf(__builtin_bit_cast(float, b[0]), __builtin_bit_cast(float, b[1]));
+    const uint32_t b0 = b[0], b1 = b[1];
+    return fmaxf(__builtin_bit_cast(float, b0), __builtin_bit_cast(float, b1));
 }
 
 // f32 -> (high f16, residual f16); lane columns < 8 take the high part.

@@ -566,6 +566,318 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
     }
 }
 
+// ---------------------------------------------------------------------------------
+// Paged prefill attention, q8_0 pools, d = 128: the MFMA-throughput form of
+// k_prefill_f16 (64 query rows per workgroup, 16 per wave, 32-position tiles in LDS, the
+// same swizzled slot layout and operand reads), with the tiles staged through registers:
+//   K: int8 values as f16 (exact); each score MFMA pair covers one 32-value group, and the
+//      group's per-position scale multiplies its partial scores (v_fma_mix reads the f16
+//      scale directly);
+//   V: dequantised while staging, v = q * scale split into an f16 high part and its
+//      residual (packed f16 multiply, then a packed FMA that forms the residual exactly),
+//      so P.V takes three MFMAs per d block: P_hi V_hi + P_lo V_hi + P_hi V_lo.
+// Dequantised V values must fit f16: a V scale above 512 (127 * 512 < 65504) latches
+// ERR_RANGE and the call reports QVKV_E_UNSUPPORTED.
+// Tile t + 1 is loaded into registers during tile t's math, then converted into the other
+// LDS buffer; one barrier per tile.
+// ---------------------------------------------------------------------------------
+template <int D>
+struct Q8PrefillSlot {
+    _Float16 k[32 * D];           // int8 keys as f16, DMA-slot layout (A-operand row order)
+    _Float16 vh[32 * D], vl[32 * D];  // dequantised values: high part, residual
+    uint32_t ks[32 * (D / 64)];   // key scales, [position][group] f16
+};
+
+template <int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
+void k_prefill_q8(QV_PREFILL_PARAMS) {
+    static_assert(D == 128, "q8_0 MFMA-throughput prefill is built for d = 128");
+    constexpr int TP = 32;
+    constexpr int KS = D / 32;                 // QK k-steps = quantization groups
+    constexpr int NDB = D / 16;                // PV d blocks
+    constexpr int CPR = D / 8;                 // 8-value (16-byte f16) pieces per row
+    constexpr int NGW = D / 64;                // scale words per row (2 groups per word)
+    __shared__ __attribute__((aligned(16))) Q8PrefillSlot<D> sb[2];
+
+    const uint32_t G = (uint32_t)geo.G, B = (uint32_t)geo.B;
+    const uint32_t GS = H / G;
+    uint32_t bid = blockIdx.x;
+    if (geo.xcd_map) {
+        const uint32_t nb = gridDim.x, qn = nb / 8, rn = nb % 8;
+        const uint32_t x = bid % 8, i = bid / 8;
+        bid = x < rn ? x * (qn + 1) + i : rn * (qn + 1) + (x - rn) * qn + i;
+    }
+    const uint32_t qb = bid % n_cb;
+    const uint32_t sg = bid / n_cb;
+    const uint32_t g = sg % G;
+    const uint32_t seg = sg / G;
+    if (seg >= n_seg) return;
+    const uint32_t nt = n_tok[seg], p0s = pos0[seg], qa = q_at[seg], tab = table_at[seg];
+    if (nt == 0) return;
+    const bool lead = threadIdx.x == 0 && qb == 0 && g == 0;
+    if (nt > max_tok || (uint64_t)p0s + nt - 1 > max_pos) {
+        if (lead) flag(err, ERR_POS);
+        return;
+    }
+    if ((uint64_t)qa + nt > q_rows) {
+        if (lead) flag(err, ERR_OUT);
+        return;
+    }
+    const uint32_t n_all = p0s + nt;
+    if ((uint64_t)tab + (n_all + B - 1) / B > n_table) {
+        if (lead) flag(err, ERR_TABLE);
+        return;
+    }
+    const uint32_t nrows = nt * GS;
+    const uint32_t r0 = qb * 64u;
+    if (r0 >= nrows) return;  // the whole workgroup: no barrier has run yet
+    const uint32_t wg_last = min(nt - 1, (r0 + 63u) / GS);
+    const uint32_t n_wg = p0s + wg_last + 1;
+    const uint32_t ntiles = (n_wg + TP - 1) / TP;
+
+    const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+    const uint32_t col = lane & 15u, grp = lane >> 4;
+    const uint32_t rw0 = r0 + w * 16u;
+    const bool wave_live = rw0 < nrows;
+    const uint32_t n_wave = wave_live ? p0s + min(nt - 1, (rw0 + 15u) / GS) + 1 : 0u;
+    const uint32_t n_wave_min = wave_live ? p0s + rw0 / GS + 1 : 0u;
+    const uint32_t row = rw0 + col;
+    const bool rvalid = row < nrows;
+    const uint32_t tj = rvalid ? row / GS : 0u, hh = rvalid ? row % GS : 0u;
+    const uint32_t n_row = rvalid ? p0s + tj + 1 : 0u;
+
+    h8 qh[KS], ql[KS];
+    {
+        const float qs = (1.0f / sqrtf((float)D)) * LOG2E_F;
+        const float *qrow = q + ((uint64_t)(qa + tj) * H + (uint64_t)g * GS + hh) * D;
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            float x[8];
+            if (rvalid) {
+                const float4 a = *(const float4 *)(qrow + 32 * ks + 8 * grp);
+                const float4 b = *(const float4 *)(qrow + 32 * ks + 8 * grp + 4);
+                x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+                x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++) x[e] = 0.0f;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float y = mul_rn(x[e], qs);
+                const _Float16 hi = (_Float16)y;
+                qh[ks][e] = hi;
+                ql[ks][e] = (_Float16)(y - (float)hi);
+            }
+        }
+    }
+
+    // ---- staging: thread = (position sp = tid / 8, 16-byte piece sj = tid % 8) of the
+    // tile's stored K and V rows, plus the row's 4 V scales; threads 0..63 also move one
+    // word of K scales (position tid / 2).
+    const uint32_t sp = threadIdx.x >> 3, sj = threadIdx.x & 7u;
+    u4v xk, xv;
+    u2v xvs;
+    uint32_t xks;
+    auto load = [&](uint32_t t) {
+        const uint32_t p = t * TP + sp;
+        xk = u4v{0u, 0u, 0u, 0u};
+        xv = u4v{0u, 0u, 0u, 0u};
+        xvs = u2v{0u, 0u};
+        xks = 0u;
+        const uint32_t pk = t * TP + (threadIdx.x >> 1);  // K-scale position (tid < 64)
+        if (p < n_wg) {
+            const uint32_t blk = blocks[tab + p / B];
+            if (blk >= pool_blocks) {
+                flag(err, ERR_BLOCK);
+            } else {
+                const uint8_t *base = pool + (uint64_t)blk * geo.bb;
+                const uint64_t rw = (uint64_t)g * B + p % B;
+                xk = *(const u4v *)(base + geo.k_off + rw * D + 16u * sj);
+                xv = *(const u4v *)(base + geo.v_off + rw * D + 16u * sj);
+                xvs = *(const u2v *)(base + geo.vs_off + rw * (D / 16));
+            }
+        }
+        if (threadIdx.x < 64u && pk < n_wg) {
+            const uint32_t blk = blocks[tab + pk / B];
+            if (blk < pool_blocks)
+                xks = *(const uint32_t *)(pool + (uint64_t)blk * geo.bb + geo.ks_off +
+                                          ((uint64_t)g * B + pk % B) * (D / 16) + 4u * (threadIdx.x & 1u));
+        }
+    };
+    auto store = [&](Q8PrefillSlot<D> &sl) {
+        // K: stored bytes 16 sj .. +15 hold d = 32 i + 8 q + t with q = sj / 2 and
+        // i = 2 (sj % 2) + {0, 1}: two logical pieces 4 i + q
+        const uint32_t lr = 16u * ((sp >> 2) & 1u) + 4u * (sp >> 3) + (sp & 3u);
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t piece = 4u * (2u * (sj & 1u) + h) + (sj >> 1);
+            const h4 a = i8x4_to_h4_vals(xk[2 * h]), b = i8x4_to_h4_vals(xk[2 * h + 1]);
+            *(h8 *)(sl.k + (lr * CPR + (piece ^ kswz<D>(lr))) * 8) =
+                h8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+        }
+        // V: stored byte c * 8 + 2 gr + u holds d = 32 gr + 2 c + u; this piece holds
+        // c = 2 sj, 2 sj + 1: for each group gr, d = 32 gr + 4 sj .. +3 from bytes
+        // 2 gr, 2 gr + 1, 8 + 2 gr, 9 + 2 gr
+        bool big = false;
+#pragma unroll
+        for (int gr = 0; gr < 4; gr++) {
+            const uint32_t w0 = xv[gr >> 1], w1 = xv[2 + (gr >> 1)];
+            h2 x01, x23;
+            if (gr & 1) {
+                x01 = __builtin_bit_cast(h2, i8x2_to_h2<2>(w0));
+                x23 = __builtin_bit_cast(h2, i8x2_to_h2<2>(w1));
+            } else {
+                x01 = __builtin_bit_cast(h2, i8x2_to_h2<0>(w0));
+                x23 = __builtin_bit_cast(h2, i8x2_to_h2<0>(w1));
+            }
+            const _Float16 sc = __builtin_bit_cast(_Float16, (uint16_t)(xvs[gr >> 1] >> (16u * (gr & 1u))));
+            big |= !((float)sc <= 512.0f) && (float)sc == (float)sc;
+            const h2 s2 = {sc, sc};
+            h2 a = x01 * s2, b = x23 * s2;       // high parts (rounded products)
+            asm volatile("" : "+v"(a), "+v"(b));  // not contracted into the residuals
+            const h2 ra = __builtin_elementwise_fma(x01, s2, -a);
+            const h2 rb = __builtin_elementwise_fma(x23, s2, -b);
+            const uint32_t P = 4u * gr + (sj >> 1), hf = sj & 1u;
+            const uint32_t off = (sp * CPR + (P ^ vswz<D>(sp))) * 8 + 4 * hf;
+            *(h4 *)(sl.vh + off) = h4{a[0], a[1], b[0], b[1]};
+            *(h4 *)(sl.vl + off) = h4{ra[0], ra[1], rb[0], rb[1]};
+        }
+        if (big) flag(err, ERR_RANGE);
+        if (threadIdx.x < 64u) sl.ks[threadIdx.x] = xks;
+    };
+
+    float m = -INFINITY, l = 0.0f;
+    f4 acc[NDB];
+#pragma unroll
+    for (int j = 0; j < NDB; j++) acc[j] = f4{0.f, 0.f, 0.f, 0.f};
+
+    auto kread = [&](const Q8PrefillSlot<D> &sl, int h, int ks) {
+        const uint32_t r = 16u * h + col, p = 4u * ks + grp;
+        return *(const h8 *)(sl.k + (r * CPR + (p ^ kswz<D>(r))) * 8);
+    };
+    // transposed V read (ds_read_b64_tr_b16): lane col gets positions 8 grp .. +7 of
+    // d = 16 j + col
+    auto vread = [&](const _Float16 *v, int j) {
+        const uint32_t sidx = lane & 15u;
+        u2v wv[2];
+#pragma unroll
+        for (int hf = 0; hf < 2; hf++) {
+            const uint32_t r = 8u * grp + 4u * hf + (sidx >> 2);
+            const uint32_t d = 16u * j + 4u * (sidx & 3u);
+            const uint32_t pc = d >> 3;
+            const _Float16 *a = v + (r * CPR + (pc ^ vswz<D>(r))) * 8 + (d & 7u);
+            typedef short s4 __attribute__((ext_vector_type(4)));
+            wv[hf] = __builtin_bit_cast(u2v, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                 (__attribute__((address_space(3))) s4 *)a));
+        }
+        return __builtin_bit_cast(h8, u4v{wv[0][0], wv[0][1], wv[1][0], wv[1][1]});
+    };
+
+    auto tile = [&](const Q8PrefillSlot<D> &sl, uint32_t tp0) {
+        if (tp0 >= n_wave) return;
+        // ---- scores: lane holds positions tp0 + 8 grp + (4h + i) of row `col`
+        // key scales of this lane's 8 positions: words 2 (8 grp + e) + ks / 2
+        u4v ksw[4];
+#pragma unroll
+        for (int x = 0; x < 4; x++) ksw[x] = *(const u4v *)(sl.ks + 16u * grp + 4u * x);
+        f4 s[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            s[h] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                const h8 a = kread(sl, h, ks);
+                f4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[ks], f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[ks], t, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int e = 4 * h + i;  // position 8 grp + e
+                    const uint32_t wd = ksw[e >> 1][2 * (e & 1) + (ks >> 1)];
+                    const float sc = (float)__builtin_bit_cast(
+                        _Float16, (uint16_t)(wd >> (16 * (ks & 1))));
+                    s[h][i] = fmaf(t[i], sc, s[h][i]);
+                }
+            }
+        }
+        float sc[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) sc[e] = s[e >> 2][e & 3];
+        if (tp0 + TP > n_wave_min) {
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                if (tp0 + 8u * grp + (uint32_t)e >= n_row) sc[e] = -INFINITY;
+        }
+        float tmax = sc[0];
+#pragma unroll
+        for (int e = 1; e < 8; e++) tmax = fmaxf(tmax, sc[e]);
+        tmax = max_xor16_32(tmax);
+        if (__any(tmax > m + 8.0f)) {
+            const float mnew = fmaxf(m, tmax);
+            const float alpha = __builtin_amdgcn_exp2f(m - (mnew == -INFINITY ? 0.0f : mnew));
+            l *= alpha;
+            float ar[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) ar[i] = __shfl(alpha, 4 * (int)grp + i);
+#pragma unroll
+            for (int j = 0; j < NDB; j++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[j][i] *= ar[i];
+            m = mnew;
+        }
+        const float msafe = m == -INFINITY ? 0.0f : m;
+        float pr[8];
+        float psum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            pr[e] = __builtin_amdgcn_exp2f(sc[e] - msafe);
+            psum += pr[e];
+        }
+        l += psum;
+        h8 ph, pl;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const _Float16 hi = (_Float16)pr[e];
+            ph[e] = hi;
+            pl[e] = (_Float16)fmaf(-1.0f, (float)hi, pr[e]);
+        }
+#pragma unroll
+        for (int j = 0; j < NDB; j++) {
+            const h8 bh = vread(sl.vh, j), bl = vread(sl.vl, j);
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, bh, acc[j], 0, 0, 0);
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, bh, acc[j], 0, 0, 0);
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, bl, acc[j], 0, 0, 0);
+        }
+    };
+
+    load(0);
+    store(sb[0]);
+    __syncthreads();
+    for (uint32_t t = 0; t < ntiles; t++) {
+        const int buf = (int)(t & 1u);
+        if (t + 1 < ntiles) load(t + 1);
+        tile(sb[buf], t * TP);
+        if (t + 1 < ntiles) store(sb[buf ^ 1]);
+        __syncthreads();
+    }
+    if (!wave_live) return;
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    float lr[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) lr[i] = __shfl(l, 4 * (int)grp + i);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t rr = rw0 + 4 * grp + i;
+        if (rr >= nrows) continue;
+        const uint32_t tr = rr / GS, hr = rr % GS;
+        float *orow = out + ((uint64_t)(qa + tr) * H + (uint64_t)g * GS + hr) * D;
+        const float inv = 1.0f / lr[i];
+#pragma unroll
+        for (int j = 0; j < NDB; j++) orow[16 * j + col] = acc[j][i] * inv;
+    }
+}
+
 // Prefill, generic form: one wave per (segment, token, query head).
 template <bool Q8>
 __global__ __launch_bounds__(64) void k_prefill_generic(QV_PREFILL_PARAMS) {
@@ -647,6 +959,14 @@ hipError_t launch_prefill(const Geometry &g, const void *pool, uint64_t pool_blo
         else if (tune("QVKV_PREFILL_DMA", 1)) { QV_PF2(128, true); }
         else { QV_PF2(128, false); }
 #undef QV_PF2
+        return hipGetLastError();
+    }
+    if (q8 && g.D == 128 && tune("QVKV_PREFILL_Q8_FAST", 1)) {
+        const uint32_t n_qb = (uint32_t)(((uint64_t)max_tok * GS + 63) / 64);
+        const unsigned grid3 = (unsigned)((uint64_t)n_seg * g.G * n_qb);
+        hipLaunchKernelGGL((k_prefill_q8<128>), dim3(grid3), dim3(256), 0, s, pp, pool_blocks, q,
+                           blocks, n_table, table_at, pos0, q_at, n_tok, n_seg, heads, max_pos,
+                           max_tok, q_rows, n_qb, out, geo, err);
         return hipGetLastError();
     }
     const uint32_t n_cb = (uint32_t)(((uint64_t)max_tok * GS + 31) / 32);

@@ -150,7 +150,8 @@ class HipDevice:
         return lib.qvkv_stream(self.handle)
 
     def check(self, stream=None):
-        """Waits for `stream` and raises ShapeError for an index error a kernel latched."""
+        """Waits for `stream` and raises ShapeError for an index error a kernel latched
+        (UnsupportedError for a q8_0 value scale past the range of the MFMA prefill)."""
         check(lib.qvkv_check(self.handle, _stream(stream)))
 
     def close(self):

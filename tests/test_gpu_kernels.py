@@ -381,3 +381,48 @@ def test_index_errors_are_reported_not_faulted(hip):
     with pytest.raises(ShapeError):
         hip.check()
     hip.check()  # cleared
+
+
+DOMINANT_CASES = [(F16, 32, 8, 128), (Q8_0, 32, 8, 128), (F16, 16, 4, 64), (Q8_0, 8, 2, 64),
+                  (F16, 8, 2, 256), (Q8_0, 8, 2, 256)]
+
+
+def dominant_items(hip, L, H, r, lens, big):
+    """Items of the given lengths whose key at position big[t] is scaled x40, so that one
+    score per head sits ~40 (log2 units) away from the rest of its tile; the values stay
+    N(0, 1).  Returns the pool, tables, oracle and q."""
+    N = sum((n + 15) // 16 for n in lens) + 3
+    pool = new_pool(L, N)
+    blocks, table_at, sim = fill_items(hip, L, pool, N, lens, r)
+    for t, p in enumerate(big):
+        k = normal(r, (1, L.kv_out)) * 40.0
+        v = normal(r, (1, L.kv_out))
+        sl = slots_of(blocks, table_at, t, [p], L.block)
+        hip.append(L, pool, N, cf32(k), cf32(v), cu32(sl))
+        sim.store(k, v, sl)
+    hip.check()
+    return N, pool, blocks, table_at, sim, normal(r, (len(lens), H, L.head_dim))
+
+
+@pytest.mark.parametrize("dtype,H,G,D", DOMINANT_CASES)
+def test_attention_with_a_dominant_position(hip, dtype, H, G, D):
+    """One position far above the rest of its tile, in each row group of a 16-position
+    tile and in later tiles.  The row max must cover all 16 positions of a tile: a max
+    over only part of them leaves the dominant probability past the f16 range of the
+    P.V operand (inf, then NaN)."""
+    print(f"dominant {dtype} H={H} G={G} D={D}", flush=True)
+    r = rng(500 + D + G)
+    L = layout(dtype, G, D)
+    lens = [16, 16, 16, 16, 64, 200, 1]
+    big = [3, 7, 11, 15, 60, 100, 0]
+    N, pool, blocks, table_at, sim, q = dominant_items(hip, L, H, r, lens, big)
+    pos = np.array(lens, np.uint32) - 1
+    out = torch.full((len(lens) * H * D,), float("nan"), dtype=torch.float32, device="cuda")
+    hip.attention(L, pool, N, cf32(q), cu32(blocks), cu32(table_at), cu32(pos), H, int(pos.max()), out)
+    hip.check()
+    got = out.cpu().numpy().reshape(len(lens), H, D)
+    want = sim.attention(q, H, blocks, table_at, pos)
+    assert np.isfinite(got).all()
+    max_abs, rel = attn_errors(got, want)
+    print(f"  max_abs={max_abs:.2e} rel_l2={rel:.2e}", flush=True)
+    assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)

@@ -218,3 +218,108 @@ def test_f16_paths_track_float64_closely(hip, kind):
                                                                  n - nt + j + 1)).max())
     print(f"  {kind}: max |got - f64| = {worst:.2e}", flush=True)
     assert worst < 1e-5, worst
+
+
+@pytest.mark.parametrize("kind", ["prefill", "decode"])
+def test_q8_0_paths_track_float64_closely(hip, kind):
+    """q8_0 values are exact in both kernels: decode converts int8 to f16 and applies the
+    scales in f32; the MFMA prefill keeps keys as int8 and splits each dequantised value
+    into an f16 high part and its exact residual (products then carry ~2^-22 relative
+    error).  Against float64 attention over the dequantised pool both stay within 1e-6
+    of the largest value magnitude (outliers x8 included: |v| up to ~40; measured about
+    1e-5 absolute, against the reference tolerance of 2e-3)."""
+    r = rng(78)
+    G, D, H = 8, 128, 32
+    L = layout(Q8_0, G, D)
+    n, nt = 1200, 40
+    N = (n + 15) // 16 + 2
+    pool = new_pool(L, N)
+    blocks, table_at, _ = fill_items(hip, L, pool, N, [n], r, outliers=0.01)
+    dec = decode_pool(pool.cpu().numpy(), L, N)
+    kd = np.zeros((n, G, D)); vd = np.zeros((n, G, D))
+    grp = np.arange(D) // 32
+    for p in range(n):
+        b, o = blocks[p // 16], p % 16
+        ks = dec["ks"][b, :, o].view(np.float16).astype(np.float64)
+        vs = dec["vs"][b, :, o].view(np.float16).astype(np.float64)
+        kd[p] = dec["k"][b, :, o].astype(np.float64) * ks[:, grp]
+        vd[p] = dec["v"][b, :, o].astype(np.float64) * vs[:, grp]
+    q = normal(r, (nt, H, D))
+    out = torch.zeros(nt * H * D, dtype=torch.float32, device="cuda")
+    if kind == "prefill":
+        hip.prefill_attention(L, pool, N, cf32(q), cu32(blocks), cu32(table_at),
+                              cu32([n - nt]), cu32([0]), cu32([nt]), H, n - 1, nt, out)
+    else:
+        pos = np.arange(n - nt, n, dtype=np.uint32)
+        hip.attention(L, pool, N, cf32(q), cu32(blocks), cu32(np.zeros(nt, np.uint32)),
+                      cu32(pos), H, n - 1, out)
+    hip.check()
+    got = out.cpu().numpy().reshape(nt, H, D)
+    worst = 0.0
+    for j in range(nt):
+        for h in range(H):
+            worst = max(worst, np.abs(got[j, h] - _f64_attention(kd, vd, q[j, h], h // (H // G),
+                                                                 n - nt + j + 1)).max())
+    bound = 1e-6 * np.abs(vd).max()
+    print(f"  {kind}: max |got - f64| = {worst:.2e} (bound {bound:.2e})", flush=True)
+    assert worst < bound, (worst, bound)
+
+
+def test_q8_0_prefill_reports_value_scales_past_its_range(hip):
+    """The MFMA prefill holds dequantised values in f16: a value scale above 512 is
+    reported as UnsupportedError instead of producing infinities; the same pool through
+    decode attention (f32 scales) is fine."""
+    from qubivex_amd import UnsupportedError
+    r = rng(79)
+    G, D, H = 2, 128, 8
+    L = layout(Q8_0, G, D)
+    n = 64
+    N = n // 16 + 2
+    pool = new_pool(L, N)
+    blocks, table_at, _ = fill_items(hip, L, pool, N, [n], r)
+    k = normal(r, (1, L.kv_out)) * 1e5  # amax / 127 > 512
+    v = normal(r, (1, L.kv_out)) * 1e5
+    hip.append(L, pool, N, cf32(k), cf32(v), cu32(slots_of(blocks, table_at, 0, [n - 1], 16)))
+    hip.check()
+    q = normal(r, (1, H, D))
+    out = torch.zeros(H * D, dtype=torch.float32, device="cuda")
+    hip.prefill_attention(L, pool, N, cf32(q), cu32(blocks), cu32(table_at), cu32([n - 1]),
+                          cu32([0]), cu32([1]), H, n - 1, 1, out)
+    with pytest.raises(UnsupportedError, match="scale above 512"):
+        hip.check()
+    hip.attention(L, pool, N, cf32(q), cu32(blocks), cu32(table_at), cu32([n - 1]), H, n - 1, out)
+    hip.check()
+    assert np.isfinite(out.cpu().numpy()).all()
+
+
+@pytest.mark.parametrize("dtype,H,G,D", [(F16, 32, 8, 128), (Q8_0, 32, 8, 128), (F16, 16, 4, 64),
+                                         (Q8_0, 8, 2, 64), (F16, 8, 2, 256)])
+def test_prefill_with_a_dominant_position(hip, dtype, H, G, D):
+    """The prefill kernels' row max over a tile, with one key scaled x40 in each row group
+    and in later tiles (see test_attention_with_a_dominant_position)."""
+    from test_gpu_kernels import dominant_items
+    print(f"prefill dominant {dtype} H={H} G={G} D={D}", flush=True)
+    r = rng(600 + D + G)
+    L = layout(dtype, G, D)
+    lens = [40, 40, 40, 40, 200]
+    big = [3, 7, 11, 15, 100]
+    N, pool, blocks, table_at, sim, _ = dominant_items(hip, L, H, r, lens, big)
+    nt = 20  # the last 20 tokens of each item as one segment
+    q = normal(r, (len(lens) * nt, H, D))
+    pos0 = np.array(lens, np.uint32) - nt
+    q_at = np.arange(len(lens), dtype=np.uint32) * nt
+    out = torch.full((q.size,), float("nan"), dtype=torch.float32, device="cuda")
+    hip.prefill_attention(L, pool, N, cf32(q), cu32(blocks), cu32(table_at), cu32(pos0),
+                          cu32(q_at), cu32([nt] * len(lens)), H, max(lens) - 1, nt, out)
+    hip.check()
+    got = out.cpu().numpy().reshape(len(lens), nt, H, D)
+    worst = (0.0, 0.0)
+    for t, n in enumerate(lens):
+        pos = np.arange(n - nt, n, dtype=np.uint32)
+        want = sim.attention(q[t * nt:(t + 1) * nt], H, blocks,
+                             np.full(nt, table_at[t], np.uint32), pos)
+        assert np.isfinite(got[t]).all(), t
+        max_abs, rel = attn_errors(got[t], want)
+        worst = (max(worst[0], max_abs), max(worst[1], rel))
+    print(f"  max_abs={worst[0]:.2e} rel_l2={worst[1]:.2e}", flush=True)
+    assert worst[0] <= MAX_ABS and worst[1] <= REL_L2, worst
