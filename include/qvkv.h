@@ -149,7 +149,11 @@ int qvkv_attention_async(qvkv_dev *dev, const qvkv_layout *layout, const void *p
  * would for an item with pos = pos0[i]+j; max_pos bounds pos0[i]+n_tok[i]-1 and max_tok
  * bounds n_tok[i].  Replaces the host prefill of the reference's forward pass, which
  * stores a segment's rows and then runs math::attend per (token, head)
- * (crates/qubivex-arch/src/lib.rs:1296-1320); the reference has no device prefill. */
+ * (crates/qubivex-arch/src/lib.rs:1296-1320); the reference has no device prefill.
+ * q8_0 pools at d = 128 use a form that holds dequantised values in f16: a value scale
+ * above 512 (values that may pass 65504) makes the next qvkv_check return
+ * QVKV_E_UNSUPPORTED.  The synchronous entry points (qvkv_decode_attention,
+ * qvkv_prelude_attention) then recompute the chunk with the f32-scale form. */
 int qvkv_prefill_attention_async(qvkv_dev *dev, const qvkv_layout *layout, const void *pool,
                                  uint64_t pool_blocks, const float *q, uint64_t q_rows,
                                  const uint32_t *blocks, uint64_t n_table,

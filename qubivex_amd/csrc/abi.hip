@@ -631,13 +631,14 @@ hipError_t attend_tokens(qvkv_dev *dev, const Geometry &g, const qvkv::AttnPlan 
                          const Segments &sg, const StagedSegments &ss, Stager &st,
                          const void *pool, uint64_t held, const float *dq, const uint32_t *dblocks,
                          uint64_t n_table, const uint32_t *dtable_at, const uint32_t *dpos,
-                         uint32_t s, uint32_t heads, uint32_t max_pos, float *dout) {
+                         uint32_t s, uint32_t heads, uint32_t max_pos, float *dout,
+                         bool f16_values = true) {
     if (sg.max_tok >= 2)
         return qvkv::launch_prefill(g, pool, held, dq, dblocks, n_table,
                                     st.at<uint32_t>(dev, ss.ta), st.at<uint32_t>(dev, ss.p0),
                                     st.at<uint32_t>(dev, ss.qa), st.at<uint32_t>(dev, ss.nt),
                                     (uint32_t)sg.n_tok.size(), heads, max_pos, sg.max_tok, s,
-                                    dout, dev->d_err, dev->stream);
+                                    dout, dev->d_err, dev->stream, f16_values);
     return qvkv::launch_attention(g, plan, pool, held, dq, dblocks, n_table, dtable_at, dpos, s,
                                   heads, max_pos, dout, dev->ws, dev->d_err, dev->stream);
 }
@@ -715,12 +716,22 @@ int qvkv_decode_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *po
     e = qvkv::launch_append(g, pool->ptr, held, st.at<float>(dev, kno), st.at<float>(dev, vno),
                             st.at<uint32_t>(dev, slo), s, dev->d_err, dev->stream);
     if (int rc = launched(dev, e, "append launch (new rows)")) return rc;
-    e = attend_tokens(dev, g, p, sg, ss, st, pool->ptr, held, st.at<float>(dev, qo),
-                      st.at<uint32_t>(dev, bo), n_table, st.at<uint32_t>(dev, tao),
-                      st.at<uint32_t>(dev, po), s, heads, max_pos, st.at<float>(dev, oo));
+    auto attend = [&](bool f16_values) {
+        return attend_tokens(dev, g, p, sg, ss, st, pool->ptr, held, st.at<float>(dev, qo),
+                             st.at<uint32_t>(dev, bo), n_table, st.at<uint32_t>(dev, tao),
+                             st.at<uint32_t>(dev, po), s, heads, max_pos, st.at<float>(dev, oo),
+                             f16_values);
+    };
+    e = attend(true);
     if (int rc = launched(dev, e, "attention launch")) return rc;
     if (int rc = download(dev, out, st.at<void>(dev, oo), qb)) return rc;
-    return finish(dev, dev->stream);
+    int rc = finish(dev, dev->stream);
+    if (rc == QVKV_E_UNSUPPORTED) {  // q8_0 values past the f16 prefill's range: f32 form
+        if (int rc2 = launched(dev, attend(false), "attention launch")) return rc2;
+        if (int rc2 = download(dev, out, st.at<void>(dev, oo), qb)) return rc2;
+        rc = finish(dev, dev->stream);
+    }
+    return rc;
 }
 
 // ---------------------------------------------------------------------------------
@@ -846,16 +857,26 @@ int qvkv_prelude_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *p
     e = qvkv::launch_append(g, pool->ptr, held, dk, dv, st.at<uint32_t>(dev, slo), s, dev->d_err,
                             dev->stream);
     if (int rc = launched(dev, e, "append launch (new rows)")) return rc;
-    e = attend_tokens(dev, g, plan, sg, ss, st, pool->ptr, held, dq, st.at<uint32_t>(dev, bo),
-                      n_table, st.at<uint32_t>(dev, tao), st.at<uint32_t>(dev, po), s, heads,
-                      max_pos, st.at<float>(dev, oo));
+    auto attend = [&](bool f16_values) {
+        return attend_tokens(dev, g, plan, sg, ss, st, pool->ptr, held, dq,
+                             st.at<uint32_t>(dev, bo), n_table, st.at<uint32_t>(dev, tao),
+                             st.at<uint32_t>(dev, po), s, heads, max_pos, st.at<float>(dev, oo),
+                             f16_values);
+    };
+    e = attend(true);
     if (int rc = launched(dev, e, "attention launch")) return rc;
     if (int rc = download(dev, out, st.at<void>(dev, oo), qb)) return rc;
     if (k_new)
         if (int rc = download(dev, k_new, dk, s * rowb)) return rc;
     if (v_new)
         if (int rc = download(dev, v_new, dv, s * rowb)) return rc;
-    return finish(dev, dev->stream);
+    int rc = finish(dev, dev->stream);
+    if (rc == QVKV_E_UNSUPPORTED) {  // q8_0 values past the f16 prefill's range: f32 form
+        if (int rc2 = launched(dev, attend(false), "attention launch")) return rc2;
+        if (int rc2 = download(dev, out, st.at<void>(dev, oo), qb)) return rc2;
+        rc = finish(dev, dev->stream);
+    }
+    return rc;
 }
 
 }  // extern "C"

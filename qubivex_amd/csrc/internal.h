@@ -68,7 +68,7 @@ hipError_t launch_prefill(const Geometry &g, const void *pool, uint64_t pool_blo
                           const uint32_t *table_at, const uint32_t *pos0, const uint32_t *q_at,
                           const uint32_t *n_tok, uint32_t n_seg, uint32_t heads,
                           uint32_t max_pos, uint32_t max_tok, uint64_t q_rows, float *out,
-                          int *err, hipStream_t s);
+                          int *err, hipStream_t s, bool f16_values = true);
 hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *pool,
                             uint64_t pool_blocks, const float *q, const uint32_t *blocks,
                             uint64_t n_table, const uint32_t *table_at, const uint32_t *pos,

@@ -932,7 +932,7 @@ hipError_t launch_prefill(const Geometry &g, const void *pool, uint64_t pool_blo
                           const uint32_t *table_at, const uint32_t *pos0, const uint32_t *q_at,
                           const uint32_t *n_tok, uint32_t n_seg, uint32_t heads,
                           uint32_t max_pos, uint32_t max_tok, uint64_t q_rows, float *out,
-                          int *err, hipStream_t s) {
+                          int *err, hipStream_t s, bool f16_values) {
     if (n_seg == 0 || max_tok == 0) return hipSuccess;
     const Geo geo = to_geo(g);
     const uint8_t *pp = (const uint8_t *)pool;
@@ -961,7 +961,8 @@ hipError_t launch_prefill(const Geometry &g, const void *pool, uint64_t pool_blo
 #undef QV_PF2
         return hipGetLastError();
     }
-    if (q8 && g.D == 128 && tune("QVKV_PREFILL_Q8_FAST", 1)) {
+    // f16_values: the q8_0 MFMA-throughput form, which holds dequantised values in f16
+    if (q8 && g.D == 128 && f16_values && tune("QVKV_PREFILL_Q8_FAST", 1)) {
         const uint32_t n_qb = (uint32_t)(((uint64_t)max_tok * GS + 63) / 64);
         const unsigned grid3 = (unsigned)((uint64_t)n_seg * g.G * n_qb);
         hipLaunchKernelGGL((k_prefill_q8<128>), dim3(grid3), dim3(256), 0, s, pp, pool_blocks, q,

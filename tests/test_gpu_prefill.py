@@ -323,3 +323,35 @@ def test_prefill_with_a_dominant_position(hip, dtype, H, G, D):
         worst = (max(worst[0], max_abs), max(worst[1], rel))
     print(f"  max_abs={worst[0]:.2e} rel_l2={worst[1]:.2e}", flush=True)
     assert worst[0] <= MAX_ABS and worst[1] <= REL_L2, worst
+
+
+def test_host_entry_recomputes_a_q8_0_chunk_past_the_f16_range(hip):
+    """qvkv_decode_attention with a q8_0 prompt chunk whose values pass the f16 range
+    (scales above 512): the MFMA prefill reports the range, and the synchronous entry point
+    recomputes the chunk with the f32-scale form, so the call succeeds and matches the
+    oracle (relative tolerance: the values are ~1e5)."""
+    from qubivex_amd import KvLayout
+
+    r = rng(34)
+    L = KvLayout(Q8_0, 2, 128, 16)
+    H = 8
+    n = 40
+    N = 8
+    buf = hip.alloc(N * L.block_bytes)
+    blocks = r.permutation(N).astype(np.uint32)[:(n + 15) // 16]
+    pos = np.arange(n, dtype=np.uint32)
+    table_at = np.zeros(n, np.uint32)
+    k_new = normal(r, (n, L.kv_out))
+    v_new = normal(r, (n, L.kv_out)) * 1e5
+    q = normal(r, (n, H, 128))
+    got = hip.decode_attention(L, buf, q, H, pos, blocks, table_at,
+                               np.zeros(0, np.float32), np.zeros(0, np.uint32), k_new, v_new)
+    sim = oracle.SimPool(N, 2, 128, 16, oracle.Q8_0)
+    slots = slots_of(blocks, np.zeros(1, np.uint32), 0, pos, 16)
+    sim.store(k_new, v_new, slots)
+    want = sim.attention(q, H, blocks, table_at, pos)
+    assert np.isfinite(got).all()
+    rel = float(np.linalg.norm(got - want) / np.linalg.norm(want))
+    print(f"  rel_l2={rel:.2e}", flush=True)
+    assert rel <= REL_L2
+    buf.close()
