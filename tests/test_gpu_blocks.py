@@ -1,7 +1,8 @@
 """Block sizes other than 16: every kernel addresses positions as block * B + offset with a
-16-position tile inside one block, so B = 32 and B = 256 (the reference's KV_BLOCK,
-crates/qubivex-compute/src/discrete.rs:247-329) must give the same results.  Append and
-gather bit for bit; decode and prefill attention within the reference tolerance."""
+16-position tile inside one block, so B = 32, 48 (not a power of two), 256 (the reference's
+KV_BLOCK, crates/qubivex-compute/src/discrete.rs:247-329) and 4096 (the largest) must give
+the same results.  Append and gather bit for bit; decode and prefill attention within the
+reference tolerance."""
 import numpy as np
 import pytest
 
@@ -12,7 +13,7 @@ pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 
 
-@pytest.mark.parametrize("B", [32, 256])
+@pytest.mark.parametrize("B", [32, 48, 256, 4096])
 @pytest.mark.parametrize("dtype", [F16, Q8_0])
 def test_block_sizes(hip, dtype, B):
     print(f"blocks {dtype} B={B}", flush=True)

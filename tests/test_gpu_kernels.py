@@ -211,6 +211,12 @@ ATTN_CASES = [
     (Q8_0, 8, 2, 64, [33, 300]),
     (Q8_0, 4, 2, 256, [90]),
     (Q8_0, 6, 3, 160, [77]),  # generic kernel
+    # query groups that are not powers of two (3, 5, 6, 12 heads per KV head)
+    (F16, 12, 2, 128, [33, 700]),
+    (F16, 24, 2, 128, [129, 16]),
+    (Q8_0, 12, 4, 128, [50, 513]),
+    (Q8_0, 10, 2, 128, [300]),
+    (Q8_0, 24, 2, 64, [95]),
 ]
 
 

@@ -40,6 +40,12 @@ PREFILL_CASES = [
     (Q8_0, 8, 2, 64, [(130, 66)]),
     (Q8_0, 4, 2, 256, [(90, 20)]),
     (Q8_0, 6, 3, 160, [(70, 12)]),  # generic kernel
+    # query groups that are not powers of two
+    (F16, 12, 2, 128, [(200, 37), (45, 45)]),
+    (F16, 24, 2, 128, [(130, 20)]),
+    (Q8_0, 12, 4, 128, [(150, 40), (17, 17)]),
+    (Q8_0, 10, 2, 128, [(99, 33)]),
+    (F16, 12, 4, 64, [(80, 30)]),
 ]
 
 
