@@ -365,20 +365,32 @@ def test_decode_attention_host_entry(hip):
     buf.close()
 
 
-def test_index_errors_are_reported_not_faulted(hip):
-    """Out-of-range ids come back as ShapeError; the kernels skip them."""
+@pytest.mark.parametrize("dtype,D", [(F16, 64), (F16, 128), (Q8_0, 64), (Q8_0, 128)])
+def test_index_errors_are_reported_not_faulted(hip, dtype, D):
+    """Out-of-range ids come back as ShapeError; the kernels skip them (append, gather and
+    decode attention of every form)."""
     from qubivex_amd import ShapeError
 
-    L = layout(F16, 2, 64)
+    L = layout(dtype, 2, D)
     N = 4
     pool = new_pool(L, N)
-    k = cf32(np.ones((1, 128), np.float32))
+    k = cf32(np.ones((1, 2 * D), np.float32))
     hip.append(L, pool, N, k, k, cu32([N * 16 + 3]))
     with pytest.raises(ShapeError):
         hip.check()
     assert int(pool.count_nonzero()) == 0
-    q = cf32(np.ones((1, 2, 64), np.float32))
-    out = torch.zeros(128, dtype=torch.float32, device="cuda")
+    # gather through a block id past the pool
+    ok = torch.zeros(20 * L.kv_out, dtype=torch.float32, device="cuda")
+    ov = torch.zeros_like(ok)
+    hip.gather(L, pool, N, cu32([0, 9]), cu32([0]), cu32([20]), cu64([0]), 20, ok, ov)
+    with pytest.raises(ShapeError):
+        hip.check()
+    # gather with a table too short for its length
+    hip.gather(L, pool, N, cu32([0]), cu32([0]), cu32([20]), cu64([0]), 20, ok, ov)
+    with pytest.raises(ShapeError):
+        hip.check()
+    q = cf32(np.ones((1, 2, D), np.float32))
+    out = torch.zeros(2 * D, dtype=torch.float32, device="cuda")
     hip.attention(L, pool, N, q, cu32([0, 9]), cu32([0]), cu32([20]), 2, 20, out)
     with pytest.raises(ShapeError):
         hip.check()
@@ -387,6 +399,7 @@ def test_index_errors_are_reported_not_faulted(hip):
     with pytest.raises(ShapeError):
         hip.check()
     hip.check()  # cleared
+    assert int(pool.count_nonzero()) == 0
 
 
 DOMINANT_CASES = [(F16, 32, 8, 128), (Q8_0, 32, 8, 128), (F16, 16, 4, 64), (Q8_0, 8, 2, 64),

@@ -107,18 +107,20 @@ def test_prefill_equals_decode_kernel_per_token(hip):
     assert d < 1e-5, d
 
 
-def test_prefill_rejects_out_of_range_segments(hip):
+@pytest.mark.parametrize("dtype,D", [(F16, 64), (F16, 128), (Q8_0, 128), (Q8_0, 64)])
+def test_prefill_rejects_out_of_range_segments(hip, dtype, D):
     """A segment past max_pos, past max_tok, past q_rows or past its table is a ShapeError
-    and the kernel touches nothing."""
+    and the kernel touches nothing; a block id past the pool is a ShapeError too (every
+    prefill form: register-staged f16, DMA f16, q8_0 MFMA, decode-tile)."""
     from qubivex_amd import ShapeError
 
     r = rng(32)
-    L = layout(F16, 2, 64)
+    L = layout(dtype, 2, D)
     N = 8
     pool = new_pool(L, N)
     blocks, table_at, _ = fill_items(hip, L, pool, N, [40], r)
-    q = cf32(normal(r, (10, 4, 64)))
-    out = torch.zeros(10 * 4 * 64, dtype=torch.float32, device="cuda")
+    q = cf32(normal(r, (10, 4, D)))
+    out = torch.zeros(10 * 4 * D, dtype=torch.float32, device="cuda")
     args = dict(blocks=cu32(blocks), table_at=cu32(table_at))
     bad = [
         (np.array([35], np.uint32), np.array([0], np.uint32), np.array([10], np.uint32), 40, 10),  # max_pos
@@ -132,6 +134,14 @@ def test_prefill_rejects_out_of_range_segments(hip):
         with pytest.raises(ShapeError):
             hip.check()
     assert float(out.abs().sum()) == 0.0
+    # a block id past the pool in the segment's table
+    bad_blocks = blocks.copy()
+    bad_blocks[1] = N + 5
+    hip.prefill_attention(L, pool, N, q, cu32(bad_blocks), args["table_at"], cu32([30]),
+                          cu32([0]), cu32([10]), 4, 39, 10, out)
+    with pytest.raises(ShapeError):
+        hip.check()
+    hip.check()  # cleared
 
 
 def test_host_entry_routes_a_prefill_chunk_through_segments(hip):
