@@ -597,7 +597,7 @@ void k_prefill_q8(QV_PREFILL_PARAMS) {
     constexpr int NDB = D / 16;                // PV d blocks
     constexpr int CPR = D / 8;                 // 8-value (16-byte f16) pieces per row
     constexpr int NGW = D / 64;                // scale words per row (2 groups per word)
-    __shared__ __attribute__((aligned(16))) Q8PrefillSlot<D> sb[2];
+    __shared__ __attribute__((aligned(16))) Q8PrefillSlot<D> sb0, sb1;
 
     const uint32_t G = (uint32_t)geo.G, B = (uint32_t)geo.B;
     const uint32_t GS = H / G;
@@ -672,48 +672,78 @@ void k_prefill_q8(QV_PREFILL_PARAMS) {
         }
     }
 
-    // ---- staging: thread = (position sp = tid / 8, 16-byte piece sj = tid % 8) of the
-    // tile's stored K and V rows, plus the row's 4 V scales; threads 0..63 also move one
-    // word of K scales (position tid / 2).
-    const uint32_t sp = threadIdx.x >> 3, sj = threadIdx.x & 7u;
-    u4v xk, xv;
+    // ---- staging: thread = (position sp, lane sj = tid % 8 of the position) of the tile,
+    // plus the row's 4 V scales; threads 0..63 also move one word of K scales (position
+    // tid / 2).  The LDS stores are laid out to take the fewest bank passes:
+    //   K: store k (0, 1) of lane sj fills LDS slot sj + 8 ((k + si) & 1) of its row, so
+    //      each 8 lanes write one aligned 128-byte half of a row and the two rows of a
+    //      16-lane group write opposite halves; the lane loads the two stored 8-byte chunks
+    //      (4 (P % 4) + P / 4 holds logical piece P) that its slots need;
+    //   V: lane sj loads stored bytes 16 sj .. +15 and writes 8-byte quarter pieces; the
+    //      position order (sp bit 1 = si bit 0, sp bit 3 = si bit 1) puts the rows of each
+    //      2- and 4-row group of an LDS store in distinct 64-byte quarters of the banks.
+    const uint32_t si = threadIdx.x >> 3;
+    const uint32_t sp = ((si & 1u) << 1) | ((si & 2u) << 2) | ((si >> 2) & 1u) |
+                        (((si >> 3) & 1u) << 2) | (si & 16u),
+                   sj = threadIdx.x & 7u;
+    const uint32_t klr = 16u * ((sp >> 2) & 1u) + 4u * (sp >> 3) + (sp & 3u);  // K row in LDS
+    uint32_t kslot[2], kchunk[2];
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        kslot[k] = sj + 8u * ((k + si) & 1u);
+        const uint32_t P = kslot[k] ^ kswz<D>(klr);  // logical piece of the slot
+        kchunk[k] = 4u * (P & 3u) + (P >> 2);       // stored 8-byte chunk holding it
+    }
+    u2v xk[2];
+    u4v xv;
     u2v xvs;
     uint32_t xks;
+    // The block of each 16-position half of a tile, resolved on the scalar unit (a
+    // constant-address-space load of the table entry): the block base and the first row
+    // of the half (g * B + its offset in the block), or null past n_wg / for a bad id.
+    struct Half {
+        const uint8_t *base;
+        uint32_t row0;
+    };
+    auto half_of = [&](uint32_t ph) -> Half {
+        if (ph >= n_wg) return Half{nullptr, 0u};
+        const uint32_t bi = geo.fd_b.div(ph);
+        const uint32_t blk = ((const __attribute__((address_space(4))) uint32_t *)blocks)[tab + bi];
+        if (blk >= pool_blocks) {
+            if (threadIdx.x == 0) flag(err, ERR_BLOCK);
+            return Half{nullptr, 0u};
+        }
+        return Half{pool + (uint64_t)blk * geo.bb, g * B + (ph - bi * B)};
+    };
     auto load = [&](uint32_t t) {
-        const uint32_t p = t * TP + sp;
-        xk = u4v{0u, 0u, 0u, 0u};
+        const uint32_t p0 = t * TP;
+        const Half h0 = half_of(p0), h1 = half_of(p0 + 16u);
+        xk[0] = u2v{0u, 0u};
+        xk[1] = u2v{0u, 0u};
         xv = u4v{0u, 0u, 0u, 0u};
         xvs = u2v{0u, 0u};
         xks = 0u;
-        const uint32_t pk = t * TP + (threadIdx.x >> 1);  // K-scale position (tid < 64)
-        if (p < n_wg) {
-            const uint32_t blk = blocks[tab + p / B];
-            if (blk >= pool_blocks) {
-                flag(err, ERR_BLOCK);
-            } else {
-                const uint8_t *base = pool + (uint64_t)blk * geo.bb;
-                const uint64_t rw = (uint64_t)g * B + p % B;
-                xk = *(const u4v *)(base + geo.k_off + rw * D + 16u * sj);
-                xv = *(const u4v *)(base + geo.v_off + rw * D + 16u * sj);
-                xvs = *(const u2v *)(base + geo.vs_off + rw * (D / 16));
-            }
+        const Half &hp = (sp & 16u) ? h1 : h0;
+        if (hp.base != nullptr && p0 + sp < n_wg) {
+            const uint32_t rw = hp.row0 + (sp & 15u);
+            xk[0] = *(const u2v *)(hp.base + geo.k_off + rw * D + 8u * kchunk[0]);
+            xk[1] = *(const u2v *)(hp.base + geo.k_off + rw * D + 8u * kchunk[1]);
+            xv = *(const u4v *)(hp.base + geo.v_off + rw * D + 16u * sj);
+            xvs = *(const u2v *)(hp.base + geo.vs_off + rw * (D / 16));
         }
-        if (threadIdx.x < 64u && pk < n_wg) {
-            const uint32_t blk = blocks[tab + pk / B];
-            if (blk < pool_blocks)
-                xks = *(const uint32_t *)(pool + (uint64_t)blk * geo.bb + geo.ks_off +
-                                          ((uint64_t)g * B + pk % B) * (D / 16) + 4u * (threadIdx.x & 1u));
-        }
+        // K scales: threads 0..63, position tid / 2, word tid % 2
+        const uint32_t pk = threadIdx.x >> 1;
+        const Half &hk = (pk & 16u) ? h1 : h0;
+        if (threadIdx.x < 64u && hk.base != nullptr && p0 + pk < n_wg)
+            xks = *(const uint32_t *)(hk.base + geo.ks_off + (hk.row0 + (pk & 15u)) * (D / 16) +
+                                      4u * (threadIdx.x & 1u));
     };
     auto store = [&](Q8PrefillSlot<D> &sl) {
-        // K: stored bytes 16 sj .. +15 hold d = 32 i + 8 q + t with q = sj / 2 and
-        // i = 2 (sj % 2) + {0, 1}: two logical pieces 4 i + q
-        const uint32_t lr = 16u * ((sp >> 2) & 1u) + 4u * (sp >> 3) + (sp & 3u);
+        // K: each loaded 8-byte chunk is one logical 8-value piece, stored at its slot
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const uint32_t piece = 4u * (2u * (sj & 1u) + h) + (sj >> 1);
-            const h4 a = i8x4_to_h4_vals(xk[2 * h]), b = i8x4_to_h4_vals(xk[2 * h + 1]);
-            *(h8 *)(sl.k + (lr * CPR + (piece ^ kswz<D>(lr))) * 8) =
+        for (int k = 0; k < 2; k++) {
+            const h4 a = i8x4_to_h4_vals(xk[k].x), b = i8x4_to_h4_vals(xk[k].y);
+            *(h8 *)(sl.k + (klr * CPR + kslot[k]) * 8) =
                 h8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
         }
         // V: stored byte c * 8 + 2 gr + u holds d = 32 gr + 2 c + u; this piece holds
@@ -731,8 +761,10 @@ void k_prefill_q8(QV_PREFILL_PARAMS) {
                 x01 = __builtin_bit_cast(h2, i8x2_to_h2<0>(w0));
                 x23 = __builtin_bit_cast(h2, i8x2_to_h2<0>(w1));
             }
-            const _Float16 sc = __builtin_bit_cast(_Float16, (uint16_t)(xvs[gr >> 1] >> (16u * (gr & 1u))));
-            big |= !((float)sc <= 512.0f) && (float)sc == (float)sc;
+            const uint32_t sbits = (xvs[gr >> 1] >> (16u * (gr & 1u))) & 0xffffu;
+            const _Float16 sc = __builtin_bit_cast(_Float16, (uint16_t)sbits);
+            // |scale| above 512 (f16 0x6000), infinities included, NaN (above 0x7c00) not
+            big |= (sbits & 0x7fffu) - 0x6001u < 0x7c00u - 0x6000u;
             const h2 s2 = {sc, sc};
             h2 a = x01 * s2, b = x23 * s2;       // high parts (rounded products)
             asm volatile("" : "+v"(a), "+v"(b));  // not contracted into the residuals
@@ -850,15 +882,21 @@ void k_prefill_q8(QV_PREFILL_PARAMS) {
         }
     };
 
-    load(0);
-    store(sb[0]);
-    __syncthreads();
-    for (uint32_t t = 0; t < ntiles; t++) {
-        const int buf = (int)(t & 1u);
+    // Tile t is computed from one buffer while tile t + 1 is loaded into registers and then
+    // stored into the other; the loop is unrolled by two so both buffers have fixed LDS
+    // addresses.
+    auto step = [&](uint32_t t, const Q8PrefillSlot<D> &cur, Q8PrefillSlot<D> &nxt) {
         if (t + 1 < ntiles) load(t + 1);
-        tile(sb[buf], t * TP);
-        if (t + 1 < ntiles) store(sb[buf ^ 1]);
+        tile(cur, t * TP);
+        if (t + 1 < ntiles) store(nxt);
         __syncthreads();
+    };
+    load(0);
+    store(sb0);
+    __syncthreads();
+    for (uint32_t t = 0; t < ntiles; t += 2) {
+        step(t, sb0, sb1);
+        if (t + 1 < ntiles) step(t + 1, sb1, sb0);
     }
     if (!wave_live) return;
     l += __shfl_xor(l, 16);
