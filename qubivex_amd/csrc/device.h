@@ -94,6 +94,43 @@ __device__ __forceinline__ h4 i8x4_to_h4_vals(uint32_t w) {
     return h4_of(a, b);
 }
 
+// Two MFMA operands in one block (one s_nop for both): i8x8_to_h4x2: bytes 0..3 of w0
+// and of w1; bytes_to_h4x2<BY>: byte BY, then byte BY + 1, of w0, w1, w2, w3.
+__device__ __forceinline__ void i8x8_to_h4x2(uint32_t w0, uint32_t w1, h4 &x, h4 &y) {
+    uint32_t a, b, c, d;
+    asm(QV_CVT("%0", "%4", "WORD_0", "UNUSED_PAD", "BYTE_0")
+        QV_CVT("%0", "%4", "WORD_1", "UNUSED_PRESERVE", "BYTE_1")
+        QV_CVT("%1", "%4", "WORD_0", "UNUSED_PAD", "BYTE_2")
+        QV_CVT("%1", "%4", "WORD_1", "UNUSED_PRESERVE", "BYTE_3")
+        QV_CVT("%2", "%5", "WORD_0", "UNUSED_PAD", "BYTE_0")
+        QV_CVT("%2", "%5", "WORD_1", "UNUSED_PRESERVE", "BYTE_1")
+        QV_CVT("%3", "%5", "WORD_0", "UNUSED_PAD", "BYTE_2")
+        QV_CVT("%3", "%5", "WORD_1", "UNUSED_PRESERVE", "BYTE_3") "s_nop 1"
+        : "=&v"(a), "=&v"(b), "=&v"(c), "=&v"(d) : "v"(w0), "v"(w1));
+    x = h4_of(a, b);
+    y = h4_of(c, d);
+}
+#define QV_CVT8(B0, B1)                                                                         \
+    QV_CVT("%0", "%4", "WORD_0", "UNUSED_PAD", B0) QV_CVT("%0", "%5", "WORD_1", "UNUSED_PRESERVE", B0) \
+    QV_CVT("%1", "%6", "WORD_0", "UNUSED_PAD", B0) QV_CVT("%1", "%7", "WORD_1", "UNUSED_PRESERVE", B0) \
+    QV_CVT("%2", "%4", "WORD_0", "UNUSED_PAD", B1) QV_CVT("%2", "%5", "WORD_1", "UNUSED_PRESERVE", B1) \
+    QV_CVT("%3", "%6", "WORD_0", "UNUSED_PAD", B1) QV_CVT("%3", "%7", "WORD_1", "UNUSED_PRESERVE", B1) \
+    "s_nop 1"
+template <int BY>
+__device__ __forceinline__ void bytes_to_h4x2(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
+                                              h4 &x, h4 &y) {
+    uint32_t a, b, c, d;
+    if constexpr (BY == 0)
+        asm(QV_CVT8("BYTE_0", "BYTE_1")
+            : "=&v"(a), "=&v"(b), "=&v"(c), "=&v"(d) : "v"(w0), "v"(w1), "v"(w2), "v"(w3));
+    else
+        asm(QV_CVT8("BYTE_2", "BYTE_3")
+            : "=&v"(a), "=&v"(b), "=&v"(c), "=&v"(d) : "v"(w0), "v"(w1), "v"(w2), "v"(w3));
+    x = h4_of(a, b);
+    y = h4_of(c, d);
+}
+#undef QV_CVT8
+
 // Bytes BY and BY + 1 of w -> two f16 (low, high half); for a non-MFMA consumer.
 template <int BY>
 __device__ __forceinline__ uint32_t i8x2_to_h2(uint32_t w) {
@@ -302,8 +339,10 @@ __device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<
 #pragma unroll
         for (int gi = 0; gi < NG; gi++) {
             f4 sg = f4{0.f, 0.f, 0.f, 0.f};
-            sg = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4(t.k[2 * gi]), qf[2 * gi], sg, 0, 0, 0);
-            sg = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4(t.k[2 * gi + 1]), qf[2 * gi + 1], sg, 0, 0, 0);
+            h4 ka, kb;
+            i8x8_to_h4x2(t.k[2 * gi], t.k[2 * gi + 1], ka, kb);
+            sg = __builtin_amdgcn_mfma_f32_16x16x16f16(ka, qf[2 * gi], sg, 0, 0, 0);
+            sg = __builtin_amdgcn_mfma_f32_16x16x16f16(kb, qf[2 * gi + 1], sg, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; i++) s[i] = fmaf(sg[i], half_at(t.ks, i * NG + gi), s[i]);
         }
@@ -380,19 +419,12 @@ __device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<
         // P'.V for the two MFMAs of group gi (bytes 2gi, 2gi+1 of each row's run): the B
         // operand of MFMA j is byte j % 4 of word j / 4 of rows 0..3, converted by SDWA.
         auto pv_group = [&](const h4 &pa, int gi) {
-#pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const int j = 2 * gi + u;
-                const int wd = j >> 2;
-                h4 bop;
-                switch (j & 3) {
-                    case 0: bop = bytes_to_h4<0>(vw[0][wd], vw[1][wd], vw[2][wd], vw[3][wd]); break;
-                    case 1: bop = bytes_to_h4<1>(vw[0][wd], vw[1][wd], vw[2][wd], vw[3][wd]); break;
-                    case 2: bop = bytes_to_h4<2>(vw[0][wd], vw[1][wd], vw[2][wd], vw[3][wd]); break;
-                    default: bop = bytes_to_h4<3>(vw[0][wd], vw[1][wd], vw[2][wd], vw[3][wd]); break;
-                }
-                st.acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, bop, st.acc[j], 0, 0, 0);
-            }
+            const int wd = gi >> 1;  // MFMAs j = 2 gi, 2 gi + 1: bytes 2 (gi % 2), +1
+            h4 b0, b1;
+            if (gi & 1) bytes_to_h4x2<2>(vw[0][wd], vw[1][wd], vw[2][wd], vw[3][wd], b0, b1);
+            else bytes_to_h4x2<0>(vw[0][wd], vw[1][wd], vw[2][wd], vw[3][wd], b0, b1);
+            st.acc[2 * gi] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, b0, st.acc[2 * gi], 0, 0, 0);
+            st.acc[2 * gi + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, b1, st.acc[2 * gi + 1], 0, 0, 0);
         };
         if constexpr (PK) {
             // Groups 2m and 2m+1 share one A operand: the scales of row i are the low and
