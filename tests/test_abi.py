@@ -71,3 +71,67 @@ def test_open_without_a_device_is_a_device_error():
 
     with pytest.raises(DeviceError):
         HipDevice(0)
+
+
+def _prototypes():
+    """name -> number of parameters, from the header's prototypes."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    protos = {}
+    for m in re.finditer(r"\b(qvkv_[a-z0-9_]+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
+        args = m.group(2).strip()
+        protos[m.group(1)] = 0 if args in ("", "void") else args.count(",") + 1
+    return protos
+
+
+def test_ctypes_signatures_match_the_prototypes():
+    """The Python binding declares as many arguments as each C prototype takes."""
+    from qubivex_amd import _lib
+
+    protos = _prototypes()
+    assert set(protos) == set(declared())
+    for name, n in protos.items():
+        assert len(_lib.SIGNATURES[name][1]) == n, (name, n, len(_lib.SIGNATURES[name][1]))
+
+
+@pytest.mark.parametrize("lang", ["c", "c++"])
+def test_header_compiles_standalone(tmp_path, lang):
+    """include/qvkv.h is a plain C header (what bindgen, cgo or a JNI shim would read)."""
+    src = tmp_path / ("h.c" if lang == "c" else "h.cpp")
+    src.write_text('#include "qvkv.h"\nint main(void) { return 0; }\n')
+    cc = ["gcc", "-std=c99"] if lang == "c" else ["g++", "-std=c++11"]
+    r = subprocess.run(cc + ["-Wall", "-Werror", "-pedantic", "-fsyntax-only", "-I",
+                             os.path.dirname(HEADER), str(src)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
+def test_a_c_program_links_and_calls_the_library(tmp_path):
+    """A C consumer links libqvkv.so and calls a GPU-free entry point through the header:
+    the layout size rule and the thread-local error text."""
+    from qubivex_amd import _lib
+
+    src = tmp_path / "use.c"
+    src.write_text(r'''
+#include <stdio.h>
+#include <string.h>
+#include "qvkv.h"
+int main(void) {
+    qvkv_layout l = {QVKV_Q8_0, 8, 128, 16};
+    uint64_t bytes = 0;
+    if (qvkv_block_bytes(&l, &bytes) != QVKV_OK || bytes != 2ull * 16 * 8 * 128 * 34 / 32) return 1;
+    qvkv_layout bad = {QVKV_F16, 4, 100, 16};
+    if (qvkv_block_bytes(&bad, &bytes) != QVKV_E_SHAPE) return 2;
+    char msg[256];
+    qvkv_last_error(msg, sizeof msg);
+    if (strstr(msg, "shape mismatch") == NULL) return 3;
+    puts("ok");
+    return 0;
+}
+''')
+    exe = tmp_path / "use"
+    libdir = os.path.dirname(_lib.LIB)
+    r = subprocess.run(["gcc", "-std=c99", "-I", os.path.dirname(HEADER), str(src), "-L", libdir,
+                        "-lqvkv", "-Wl,-rpath," + libdir, "-o", str(exe)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    r = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert r.returncode == 0 and r.stdout.strip() == "ok", (r.returncode, r.stdout, r.stderr)
