@@ -153,7 +153,10 @@ int qvkv_attention_async(qvkv_dev *dev, const qvkv_layout *layout, const void *p
  * q8_0 pools at d = 128 use a form that holds dequantised values in f16: a value scale
  * above 512 (values that may pass 65504) makes the next qvkv_check return
  * QVKV_E_UNSUPPORTED.  The synchronous entry points (qvkv_decode_attention,
- * qvkv_prelude_attention) then recompute the chunk with the f32-scale form. */
+ * qvkv_prelude_attention) then recompute the chunk with the f32-scale form.
+ * Non-finite stored values: a NaN or infinity at one of a segment's own positions reaches
+ * the segment's earlier tokens as NaN, and in f16 pools at d = 64 or 128 an infinity can
+ * give NaN where the CPU path gives an infinity; finite values are unaffected. */
 int qvkv_prefill_attention_async(qvkv_dev *dev, const qvkv_layout *layout, const void *pool,
                                  uint64_t pool_blocks, const float *q, uint64_t q_rows,
                                  const uint32_t *blocks, uint64_t n_table,

@@ -171,6 +171,22 @@ __device__ __forceinline__ float add_xor8(float x) {
                                                                   0xf, false));
 }
 
+// The sum of a high part and its residual held in lanes l and l ^ 8 (lanes with hi_col
+// hold the high part): hi + lo, or hi alone when hi is infinite (the residual of an
+// infinite product is inf * 0 = NaN or an infinity of the other sign, where the f32
+// product the split stands for is just the infinity).  Both lanes get the same value.
+__device__ __forceinline__ float split_sum(float x, bool hi_col) {
+    const float o = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x),
+                                                                       0x128 /* row_ror:8 */, 0xf,
+                                                                       0xf, false));
+    const float hi = hi_col ? x : o, lo = hi_col ? o : x;
+    return __builtin_isinf(hi) ? hi : hi + lo;
+}
+// The same for a high part in lane l and its residual in lane l ^ 32.
+__device__ __forceinline__ float split_sum32(float hi, float lo) {
+    return __builtin_isinf(hi) ? hi : hi + lo;
+}
+
 // max of x over lanes l, l ^ 16, l ^ 32, l ^ 48.  v_permlane16_swap (vdst, vsrc both x)
 // leaves x of rows (0, 0, 2, 2) in one result and (1, 1, 3, 3) in the other; the max of
 // the two is the max over l and l ^ 16.  v_permlane32_swap does the same for halves.
@@ -353,6 +369,17 @@ __device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<
     const bool partial = p0 + 16u > n_max;  // wave-uniform
 #pragma unroll
     for (int i = 0; i < 4; i++) sc[i] = add_xor8(s[i]);
+    if constexpr (!Q8) {
+        // An infinite key makes the high column's q_hi k infinite and the residual's
+        // inf * q_lo NaN (q_lo = 0) or an opposite infinity, where the reference's q . k is
+        // just the infinity: when a sum came out NaN, redo the tile's sums with an infinite
+        // high part standing alone (rare, so the common path keeps the single add).
+        const bool nan_sum = (sc[0] != sc[0]) | (sc[1] != sc[1]) | (sc[2] != sc[2]) | (sc[3] != sc[3]);
+        if (__builtin_expect(__any(nan_sum), 0)) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) sc[i] = split_sum(s[i], hi_col);
+        }
+    }
     if (__any(p0 + 16u > n_col)) {
 #pragma unroll
         for (int i = 0; i < 4; i++)

@@ -837,7 +837,11 @@ __device__ __forceinline__ void attn_body(QV_ATTN_PARAMS) {
 #pragma unroll
     for (int j = 0; j < NJ; j++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) acc[j][i] += __shfl_xor(acc[j][i], 32);
+        for (int i = 0; i < 4; i++) {
+            const float o = __shfl_xor(acc[j][i], 32);
+            // rows 0-7 hold P_hi . V, rows 8-15 P_lo . V (lanes qg < 2 keep the sum)
+            acc[j][i] = Q8 ? acc[j][i] + o : split_sum32(acc[j][i], o);
+        }
     if (qg == 0 && c < 8) {
         sm[w][c] = m;
         sl[w][c] = l;

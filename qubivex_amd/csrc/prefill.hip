@@ -98,7 +98,10 @@ __global__ __launch_bounds__(256) void k_prefill_mfma(QV_PREFILL_PARAMS) {
 #pragma unroll
     for (int j = 0; j < NJ; j++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) st.acc[j][i] += __shfl_xor(st.acc[j][i], 32);
+        for (int i = 0; i < 4; i++) {
+            const float o = __shfl_xor(st.acc[j][i], 32);
+            st.acc[j][i] = Q8 ? st.acc[j][i] + o : split_sum32(st.acc[j][i], o);
+        }
     float lr[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) lr[i] = __shfl(l, 4 * (int)(qg & 1u) + i);

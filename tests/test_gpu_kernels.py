@@ -3,6 +3,8 @@
 Append, gather and block copy are checked bit for bit; attention within max-abs 2e-3
 and relative L2 1e-3 of the oracle's `attend` (f32, the reference's sequential order).
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -445,3 +447,89 @@ def test_attention_with_a_dominant_position(hip, dtype, H, G, D):
     max_abs, rel = attn_errors(got, want)
     print(f"  max_abs={max_abs:.2e} rel_l2={rel:.2e}", flush=True)
     assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)
+
+
+POISON_CASES = [(F16, 32, 8, 128), (F16, 8, 2, 64), (F16, 8, 2, 256), (F16, 4, 4, 96),
+                (Q8_0, 32, 8, 128), (Q8_0, 8, 2, 64), (Q8_0, 8, 2, 256)]
+
+
+@pytest.mark.parametrize("dtype,H,G,D", POISON_CASES)
+@pytest.mark.parametrize("poison", [float("nan"), float("inf"), float("-inf")])
+@pytest.mark.parametrize("where", ["k", "v"])
+def test_attention_propagates_nan_and_inf_like_the_reference(hip, dtype, H, G, D, poison, where):
+    """One K or V element of one written position is NaN or +-inf (the reference kernel
+    harness, crates/qubivex-backend-vulkan/tests/attention_spike.rs:468-486): the outputs
+    are NaN exactly where the CPU path's are (q8_0 quantizes the poison first, as the
+    reference's quantizer does), and finite outputs stay within tolerance.  Decode attention
+    for every form; prefill for q8_0, for NaN, and for the f16 forms that keep the high
+    part and residual of q and p apart.  The f16 MFMA prefill at d = 64 and 128 accumulates
+    both into one MFMA accumulator, so an infinite f16 key or value (a value past 65504 at
+    append) can give NaN there where the reference gives an infinity or a finite value.
+    And in every prefill form a non-finite value at one of a segment's own positions
+    reaches the segment's earlier tokens as NaN: their probability for it is masked to 0
+    and the MFMA's 0 * NaN is NaN.  So the prefill checks keep the poison before the
+    segments (item 2's segment is its one poisoned last token)."""
+    r = rng(700 + D + G)
+    L = layout(dtype, G, D)
+    lens = [40, 40, 17]
+    N = sum((n + 15) // 16 for n in lens) + 3
+    pool = new_pool(L, N)
+    blocks, table_at, sim = fill_items(hip, L, pool, N, lens, r)
+    # item 0 position 5, KV head 0, d = 3 (and item 2, its last position)
+    for t, p in ((0, 5), (2, 16)):
+        k = normal(r, (1, L.kv_out))
+        v = normal(r, (1, L.kv_out))
+        (k if where == "k" else v)[0, 3] = poison
+        sl = slots_of(blocks, table_at, t, [p], L.block)
+        hip.append(L, pool, N, cf32(k), cf32(v), cu32(sl))
+        sim.store(k, v, sl)
+    hip.check()
+    q = normal(r, (len(lens), H, D))
+    pos = np.array(lens, np.uint32) - 1
+    out = torch.zeros(len(lens) * H * D, dtype=torch.float32, device="cuda")
+    hip.attention(L, pool, N, cf32(q), cu32(blocks), cu32(table_at), cu32(pos), H, int(pos.max()), out)
+    hip.check()
+    got = out.cpu().numpy().reshape(len(lens), H, D)
+    want = sim.attention(q, H, blocks, table_at, pos)
+    assert np.array_equal(np.isnan(got), np.isnan(want)), (np.isnan(got).sum(), np.isnan(want).sum())
+    fin = ~np.isnan(want)
+    assert np.array_equal(np.isinf(got[fin]), np.isinf(want[fin]))
+    ok = np.isfinite(want)
+    if ok.any():
+        assert np.abs(got[ok] - want[ok]).max() <= MAX_ABS
+    if dtype == F16 and D in (64, 128) and not np.isnan(poison):
+        return
+    # prefill: the last 10 tokens of items 0 and 1, the last token of item 2
+    n_tok = np.array([10, 10, 1], np.uint32)
+    T = int(n_tok.sum())
+    qp = normal(r, (T, H, D))
+    outp = torch.zeros(qp.size, dtype=torch.float32, device="cuda")
+    pos0 = (np.array(lens) - n_tok).astype(np.uint32)
+    q_at = np.concatenate([[0], np.cumsum(n_tok)[:-1]]).astype(np.uint32)
+
+    def prefill():
+        hip.prefill_attention(L, pool, N, cf32(qp), cu32(blocks), cu32(table_at), cu32(pos0),
+                              cu32(q_at), cu32(n_tok), H, int(max(lens)) - 1, int(n_tok.max()), outp)
+        hip.check()
+
+    if dtype == Q8_0 and D == 128 and where == "v" and np.isinf(poison):
+        # an infinite value scale: the MFMA prefill reports its range; the f32-scale form
+        from qubivex_amd import UnsupportedError
+        with pytest.raises(UnsupportedError):
+            prefill()
+        os.environ["QVKV_PREFILL_Q8_FAST"] = "0"
+        try:
+            prefill()
+        finally:
+            del os.environ["QVKV_PREFILL_Q8_FAST"]
+    else:
+        prefill()
+    gotp = outp.cpu().numpy().reshape(T, H, D)
+    ta = np.repeat(table_at, n_tok).astype(np.uint32)
+    pt = np.concatenate([np.arange(p, p + m) for p, m in zip(pos0, n_tok)]).astype(np.uint32)
+    wantp = sim.attention(qp, H, blocks, ta, pt)
+    assert np.array_equal(np.isnan(gotp), np.isnan(wantp)), (np.isnan(gotp).sum(), np.isnan(wantp).sum())
+    assert np.array_equal(np.isinf(gotp), np.isinf(wantp))
+    ok = np.isfinite(wantp)
+    if ok.any():
+        assert np.abs(gotp[ok] - wantp[ok]).max() <= MAX_ABS
