@@ -207,3 +207,39 @@ def test_host_entry_points_reject_null_arrays(hip):
         with pytest.raises(ShapeError):
             _lib.check(call())
     buf.close()
+
+
+def test_a_dropped_sync_row_is_caught(hip):
+    """Positive control for the host-authoritative sync (discrete.rs:951-1009): the same
+    call with one sync row left out no longer matches the oracle that has every row."""
+    from qubivex_amd import KvLayout
+
+    L = KvLayout("f16", 2, 64, 16)
+    H = 8
+    r = np.random.default_rng(77)
+    N = 8
+    n = 50
+    pos = np.array([n], np.uint32)
+    blocks, table_at = random_tables(r, [n + 1], 16, N)
+    sync = r.standard_normal((n, 2 * L.kv_out)).astype(np.float32)
+    sync_to = slots_of(blocks, table_at, 0, np.arange(n), 16)
+    kn = r.standard_normal((1, L.kv_out)).astype(np.float32)
+    vn = r.standard_normal((1, L.kv_out)).astype(np.float32)
+    q = (4.0 * r.standard_normal((1, H, 64))).astype(np.float32)  # peaked scores
+    sim = oracle.SimPool(N, 2, 64, 16, oracle.F16)
+    sim.store(sync[:, :L.kv_out], sync[:, L.kv_out:], sync_to)
+    sim.store(kn, vn, slots_of(blocks, table_at, 0, [n], 16))
+    want = sim.attention(q, H, blocks, table_at, pos)
+    buf = hip.alloc(N * L.block_bytes)
+    got = hip.decode_attention(L, buf, q, H, pos, blocks, table_at, sync.reshape(-1), sync_to, kn, vn)
+    e = attn_errors(got, want)
+    assert e[0] <= MAX_ABS and e[1] <= REL_L2, e
+    buf.close()
+    buf = hip.alloc(N * L.block_bytes)
+    hip.write(buf, 0, bytes(N * L.block_bytes))  # the dropped row reads as zeros
+    keep = np.arange(n) != 20
+    got = hip.decode_attention(L, buf, q, H, pos, blocks, table_at, sync[keep].reshape(-1),
+                               sync_to[keep], kn, vn)
+    e = attn_errors(got, want)
+    assert not (e[0] <= MAX_ABS and e[1] <= REL_L2), e
+    buf.close()

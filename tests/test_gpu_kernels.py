@@ -533,3 +533,49 @@ def test_attention_propagates_nan_and_inf_like_the_reference(hip, dtype, H, G, D
     ok = np.isfinite(wantp)
     if ok.any():
         assert np.abs(gotp[ok] - wantp[ok]).max() <= MAX_ABS
+
+
+@pytest.mark.parametrize("dtype", [F16, Q8_0])
+def test_parity_checks_catch_broken_rules(hip, dtype):
+    """Positive controls for the parity checks above (the reference's habit,
+    docs/engineering/VULKAN_EXECUTION_AUDIT.md:2499-2513): the same kernel outputs
+    compared with an oracle that breaks one rule must fail the check -- a table entry
+    swapped with another item's, the causal limit one position short, every tile read from
+    the item's first block."""
+    r = rng(900 + (dtype == Q8_0))
+    L = layout(dtype, 8, 128)
+    H = 32
+    lens = [300, 130, 47]
+    N = sum((n + 15) // 16 for n in lens) + 3
+    pool = new_pool(L, N)
+    blocks, table_at, sim = fill_items(hip, L, pool, N, lens, r)
+    q = normal(r, (len(lens), H, 128))
+    pos = np.array(lens, np.uint32) - 1
+    out = torch.zeros(len(lens) * H * 128, dtype=torch.float32, device="cuda")
+    hip.attention(L, pool, N, cf32(q), cu32(blocks), cu32(table_at), cu32(pos), H, int(pos.max()), out)
+    hip.check()
+    got = out.cpu().numpy().reshape(len(lens), H, 128)
+
+    def passes(want):
+        e = attn_errors(got, want)
+        return e[0] <= MAX_ABS and e[1] <= REL_L2
+
+    assert passes(sim.attention(q, H, blocks, table_at, pos))
+    # (a swap inside one item's visible range would not show: attention is a sum over
+    # positions, blind to their order; swap a block between two items)
+    swapped = blocks.copy()
+    swapped[[1, table_at[1] + 1]] = swapped[[table_at[1] + 1, 1]]
+    assert not passes(sim.attention(q, H, swapped, table_at, pos))
+    assert not passes(sim.attention(q, H, blocks, table_at, pos - 1))
+    first = np.repeat(blocks[table_at], [(n + 15) // 16 for n in lens]).astype(np.uint32)
+    assert not passes(sim.attention(q, H, first, table_at, pos))
+    # gather: bit-exact, so one swapped entry is caught
+    total = int(sum(lens))
+    out_at = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.uint64)
+    ok = torch.zeros(total * L.kv_out, dtype=torch.float32, device="cuda")
+    ov = torch.zeros_like(ok)
+    hip.gather(L, pool, N, cu32(blocks), cu32(table_at), cu32(lens), cu64(out_at), max(lens), ok, ov)
+    hip.check()
+    gk = ok.cpu().numpy()[: lens[0] * L.kv_out]
+    assert np.array_equal(gk.view(np.uint32), sim.gather(blocks, table_at, 0, lens[0])[0].reshape(-1).view(np.uint32))
+    assert not np.array_equal(gk.view(np.uint32), sim.gather(swapped, table_at, 0, lens[0])[0].reshape(-1).view(np.uint32))
