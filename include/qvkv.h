@@ -98,7 +98,10 @@ int qvkv_write(qvkv_dev *dev, qvkv_buf *buf, size_t offset, const void *host, si
 /* Device bytes back to the host (the readback of k_new/v_new in the reference). */
 int qvkv_read(qvkv_dev *dev, const qvkv_buf *buf, size_t offset, void *host, size_t len);
 /* Waits for `stream` (as given: 0 is the null stream) and reports any index error a
- * kernel latched since the last check (QVKV_E_SHAPE), clearing it. */
+ * kernel latched since the last check (QVKV_E_SHAPE), or the q8_0 prefill's range report
+ * alone (QVKV_E_UNSUPPORTED), clearing it.  The latch is one per device: with kernels in
+ * flight on several streams, a check reports what any of them latched, and the
+ * synchronous entry points check it too. */
 int qvkv_check(qvkv_dev *dev, void *stream);
 
 /* ---- layout ---- */
