@@ -565,6 +565,14 @@ __device__ __forceinline__ void store_run(float *dst, const float *y, int n) {
     else __builtin_nontemporal_store(f2v{y[0], y[1]}, (f2v *)dst);
 }
 
+// A wave's LDS writes before its reads of other lanes' data, and those reads before the
+// next writes: a wave's LDS operations execute in issue order, so this waits for its LDS
+// counter and keeps the compiler from moving LDS accesses across (no wave fence: on gfx9
+// a fence also waits for every outstanding global load and store).
+__device__ __forceinline__ void lds_order() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
 template <int D>
 __global__ __launch_bounds__(256) void k_gather_q8(const uint8_t *__restrict__ pool,
                                                    uint64_t pool_blocks,
@@ -601,6 +609,8 @@ __global__ __launch_bounds__(256) void k_gather_q8(const uint8_t *__restrict__ p
     }
     const uint32_t r0 = p0 % B;
     const uint8_t *base = pool + (uint64_t)blk * geo.bb;
+    // d = 128 keys: a per-wave LDS copy of the wave's 8 rows (row stride 132 floats)
+    __shared__ __attribute__((aligned(16))) float kx[4][D == 128 ? 8 * 132 : 4];
     constexpr uint32_t PR = D / 16;           // pieces per row
     constexpr uint32_t NS = D / 32;           // scales per row
     constexpr uint32_t NC = D >= 256 ? 1 : 256 / D, NG = 8 / NC;
@@ -643,6 +653,27 @@ __global__ __launch_bounds__(256) void k_gather_q8(const uint8_t *__restrict__ p
             };
             if (!isv) {
                 const uint32_t qq = (16u * j) / (D / 4), i0 = ((16u * j) % (D / 4)) / 8u;
+                if constexpr (D == 128) {
+                    // The piece's two 8-value runs go through the row's LDS copy in
+                    // logical order, and lane j writes d = 32 k + 4 j .. +3 for k = 0..3:
+                    // each store instruction then covers whole 128-byte output lines.
+                    float *rowbuf = kx[threadIdx.x >> 6] + ((threadIdx.x & 63u) >> 3) * 132u;
+#pragma unroll
+                    for (uint32_t h = 0; h < 2; h++) {
+                        const float s = scale(i0 + h);
+                        float y[8];
+#pragma unroll
+                        for (uint32_t t = 0; t < 8; t++) y[t] = qv(8u * h + t) * s;
+                        *(f4v *)(rowbuf + 32u * (i0 + h) + 8u * qq) = f4v{y[0], y[1], y[2], y[3]};
+                        *(f4v *)(rowbuf + 32u * (i0 + h) + 8u * qq + 4) = f4v{y[4], y[5], y[6], y[7]};
+                    }
+                    lds_order();
+#pragma unroll
+                    for (uint32_t k = 0; k < 4; k++)
+                        __builtin_nontemporal_store(*(const f4v *)(rowbuf + 32u * k + 4u * j),
+                                                    (f4v *)(dst[u] + 32u * k + 4u * j));
+                    lds_order();
+                } else {
 #pragma unroll
                 for (uint32_t h = 0; h < 2; h++) {
                     const float s = scale(i0 + h);
@@ -650,6 +681,7 @@ __global__ __launch_bounds__(256) void k_gather_q8(const uint8_t *__restrict__ p
 #pragma unroll
                     for (uint32_t t = 0; t < 8; t++) y[t] = qv(8u * h + t) * s;
                     store_f8(dst[u] + 32u * (i0 + h) + 8u * qq, y);
+                }
                 }
             } else {
                 const uint32_t c0 = (16u * j) / PR, g0 = ((16u * j) % PR) / 2u;
