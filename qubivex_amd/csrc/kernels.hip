@@ -500,6 +500,44 @@ __global__ __launch_bounds__(256) void k_gather(const uint8_t *__restrict__ pool
         }
         return;
     }
+    if (DT == QVKV_F16 && OUT == QVKV_F32) {
+        // f16 -> f32: 4 values per thread (an 8-byte load, a 16-byte store), so
+        // consecutive lanes store consecutive 16-byte pieces and every store instruction
+        // covers whole output lines; 8 loads in flight per thread.
+        const uint32_t c4 = D >> 2;
+        const uint32_t per4 = G * 16u * c4;
+        constexpr int U = 8;
+        for (uint32_t b0 = 0; b0 < 2u * per4; b0 += 256u * U) {
+            u2v x[U];
+            float *dst[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                dst[u] = nullptr;
+                const uint32_t idx = b0 + u * 256u + threadIdx.x;
+                if (idx >= 2u * per4) continue;
+                const bool isv = idx >= per4;
+                uint32_t r = isv ? idx - per4 : idx;
+                const uint32_t e = (r % c4) * 4u;
+                r /= c4;
+                const uint32_t row = r & 15u, g = r >> 4, p = p0 + row;
+                if (p >= len) continue;
+                x[u] = __builtin_nontemporal_load(
+                    (const u2v *)(base + (isv ? geo.v_off : geo.k_off) +
+                                  (((uint64_t)g * B + r0 + row) * D + e) * 2u));
+                dst[u] = (float *)(isv ? out_v : out_k) + oat * (uint64_t)G * D +
+                         ((uint64_t)g * len + p) * D + e;
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                if (!dst[u]) continue;
+                const uint32_t w0 = x[u].x, w1 = x[u].y;
+                const h2 a = __builtin_bit_cast(h2, w0), b = __builtin_bit_cast(h2, w1);
+                __builtin_nontemporal_store(f4v{(float)a.x, (float)a.y, (float)b.x, (float)b.y},
+                                            (f4v *)dst[u]);
+            }
+        }
+        return;
+    }
     for (uint32_t idx = threadIdx.x; idx < 2u * per_kv; idx += 256u) {
         const bool isv = idx >= per_kv;
         uint32_t r = isv ? idx - per_kv : idx;
