@@ -599,7 +599,6 @@ void k_prefill_q8(QV_PREFILL_PARAMS) {
     constexpr int KS = D / 32;                 // QK k-steps = quantization groups
     constexpr int NDB = D / 16;                // PV d blocks
     constexpr int CPR = D / 8;                 // 8-value (16-byte f16) pieces per row
-    constexpr int NGW = D / 64;                // scale words per row (2 groups per word)
     __shared__ __attribute__((aligned(16))) Q8PrefillSlot<D> sb0, sb1;
 
     const uint32_t G = (uint32_t)geo.G, B = (uint32_t)geo.B;
