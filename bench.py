@@ -32,7 +32,7 @@ PEAK_F16_TFLOPS = 2500.0  # dense f16 MFMA, MI355X
 CONFIGS = {
     # layers, kv heads, head dim, q heads, sequences, context (int or (lo, hi)), dtype, outliers
     "cfg5": dict(layers=48, kv_heads=4, head_dim=128, q_heads=32, seqs=128, ctx=8192,
-                 dtype="f16", outliers=0.0,
+                 dtype="f16", outliers=0.0, qk_norm="per_head",
                  name="cfg5 (Qwen3-30B-A3B-like KV, 128 seqs x 8192)"),
     "cfg2": dict(layers=32, kv_heads=8, head_dim=128, q_heads=32, seqs=32, ctx=(256, 4096),
                  dtype="f16", outliers=0.0,
@@ -55,7 +55,7 @@ def parse():
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--legs", default="append,decode,gather,copy,prefill")
+    ap.add_argument("--legs", default="append,decode,gather,copy,prefill,prelude")
     return ap.parse_args()
 
 
@@ -306,6 +306,43 @@ def main():
             f"{p_ms:.3f} ms = {result['prefill_tok_s']:.0f} tok/s, {result['prefill_tflops']:.1f} TFLOP/s")
         del qp, op
 
+    if "prelude" in legs:
+        # The attention prelude over one layer's 512-token prefill chunk of every sequence:
+        # q/k/v rows in place (bias, QK RMSNorm per head for the Qwen3-like cfg5, else
+        # none; RoPE).  Bytes: q, k, v read and written, the RoPE rows read.
+        PT = S * 512
+        norm = cfg.get("qk_norm", "none")
+        xq = torch.randn((PT, H * D), generator=gen, device="cuda")
+        xk = torch.randn((PT, kv_out), generator=gen, device="cuda")
+        xv = torch.randn((PT, kv_out), generator=gen, device="cuda")
+        ang = torch.rand((PT, D // 2), generator=gen, device="cuda") * 6.283
+        rope = torch.cat([torch.cos(ang), torch.sin(ang)], dim=1).contiguous()
+        qb = torch.randn(H * D, generator=gen, device="cuda")
+        kb, vb = (torch.randn(kv_out, generator=gen, device="cuda") for _ in range(2))
+        wn = D if norm == "per_head" else None
+        qn = torch.rand(wn, generator=gen, device="cuda") + 0.5 if wn else None
+        kn = torch.rand(wn, generator=gen, device="cuda") + 0.5 if wn else None
+
+        def pre():
+            dev.prelude(L, H, xq, xk, xv, rope, norm=norm, q_bias=qb, k_bias=kb, v_bias=vb,
+                        q_norm=qn, k_norm=kn)
+        for _ in range(2):
+            pre()
+        torch.cuda.synchronize()
+        reps = 5
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            pre()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        r_ms = e0.elapsed_time(e1) / reps
+        r_bytes = PT * (H + 2 * G) * D * 4 * 2 + PT * D * 4
+        result.update(prelude_ms=r_ms, prelude_gbs=r_bytes / (r_ms / 1e3) / 1e9)
+        log(f"[bench] prelude {PT} tokens ({norm} QK norm): {r_ms:.3f} ms = "
+            f"{result['prelude_gbs']:.0f} GB/s")
+        del xq, xk, xv, rope
+
     if append_ms:
         a_ms = float(np.mean(append_ms))
         a_gbs = float(np.mean(append_bytes)) / (a_ms / 1e3) / 1e9
@@ -365,6 +402,7 @@ def main():
             "append": round(result.get("append_gbs", 0) / PEAK_HBM_GBS, 4),
             "gather": round(result.get("gather_gbs", 0) / PEAK_HBM_GBS, 4),
             "block_copy": round(result.get("copy_gbs", 0) / PEAK_HBM_GBS, 4),
+            "prelude": round(result.get("prelude_gbs", 0) / PEAK_HBM_GBS, 4),
         }
         # MFMA issue rate against the dense f16 peak (2.5 PFLOP/s): decode attention is
         # HBM-bound and uses the matrix cores only for the GQA group contraction.

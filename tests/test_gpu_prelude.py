@@ -29,17 +29,27 @@ CASES = [
     (16, 2, 64, "none", 5.0, True, 10.0),
     (8, 8, 96, "per_head", 2.0, False, 1.0),
     (4, 1, 200, "full", None, True, 1.0),
+    # the register kernel (d = 64/128/256 without a full-row norm): partial head batches
+    # (12 heads = 8 + 4 at d = 128), pairs across lanes (d = 64), 37 tokens (partial workgroup)
+    (64, 8, 256, "per_head", 4.0, True, 2.0),
+    (16, 4, 64, "per_head", None, True, 3.0),
+    (12, 3, 128, "none", None, True, 1.0),
+    (32, 4, 128, "per_head", 6.0, True, 5.0),
 ]
 
 
+@pytest.mark.parametrize("fast", [1, 0], ids=["default", "lds_kernel"])
 @pytest.mark.parametrize("heads,kvh,d,norm,clip,bias,scale", CASES)
-def test_prelude_bit_exact(hip, heads, kvh, d, norm, clip, bias, scale):
+def test_prelude_bit_exact(hip, monkeypatch, heads, kvh, d, norm, clip, bias, scale, fast):
     from qubivex_amd import KvLayout
 
-    print(f"prelude heads={heads} kvh={kvh} d={d} norm={norm} clip={clip} bias={bias}", flush=True)
+    # QVKV_PRELUDE_FAST=0 forces the LDS kernel, the form for every other shape
+    monkeypatch.setenv("QVKV_PRELUDE_FAST", str(fast))
+    print(f"prelude heads={heads} kvh={kvh} d={d} norm={norm} clip={clip} bias={bias} "
+          f"fast={fast}", flush=True)
     r = np.random.default_rng(heads * d + kvh)
     L = KvLayout("f16", kvh, d, 16)
-    s = 5
+    s = 37
     q = (r.standard_normal((s, heads * d)) * scale).astype(np.float32)
     k = (r.standard_normal((s, kvh * d)) * scale).astype(np.float32)
     v = (r.standard_normal((s, kvh * d)) * scale).astype(np.float32)
