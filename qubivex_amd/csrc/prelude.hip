@@ -116,8 +116,8 @@ __global__ __launch_bounds__(64) void k_prelude(float *__restrict__ q, float *__
     }
 }
 
-// Register form for d = 64, 128, 256 without a full-row norm: one wave per (token, q|k|v,
-// batch of HB = 1024/d heads), lane l holding elements 64j + l of each head (j < d/64) in
+// Register form for d = 64, 128, 256: one wave per (token, q|k|v, batch of HB = 1024/d
+// heads, or the whole row under a full-row norm), lane l holding elements 64j + l of each head (j < d/64) in
 // registers.  A head's sum of squares is then lane l's in-order fma over j followed by the
 // same 64-lane tree (lane_tree_x); the heads' totals are gathered one per lane so a single
 // vector rms_scale_of serves every head of the wave.  Every RoPE pair (i, i + d/2) lies in
@@ -125,12 +125,16 @@ __global__ __launch_bounds__(64) void k_prelude(float *__restrict__ q, float *__
 // Loads and stores are dword-coalesced 256-byte runs; no LDS, no barriers, 4 independent
 // waves per workgroup.  Measured against the LDS kernel at 65 536 tokens, 32 query heads:
 // d = 128 with per-head norms 2.66 -> 0.60 ms, without norms 1.86 -> 0.52 ms.
-template <int D>
+// FULL: one norm over each whole row (QkNorm::Full): the wave takes the whole q, k or v row
+// (up to 4096 values, 64 per lane), whose element order h*d + 64j + l is lane l's order
+// of the reference's reduction.
+template <int D, bool FULL>
 __global__ __launch_bounds__(256) void k_prelude_r(float *__restrict__ q, float *__restrict__ k,
                                                    float *__restrict__ v, uint32_t s,
                                                    uint32_t heads, uint32_t kvh, uint32_t uq,
                                                    uint32_t ukv, PreludeArgs a) {
-    constexpr uint32_t HB = 1024 / D;  // heads per wave (best of 512, 1024, 2048 values)
+    // heads per wave: 1024 values was the best of 512, 1024, 2048 without a full norm
+    constexpr uint32_t HB = (FULL ? 4096 : 1024) / D;
     constexpr uint32_t J = D >= 64 ? D / 64 : 1;
     const uint32_t per_tok = uq + 2 * ukv;
     const uint32_t u = blockIdx.x * 4u + (threadIdx.x >> 6);
@@ -163,7 +167,21 @@ __global__ __launch_bounds__(256) void k_prelude_r(float *__restrict__ q, float 
             }
     if (part != 2) {
         const float *w = part == 0 ? a.q_norm : a.k_norm;
-        if (a.norm == QVKV_NORM_PER_HEAD && w) {
+        if (FULL && w) {
+            float acc = 0.0f;
+#pragma unroll
+            for (uint32_t h = 0; h < HB; h++)
+                if (h < nh)
+#pragma unroll
+                    for (uint32_t j = 0; j < J; j++) acc = fmaf(z[h][j], z[h][j], acc);
+            const float rs = rms_scale_of(lane_tree_x(acc), (float)(nh * D), a.eps);
+#pragma unroll
+            for (uint32_t h = 0; h < HB; h++)
+                if (h < nh)
+#pragma unroll
+                    for (uint32_t j = 0; j < J; j++)
+                        z[h][j] = (z[h][j] * rs) * w[h * D + 64 * j + lane];
+        } else if (!FULL && a.norm == QVKV_NORM_PER_HEAD && w) {
             // head h's sum of squares to lane h; one rms_scale_of for all heads
             float tot = 0.0f;
 #pragma unroll
@@ -238,20 +256,27 @@ __global__ __launch_bounds__(256) void k_prelude_r(float *__restrict__ q, float 
 hipError_t launch_prelude(float *q, float *k, float *v, uint32_t s, uint32_t heads,
                           uint32_t kvh, uint32_t d, const PreludeArgs &a, hipStream_t st) {
     if (s == 0) return hipSuccess;
-    if ((d == 64 || d == 128 || d == 256) && a.norm != QVKV_NORM_FULL &&
+    const bool full = a.norm == QVKV_NORM_FULL;
+    if ((d == 64 || d == 128 || d == 256) && (!full || (heads * d <= 4096 && kvh * d <= 4096)) &&
         tune("QVKV_PRELUDE_FAST", 1) != 0) {
-        const uint32_t hb = 1024 / d;
+        const uint32_t hb = (full ? 4096 : 1024) / d;
         const uint32_t uq = (heads + hb - 1) / hb, ukv = (kvh + hb - 1) / hb;
         const uint64_t waves = (uint64_t)s * (uq + 2 * ukv);
         const uint64_t grid = (waves + 3) / 4;
         if (waves > 0xffffffffull || grid > 0x7fffffffull) return hipErrorInvalidValue;
+#define QV_PRE1(DD, FF)                                                                         \
+    hipLaunchKernelGGL((k_prelude_r<DD, FF>), dim3((unsigned)grid), dim3(256), 0, st, q, k, v,   \
+                       s, heads, kvh, uq, ukv, a)
 #define QV_PRE(DD)                                                                              \
-    hipLaunchKernelGGL(k_prelude_r<DD>, dim3((unsigned)grid), dim3(256), 0, st, q, k, v, s,      \
-                       heads, kvh, uq, ukv, a)
+    do {                                                                                        \
+        if (full) QV_PRE1(DD, true);                                                            \
+        else QV_PRE1(DD, false);                                                                \
+    } while (0)
         if (d == 64) QV_PRE(64);
         else if (d == 128) QV_PRE(128);
         else QV_PRE(256);
 #undef QV_PRE
+#undef QV_PRE1
         return hipGetLastError();
     }
     const uint64_t lds = (uint64_t)(heads > kvh ? heads : kvh) * d * 4;

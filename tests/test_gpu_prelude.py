@@ -35,6 +35,10 @@ CASES = [
     (16, 4, 64, "per_head", None, True, 3.0),
     (12, 3, 128, "none", None, True, 1.0),
     (32, 4, 128, "per_head", 6.0, True, 5.0),
+    # full-row norms in the register kernel (rows up to 4096 values) and past it (5120)
+    (16, 2, 256, "full", None, True, 2.0),
+    (64, 8, 64, "full", 3.0, False, 4.0),
+    (40, 8, 128, "full", None, True, 1.0),
 ]
 
 
