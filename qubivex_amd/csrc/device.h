@@ -482,6 +482,24 @@ __device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 
+// Probabilities x0, x1 as f16 high parts (round to nearest even, packed) and the f16
+// residuals x - hi: x - hi is exact in f32, so one rounding to f16 makes the residual,
+// as (_Float16)(x - (float)hi) does.  v_fma_mixlo/mixhi_f16 read hi straight from the
+// packed word (op_sel_hi: source 0 is f16; op_sel picks its half) instead of converting it
+// back to f32 first: 6 instructions per pair instead of 14.  The residual feeds an MFMA,
+// and a VALU write read by an MFMA needs 2 wait states, which the compiler's hazard
+// checks do not insert for inline asm: hence the s_nop.
+__device__ __forceinline__ void split_pair(float x0, float x1, uint32_t &hi, uint32_t &lo) {
+    hi = __builtin_bit_cast(uint32_t, h2{(_Float16)x0, (_Float16)x1});
+    uint32_t r;
+    asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixhi_f16 %0, %1, -1.0, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+        "s_nop 1"
+        : "=&v"(r)
+        : "v"(hi), "v"(x0), "v"(x1));
+    lo = r;
+}
+
 // ---------------------------------------------------------------------------------
 // Decode attention, generic form (any d that is a multiple of 8 up to 512, any group):
 // one wave per (item, query head); lanes take 64 positions at a time for the scores,

@@ -365,16 +365,15 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
     auto tile = [&](uint32_t tp0, auto kread, auto vread) {
         if (tp0 >= n_wave) return;
         // ---- scores: lane holds positions tp0 + 8 grp + (4h + i) of row `col`
-        f4 s[2];
+        // the two 16-position halves' accumulation chains interleaved (each keeps its order)
+        f4 s[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            s[h] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < KS; ks++) {
-                const h8 a = kread(h, ks);
-                s[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[ks], s[h], 0, 0, 0);
-                s[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[ks], s[h], 0, 0, 0);
-            }
+        for (int ks = 0; ks < KS; ks++) {
+            const h8 a0 = kread(0, ks), a1 = kread(1, ks);
+            s[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qh[ks], s[0], 0, 0, 0);
+            s[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qh[ks], s[1], 0, 0, 0);
+            s[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, ql[ks], s[0], 0, 0, 0);
+            s[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, ql[ks], s[1], 0, 0, 0);
         }
         float sc[8];
 #pragma unroll
@@ -413,13 +412,11 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
             psum += pr[e];
         }
         l += psum;
-        h8 ph, pl;
+        uint32_t phw[4], plw[4];  // high parts and exact residuals, one rounding each
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const _Float16 hi = (_Float16)pr[e];
-            ph[e] = hi;
-            pl[e] = (_Float16)fmaf(-1.0f, (float)hi, pr[e]);  // exact residual, one rounding
-        }
+        for (int k = 0; k < 4; k++) split_pair(pr[2 * k], pr[2 * k + 1], phw[k], plw[k]);
+        const h8 ph = __builtin_bit_cast(h8, u4v{phw[0], phw[1], phw[2], phw[3]});
+        const h8 pl = __builtin_bit_cast(h8, u4v{plw[0], plw[1], plw[2], plw[3]});
 #pragma unroll
         for (int j = 0; j < NDB; j++) {
             const h8 b = vread(j);
@@ -483,8 +480,12 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
                 if (full) {
                     // the LDS address is the wave's first chunk; lanes follow at 16 bytes.
                     // Cached loads (aux 0): the n_cb workgroups of a (segment, KV head) read
-                    // the same tiles and share them through the XCD's L2.
-                    __builtin_amdgcn_global_load_lds(((pos & 16u) ? b1 : b0) + off,
+                    // the same tiles and share them through the XCD's L2.  A wave's 64
+                    // chunks are 4 (d = 128) or 8 (d = 64) consecutive LDS rows, which lie in
+                    // one 16-position half of the tile, so the block base is chosen on the
+                    // scalar unit and the load takes a scalar base plus a 32-bit lane offset.
+                    const bool upper = __builtin_amdgcn_readfirstlane(pos & 16u) != 0;
+                    __builtin_amdgcn_global_load_lds((upper ? b1 : b0) + off,
                                                      dst + (cc - lane) * 8, 16, 0, 0);
                 } else {
                     const u4v x = fetch(b0, b1, valid, pos, off);
