@@ -58,8 +58,21 @@ def build(verbose: bool = False, jobs: int = 4) -> str:
         raise RuntimeError(f"build failed: {failed[0]}")
     tmp = LIB + ".tmp"
     _run(["hipcc", f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp], verbose)
+    _check_stubs(tmp)
     os.replace(tmp, LIB)
     return LIB
+
+
+def _check_stubs(path: str) -> None:
+    """Fails the build when a kernel's host launch stub is referenced but not defined: the
+    host pass of hipcc can drop one without a diagnostic, and the library would then fail
+    only when loaded."""
+    out = subprocess.run(["nm", "-D", "--undefined-only", path], check=True,
+                         capture_output=True, text=True).stdout
+    missing = [ln.split()[-1] for ln in out.splitlines() if "__device_stub__" in ln]
+    if missing:
+        os.remove(path)
+        raise RuntimeError(f"build failed: undefined kernel launch stubs {missing}")
 
 
 if __name__ == "__main__":

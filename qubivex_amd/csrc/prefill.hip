@@ -365,8 +365,11 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
     auto tile = [&](uint32_t tp0, auto kread, auto vread) {
         if (tp0 >= n_wave) return;
         // ---- scores: lane holds positions tp0 + 8 grp + (4h + i) of row `col`
-        // the two 16-position halves' accumulation chains interleaved (each keeps its order)
-        f4 s[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
+        // the two 16-position halves' accumulation chains interleaved (each keeps its order).
+        // The accumulators start at -m0 (m0: the row's max so far, 0 before any), so the
+        // scores come out shifted for exp2 without a subtraction per score.
+        const float m0 = m == -INFINITY ? 0.0f : m;
+        f4 s[2] = {f4{-m0, -m0, -m0, -m0}, f4{-m0, -m0, -m0, -m0}};
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
             const h8 a0 = kread(0, ks), a1 = kread(1, ks);
@@ -386,7 +389,7 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
         float tmax = sc[0];
 #pragma unroll
         for (int e = 1; e < 8; e++) tmax = fmaxf(tmax, sc[e]);
-        tmax = max_xor16_32(tmax);
+        tmax = max_xor16_32(tmax) + m0;
         // Lazy rescale: the reference max m moves only when a row's scores exceed it by
         // more than 2^8, so probabilities stay <= 256 (exact under the f16 high +
         // residual split) and the O rescale runs on few tiles.
@@ -402,13 +405,15 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) acc[j][i] *= ar[i];
             m = mnew;
+            const float shift = (m == -INFINITY ? 0.0f : m) - m0;
+#pragma unroll
+            for (int e = 0; e < 8; e++) sc[e] -= shift;
         }
-        const float msafe = m == -INFINITY ? 0.0f : m;
         float pr[8];
         float psum = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            pr[e] = __builtin_amdgcn_exp2f(sc[e] - msafe);
+            pr[e] = __builtin_amdgcn_exp2f(sc[e]);
             psum += pr[e];
         }
         l += psum;
@@ -463,31 +468,54 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
         // pool offsets of the K and V parts of a block, as values (a per-lane choice
         // between two kernel-argument fields would otherwise load through a vector address)
         const uint32_t koff = (uint32_t)geo.k_off, voff = (uint32_t)geo.v_off;
-        auto issue = [&](uint32_t t, DmaSlot<D> &sl) {
-            const uint32_t p0 = t * TP;
-            const uint8_t *b0 = half_base(p0), *b1 = half_base(p0 + 16u);
-            const uint32_t valid = n_wg - p0 < (uint32_t)TP ? n_wg - p0 : (uint32_t)TP;
-            const bool full = valid == (uint32_t)TP && b0 != nullptr && b1 != nullptr;  // uniform
+        // Per chunk u of this thread, fixed for every tile: its pool offset inside a block,
+        // and for its wave (a wave's 64 chunks are 4 (d = 128) or 8 (d = 64) consecutive LDS
+        // rows of one K or V tile, inside one 16-position half) the half, whether it is V,
+        // and the LDS offset of the wave's first chunk.  The load then takes a scalar block
+        // base plus a 32-bit lane offset.
+        // (in a lambda: the host pass of a kernel body must not see the device builtins)
+        uint32_t c_off[CPT], c_lds[CPT], c_up[CPT], c_v[CPT];
+        [&]() {
 #pragma unroll
             for (int u = 0; u < CPT; u++) {
                 const uint32_t c = threadIdx.x + 256u * u;
                 uint32_t pos, piece;
                 bool isv;
                 chunk(c, pos, piece, isv);
-                const uint32_t off = (isv ? voff : koff) + ((pos & 15u) * D + piece * 8) * 2u;
-                _Float16 *dst = isv ? sl.v : sl.k;
+                c_off[u] = (isv ? voff : koff) + ((pos & 15u) * D + piece * 8) * 2u;
                 const uint32_t cc = isv ? c - CH : c;
-                if (full) {
-                    // the LDS address is the wave's first chunk; lanes follow at 16 bytes.
-                    // Cached loads (aux 0): the n_cb workgroups of a (segment, KV head) read
-                    // the same tiles and share them through the XCD's L2.  A wave's 64
-                    // chunks are 4 (d = 128) or 8 (d = 64) consecutive LDS rows, which lie in
-                    // one 16-position half of the tile, so the block base is chosen on the
-                    // scalar unit and the load takes a scalar base plus a 32-bit lane offset.
-                    const bool upper = __builtin_amdgcn_readfirstlane(pos & 16u) != 0;
-                    __builtin_amdgcn_global_load_lds((upper ? b1 : b0) + off,
-                                                     dst + (cc - lane) * 8, 16, 0, 0);
-                } else {
+                c_lds[u] = __builtin_amdgcn_readfirstlane((cc - lane) * 8);
+                c_up[u] = __builtin_amdgcn_readfirstlane(pos & 16u);
+                c_v[u] = __builtin_amdgcn_readfirstlane(isv ? 1u : 0u);
+            }
+        }();
+        auto issue = [&](uint32_t t, DmaSlot<D> &sl) {
+            const uint32_t p0 = t * TP;
+            const uint8_t *b0 = half_base(p0), *b1 = half_base(p0 + 16u);
+            const uint32_t valid = n_wg - p0 < (uint32_t)TP ? n_wg - p0 : (uint32_t)TP;
+            const bool full = valid == (uint32_t)TP && b0 != nullptr && b1 != nullptr;  // uniform
+            if (full) {
+                // Cached loads (aux 0): the n_cb workgroups of a (segment, KV head) read the
+                // same tiles and share them through the XCD's L2.
+#pragma unroll
+                for (int u = 0; u < CPT; u++) {
+                    // (operands named first: with them inline, hipcc's host pass dropped the
+                    // kernel's launch stub without a diagnostic)
+                    const uint8_t *src = (c_up[u] ? b1 : b0) + c_off[u];
+                    _Float16 *lds_dst = (c_v[u] ? sl.v : sl.k) + c_lds[u];
+                    __builtin_amdgcn_global_load_lds(src, lds_dst, 16, 0, 0);
+                }
+            } else {
+                // past n_wg or a bad block: through registers, zeros where invalid
+#pragma unroll
+                for (int u = 0; u < CPT; u++) {
+                    const uint32_t c = threadIdx.x + 256u * u;
+                    uint32_t pos, piece;
+                    bool isv;
+                    chunk(c, pos, piece, isv);
+                    const uint32_t off = (isv ? voff : koff) + ((pos & 15u) * D + piece * 8) * 2u;
+                    _Float16 *dst = isv ? sl.v : sl.k;
+                    const uint32_t cc = isv ? c - CH : c;
                     const u4v x = fetch(b0, b1, valid, pos, off);
                     *(u4v *)(dst + cc * 8) = x;
                 }
