@@ -410,12 +410,11 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
             for (int e = 0; e < 8; e++) sc[e] -= shift;
         }
         float pr[8];
-        float psum = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            pr[e] = __builtin_amdgcn_exp2f(sc[e]);
-            psum += pr[e];
-        }
+        for (int e = 0; e < 8; e++) pr[e] = __builtin_amdgcn_exp2f(sc[e]);
+        float psum = pr[0];  // (0 + p0 = p0: the same sum without the first add)
+#pragma unroll
+        for (int e = 1; e < 8; e++) psum += pr[e];
         l += psum;
         uint32_t phw[4], plw[4];  // high parts and exact residuals, one rounding each
 #pragma unroll
@@ -844,10 +843,13 @@ void k_prefill_q8(QV_PREFILL_PARAMS) {
         u4v ksw[4];
 #pragma unroll
         for (int x = 0; x < 4; x++) ksw[x] = *(const u4v *)(sl.ks + 16u * grp + 4u * x);
+        // scores accumulate from -m0 (m0: the row's max so far, 0 before any), so they come
+        // out shifted for exp2 without a subtraction per score
+        const float m0 = m == -INFINITY ? 0.0f : m;
         f4 s[2];
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            s[h] = f4{0.f, 0.f, 0.f, 0.f};
+            s[h] = f4{-m0, -m0, -m0, -m0};
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) {
                 const h8 a = kread(sl, h, ks);
@@ -874,7 +876,7 @@ void k_prefill_q8(QV_PREFILL_PARAMS) {
         float tmax = sc[0];
 #pragma unroll
         for (int e = 1; e < 8; e++) tmax = fmaxf(tmax, sc[e]);
-        tmax = max_xor16_32(tmax);
+        tmax = max_xor16_32(tmax) + m0;
         if (__any(tmax > m + 8.0f)) {
             const float mnew = fmaxf(m, tmax);
             const float alpha = __builtin_amdgcn_exp2f(m - (mnew == -INFINITY ? 0.0f : mnew));
@@ -887,23 +889,22 @@ void k_prefill_q8(QV_PREFILL_PARAMS) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) acc[j][i] *= ar[i];
             m = mnew;
+            const float shift = (m == -INFINITY ? 0.0f : m) - m0;
+#pragma unroll
+            for (int e = 0; e < 8; e++) sc[e] -= shift;
         }
-        const float msafe = m == -INFINITY ? 0.0f : m;
         float pr[8];
-        float psum = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            pr[e] = __builtin_amdgcn_exp2f(sc[e] - msafe);
-            psum += pr[e];
-        }
+        for (int e = 0; e < 8; e++) pr[e] = __builtin_amdgcn_exp2f(sc[e]);
+        float psum = pr[0];
+#pragma unroll
+        for (int e = 1; e < 8; e++) psum += pr[e];
         l += psum;
-        h8 ph, pl;
+        uint32_t phw[4], plw[4];  // high parts and exact residuals, one rounding each
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const _Float16 hi = (_Float16)pr[e];
-            ph[e] = hi;
-            pl[e] = (_Float16)fmaf(-1.0f, (float)hi, pr[e]);
-        }
+        for (int k = 0; k < 4; k++) split_pair(pr[2 * k], pr[2 * k + 1], phw[k], plw[k]);
+        const h8 ph = __builtin_bit_cast(h8, u4v{phw[0], phw[1], phw[2], phw[3]});
+        const h8 pl = __builtin_bit_cast(h8, u4v{plw[0], plw[1], plw[2], plw[3]});
 #pragma unroll
         for (int j = 0; j < NDB; j++) {
             const h8 bh = vread(sl.vh, j), bl = vread(sl.vl, j);
