@@ -135,3 +135,27 @@ int main(void) {
     assert r.returncode == 0, r.stderr
     r = subprocess.run([str(exe)], capture_output=True, text=True)
     assert r.returncode == 0 and r.stdout.strip() == "ok", (r.returncode, r.stdout, r.stderr)
+
+
+def test_build_rejects_a_library_with_an_undefined_launch_stub(tmp_path):
+    """The build's guard against hipcc's host pass dropping a kernel's launch stub: a shared
+    library that references an undefined __device_stub__ symbol is refused (and removed),
+    one without is accepted."""
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("qvkv_build",
+                                                  os.path.join(ROOT, "qubivex_amd", "build.py"))
+    build = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(build)
+    bad_c = tmp_path / "bad.c"
+    bad_c.write_text("extern void _ZN4qvkv22__device_stub__k_demoEv(void);\n"
+                     "void launch(void) { _ZN4qvkv22__device_stub__k_demoEv(); }\n")
+    good_c = tmp_path / "good.c"
+    good_c.write_text("int launch(void) { return 1; }\n")
+    for src in (bad_c, good_c):
+        subprocess.run(["gcc", "-shared", "-fPIC", str(src), "-o", str(src.with_suffix(".so"))],
+                       check=True)
+    build._check_stubs(str(good_c.with_suffix(".so")))
+    with pytest.raises(RuntimeError, match="undefined kernel launch stubs"):
+        build._check_stubs(str(bad_c.with_suffix(".so")))
+    assert not bad_c.with_suffix(".so").exists()
