@@ -421,11 +421,14 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
         for (int k = 0; k < 4; k++) split_pair(pr[2 * k], pr[2 * k + 1], phw[k], plw[k]);
         const h8 ph = __builtin_bit_cast(h8, u4v{phw[0], phw[1], phw[2], phw[3]});
         const h8 pl = __builtin_bit_cast(h8, u4v{plw[0], plw[1], plw[2], plw[3]});
+        // two d blocks at a time, so each accumulator's two MFMAs are not back to back
 #pragma unroll
-        for (int j = 0; j < NDB; j++) {
-            const h8 b = vread(j);
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, b, acc[j], 0, 0, 0);
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, b, acc[j], 0, 0, 0);
+        for (int j = 0; j < NDB; j += 2) {
+            const h8 b0 = vread(j), b1 = vread(j + 1);
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, b0, acc[j], 0, 0, 0);
+            acc[j + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, b1, acc[j + 1], 0, 0, 0);
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, b0, acc[j], 0, 0, 0);
+            acc[j + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, b1, acc[j + 1], 0, 0, 0);
         }
     };
 
