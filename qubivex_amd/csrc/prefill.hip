@@ -389,12 +389,13 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
         float tmax = sc[0];
 #pragma unroll
         for (int e = 1; e < 8; e++) tmax = fmaxf(tmax, sc[e]);
-        tmax = max_xor16_32(tmax) + m0;
         // Lazy rescale: the reference max m moves only when a row's scores exceed it by
         // more than 2^8, so probabilities stay <= 256 (exact under the f16 high +
-        // residual split) and the O rescale runs on few tiles.
-        if (__any(tmax > m + 8.0f)) {
-            const float mnew = fmaxf(m, tmax);
+        // residual split) and the O rescale runs on few tiles.  The test needs no row
+        // max: adding m0 and rounding are monotonic, so some lane's own max exceeds
+        // m + 8 exactly when its row's max does; the row max is taken on that rare path.
+        if (__any(tmax + m0 > m + 8.0f)) {
+            const float mnew = fmaxf(m, max_xor16_32(tmax) + m0);
             const float alpha = __builtin_amdgcn_exp2f(m - (mnew == -INFINITY ? 0.0f : mnew));
             l *= alpha;
             float ar[4];
@@ -879,9 +880,9 @@ void k_prefill_q8(QV_PREFILL_PARAMS) {
         float tmax = sc[0];
 #pragma unroll
         for (int e = 1; e < 8; e++) tmax = fmaxf(tmax, sc[e]);
-        tmax = max_xor16_32(tmax) + m0;
-        if (__any(tmax > m + 8.0f)) {
-            const float mnew = fmaxf(m, tmax);
+        // (the row max only on the rare rescale path, as in k_prefill_f16)
+        if (__any(tmax + m0 > m + 8.0f)) {
+            const float mnew = fmaxf(m, max_xor16_32(tmax) + m0);
             const float alpha = __builtin_amdgcn_exp2f(m - (mnew == -INFINITY ? 0.0f : mnew));
             l *= alpha;
             float ar[4];
