@@ -128,13 +128,13 @@ __global__ __launch_bounds__(64) void k_prelude(float *__restrict__ q, float *__
 // FULL: one norm over each whole row (QkNorm::Full): the wave takes the whole q, k or v row
 // (up to 4096 values, 64 per lane), whose element order h*d + 64j + l is lane l's order
 // of the reference's reduction.
-template <int D, bool FULL>
+template <int D, bool FULL, int VPW = 1024>
 __global__ __launch_bounds__(256) void k_prelude_r(float *__restrict__ q, float *__restrict__ k,
                                                    float *__restrict__ v, uint32_t s,
                                                    uint32_t heads, uint32_t kvh, uint32_t uq,
                                                    uint32_t ukv, PreludeArgs a) {
     // heads per wave: 1024 values was the best of 512, 1024, 2048 without a full norm
-    constexpr uint32_t HB = (FULL ? 4096 : 1024) / D;
+    constexpr uint32_t HB = (FULL ? 4096 : VPW) / D;
     constexpr uint32_t J = D >= 64 ? D / 64 : 1;
     const uint32_t per_tok = uq + 2 * ukv;
     const uint32_t u = blockIdx.x * 4u + (threadIdx.x >> 6);
@@ -259,7 +259,11 @@ hipError_t launch_prelude(float *q, float *k, float *v, uint32_t s, uint32_t hea
     const bool full = a.norm == QVKV_NORM_FULL;
     if ((d == 64 || d == 128 || d == 256) && (!full || (heads * d <= 4096 && kvh * d <= 4096)) &&
         tune("QVKV_PRELUDE_FAST", 1) != 0) {
-        const uint32_t hb = (full ? 4096 : 1024) / d;
+        // per-head norms at d = 128: 2048 values per wave (one vector rms serves 16 heads;
+        // +2 % at 32 query heads; 5 % slower at d = 256, equal at d = 64)
+        const bool wide = !full && a.norm == QVKV_NORM_PER_HEAD && d == 128 &&
+                          tune("QVKV_PRELUDE_WIDE", 1) != 0;
+        const uint32_t hb = (full ? 4096u : wide ? 2048u : 1024u) / d;
         const uint32_t uq = (heads + hb - 1) / hb, ukv = (kvh + hb - 1) / hb;
         const uint64_t waves = (uint64_t)s * (uq + 2 * ukv);
         const uint64_t grid = (waves + 3) / 4;
@@ -267,9 +271,13 @@ hipError_t launch_prelude(float *q, float *k, float *v, uint32_t s, uint32_t hea
 #define QV_PRE1(DD, FF)                                                                         \
     hipLaunchKernelGGL((k_prelude_r<DD, FF>), dim3((unsigned)grid), dim3(256), 0, st, q, k, v,   \
                        s, heads, kvh, uq, ukv, a)
+#define QV_PRE1W(DD)                                                                            \
+    hipLaunchKernelGGL((k_prelude_r<DD, false, (DD == 128 ? 2048 : 1024)>), dim3((unsigned)grid), \
+                       dim3(256), 0, st, q, k, v, s, heads, kvh, uq, ukv, a)
 #define QV_PRE(DD)                                                                              \
     do {                                                                                        \
         if (full) QV_PRE1(DD, true);                                                            \
+        else if (wide && DD == 128) QV_PRE1W(DD);                                               \
         else QV_PRE1(DD, false);                                                                \
     } while (0)
         if (d == 64) QV_PRE(64);
@@ -277,6 +285,7 @@ hipError_t launch_prelude(float *q, float *k, float *v, uint32_t s, uint32_t hea
         else QV_PRE(256);
 #undef QV_PRE
 #undef QV_PRE1
+#undef QV_PRE1W
         return hipGetLastError();
     }
     const uint64_t lds = (uint64_t)(heads > kvh ? heads : kvh) * d * 4;
