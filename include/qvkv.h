@@ -13,11 +13,18 @@
  *  - Handles are opaque.  Host pointers are borrowed for the duration of the call.
  *  - Functions without the `_async` suffix take HOST memory, run on the device's own
  *    stream and complete before they return (the trait's "completes before return"
- *    semantics, crates/qubivex-backend-vulkan/src/lib.rs:212-225).
+ *    semantics, crates/qubivex-backend-vulkan/src/lib.rs:212-225).  They do not wait for
+ *    work a caller queued on other streams: finish it first (qvkv_check on that stream).
+ *    The pool manager's copies are the exception: they take the caller's stream and run
+ *    after the work queued there (qvkv_pool_plan_append).
  *  - `_async` functions take DEVICE pointers and enqueue on `stream`, a hipStream_t used
- *    as given (0 is HIP's null stream; qvkv_stream() returns the device's own).  Index errors found by a kernel (a block id
- *    past the pool, a table too short) are latched on the device and reported by the
- *    next qvkv_check().  Kernels never touch memory outside the pool for such input.
+ *    as given (0 is HIP's null stream; qvkv_stream() returns the device's own).  Index
+ *    errors found by a kernel (a block id past the pool, a table too short) are latched in
+ *    a flag of that stream and reported by the next qvkv_check() of the same stream.
+ *    Kernels never touch memory outside the pool for such input.
+ *  - Threads: any thread may call (the trait is Send + Sync).  The library keeps an error
+ *    flag and an attention workspace per stream, so callers on different streams never
+ *    see each other's errors or overwrite each other's partial results.
  *  - A pool position is `slot = block * layout.block + offset` (the reference's
  *    `sync_to`, crates/qubivex-compute/src/discrete.rs:301-304).  Item t of a batch is
  *    one (sequence, layer) pair: its blocks are blocks[table_at[t] ..], in position order
@@ -64,14 +71,23 @@ typedef struct qvkv_usage_t {
     uint64_t capacity, used, peak, refused;
 } qvkv_usage_t;
 
-/* Copies so far: TransferStats (crates/qubivex-compute/src/discrete.rs:376-427). */
+/* Copies so far: TransferStats (crates/qubivex-compute/src/discrete.rs:376-427).
+ * timed / gpu_ns: the synchronous calls whose GPU time was measured and that time summed
+ * (TransferStats::timed, gpu_ns); stream_waits: pool copies that waited for a caller's
+ * stream. */
 typedef struct qvkv_transfers_t {
     uint64_t uploads, upload_bytes, downloads, download_bytes, submissions, wait_ns;
+    uint64_t timed, gpu_ns, stream_waits;
 } qvkv_transfers_t;
 
 /* Detail of the calling thread's last failure (ComputeError's Display). Returns the
  * status of that failure. */
 int qvkv_last_error(char *buf, size_t len);
+
+/* ComputeError::OutOfDeviceMemory's fields (crates/qubivex-compute/src/lib.rs:64-75) for
+ * the calling thread's last failure when it was QVKV_E_OOM: bytes requested, in use and
+ * the capacity (for a dry KV pool: the pool's blocks, in bytes).  Zeros otherwise. */
+int qvkv_last_oom(uint64_t *requested, uint64_t *used, uint64_t *capacity);
 
 /* ---- device and memory ---- */
 
@@ -86,6 +102,13 @@ int qvkv_usage(const qvkv_dev *dev, qvkv_usage_t *out);
 int qvkv_transfers(const qvkv_dev *dev, qvkv_transfers_t *out);
 /* The device's own stream (a hipStream_t). */
 void *qvkv_stream(const qvkv_dev *dev);
+/* GPU time of the last synchronous (host-memory) call on this device, in nanoseconds,
+ * from events around its kernels (TransferStats::gpu_ns per submission,
+ * discrete.rs:398-402). */
+int qvkv_timing(const qvkv_dev *dev, uint64_t *gpu_ns);
+/* DiscreteDevice::max_arena (discrete.rs:525-529): the largest buffer one call can address
+ * as a whole.  Kernels address pools with 64-bit offsets, so this is the device memory. */
+int qvkv_max_arena(const qvkv_dev *dev, uint64_t *out);
 
 /* DiscreteDevice::alloc (discrete.rs:500-508): `len` bytes, contents unspecified. */
 int qvkv_alloc(qvkv_dev *dev, size_t len, qvkv_buf **out);
@@ -97,11 +120,11 @@ size_t qvkv_buf_len(const qvkv_buf *buf);
 int qvkv_write(qvkv_dev *dev, qvkv_buf *buf, size_t offset, const void *host, size_t len);
 /* Device bytes back to the host (the readback of k_new/v_new in the reference). */
 int qvkv_read(qvkv_dev *dev, const qvkv_buf *buf, size_t offset, void *host, size_t len);
-/* Waits for `stream` (as given: 0 is the null stream) and reports any index error a
- * kernel latched since the last check (QVKV_E_SHAPE), or the q8_0 prefill's range report
- * alone (QVKV_E_UNSUPPORTED), clearing it.  The latch is one per device: with kernels in
- * flight on several streams, a check reports what any of them latched, and the
- * synchronous entry points check it too. */
+/* Waits for `stream` (as given: 0 is the null stream) and reports any index error its
+ * kernels latched since the last check of that stream (QVKV_E_SHAPE), or the q8_0
+ * prefill's range report alone (QVKV_E_UNSUPPORTED).  The flag is taken by an atomic
+ * exchange on the device, ordered after the stream's kernels, so a bit latched meanwhile
+ * is kept for the next check.  Other streams' flags are not read. */
 int qvkv_check(qvkv_dev *dev, void *stream);
 
 /* ---- layout ---- */
@@ -303,13 +326,18 @@ int qvkv_seq_touch(qvkv_pool *pool, uint32_t seq);
 
 /* Plans writes of `count[i]` new positions for seqs[i] on `layer` (the positions
  * len..len+count-1): grows each table from the free list, and copies-on-write a shared
- * block that a write lands in (the COW pairs are copied on the device before this
- * returns).  slots_out receives sum(count) pool positions, seq-major.  Returns
- * QVKV_E_OOM with nothing changed for the failing sequence (`pool.full` counts it;
- * discrete.rs:882-891) when the free list runs dry.  attention_plan's growth step
- * (discrete.rs:988-994). */
+ * block that a write lands in.  slots_out receives sum(count) pool positions, seq-major.
+ * Returns QVKV_E_OOM with nothing changed (`pool.full` counts it; discrete.rs:882-891)
+ * when the free list runs dry.  attention_plan's growth step (discrete.rs:988-994).
+ *
+ * Ordering of the copies (here, in qvkv_pool_plan_attention and in qvkv_pool_compact):
+ * a copy runs after all work queued on `stream` (a hipStream_t, 0 the null stream) when
+ * the call is made, and has completed when the call returns.  So appends that filled the
+ * shared blocks must have been queued on `stream`, or finished, before the call; the
+ * caller's writes into the copies may then go on any stream.  Host-only pools ignore
+ * `stream`. */
 int qvkv_pool_plan_append(qvkv_pool *pool, const uint32_t *seqs, const uint32_t *count,
-                          uint32_t n_seqs, uint32_t layer, uint32_t *slots_out);
+                          uint32_t n_seqs, uint32_t layer, uint32_t *slots_out, void *stream);
 /* The attention plan of one decode pass on `layer` with a host-authoritative cache:
  * attention_plan (crates/qubivex-runtime/src/discrete.rs:951-1009).  For each seqs[i] with
  * the host's newest position pos[i] and cache epoch epochs[i]: a sequence whose epoch
@@ -321,13 +349,15 @@ int qvkv_pool_plan_append(qvkv_pool *pool, const uint32_t *seqs, const uint32_t 
  * AttnPlan's blocks / table_at / pos (pos is the input).  The plan marks the layer synced
  * to pos+1 (a failed pass is repaired by the min above on the next plan).  A dry free list
  * returns QVKV_E_OOM and counts `full`; blocks taken before it stay with their sequence, as
- * in the reference.  blocks_cap / sync_cap bound the outputs. */
+ * in the reference.  blocks_cap / sync_cap bound the outputs.  Copies are ordered after
+ * `stream` as in qvkv_pool_plan_append. */
 int qvkv_pool_plan_attention(qvkv_pool *pool, const uint32_t *seqs, const uint32_t *pos,
                              const uint64_t *epochs, uint32_t n_seqs, uint32_t layer,
                              uint32_t *blocks_out, uint64_t blocks_cap, uint64_t *n_table_out,
                              uint32_t *table_at_out, uint32_t *new_slot_out,
                              uint32_t *sync_to_out, uint32_t *sync_item_out,
-                             uint32_t *sync_pos_out, uint64_t sync_cap, uint64_t *n_sync_out);
+                             uint32_t *sync_pos_out, uint64_t sync_cap, uint64_t *n_sync_out,
+                             void *stream);
 
 /* Flattened block tables of seqs[i] on `layer` (AttnPlan.blocks/table_at/pos,
  * discrete.rs:995-997).  blocks_cap bounds blocks_out; *n_table_out receives the
@@ -343,9 +373,9 @@ int qvkv_pool_evict_lru(qvkv_pool *pool, uint64_t target_blocks, uint32_t *relea
                         uint32_t cap, uint32_t *n_released);
 /* Moves every live block into the ids 0..live-1 in the order of a permutation drawn
  * from `seed` (seed 0: ascending by current id), rewriting every table and the free
- * list, with cycle-safe batches of the block-copy kernel.  *moved receives the blocks
- * moved. */
-int qvkv_pool_compact(qvkv_pool *pool, uint64_t seed, uint64_t *moved);
+ * list, with cycle-safe batches of the block-copy kernel, ordered after `stream` as in
+ * qvkv_pool_plan_append.  *moved receives the blocks moved. */
+int qvkv_pool_compact(qvkv_pool *pool, uint64_t seed, uint64_t *moved, void *stream);
 /* Reference count of one block (0 = free). */
 int qvkv_pool_refcount(const qvkv_pool *pool, uint32_t block, uint32_t *out);
 

@@ -28,7 +28,10 @@ class UnsupportedError(ComputeError):
 
 
 class OutOfDeviceMemory(ComputeError):
+    """ComputeError::OutOfDeviceMemory with its fields: bytes requested, in use, capacity."""
+
     code = E_OOM
+    requested = used = capacity = 0
 
 
 class DeviceError(ComputeError):
@@ -49,7 +52,8 @@ class Usage(ctypes.Structure):
 
 class Transfers(ctypes.Structure):
     _fields_ = [(n, ctypes.c_uint64) for n in ("uploads", "upload_bytes", "downloads",
-                                                "download_bytes", "submissions", "wait_ns")]
+                                                "download_bytes", "submissions", "wait_ns",
+                                                "timed", "gpu_ns", "stream_waits")]
 
 
 class PoolStats(ctypes.Structure):
@@ -91,12 +95,15 @@ _LP = _P(Layout)
 # name: (restype, argtypes)
 SIGNATURES = {
     "qvkv_last_error": (_i32, [ctypes.c_char_p, _sz]),
+    "qvkv_last_oom": (_i32, [_P(_u64), _P(_u64), _P(_u64)]),
     "qvkv_open": (_i32, [_i32, _P(_vp)]),
     "qvkv_close": (None, [_vp]),
     "qvkv_describe": (_i32, [_vp, ctypes.c_char_p, _sz]),
     "qvkv_usage": (_i32, [_vp, _P(Usage)]),
     "qvkv_transfers": (_i32, [_vp, _P(Transfers)]),
     "qvkv_stream": (_vp, [_vp]),
+    "qvkv_timing": (_i32, [_vp, _P(_u64)]),
+    "qvkv_max_arena": (_i32, [_vp, _P(_u64)]),
     "qvkv_alloc": (_i32, [_vp, _sz, _P(_vp)]),
     "qvkv_free": (None, [_vp]),
     "qvkv_buf_ptr": (_vp, [_vp]),
@@ -133,12 +140,12 @@ SIGNATURES = {
     "qvkv_seq_fork": (_i32, [_vp, _u32, _u32, _P(_u32)]),
     "qvkv_seq_len": (_i32, [_vp, _u32, _u32, _P(_u32)]),
     "qvkv_seq_touch": (_i32, [_vp, _u32]),
-    "qvkv_pool_plan_append": (_i32, [_vp, _vp, _vp, _u32, _u32, _vp]),
+    "qvkv_pool_plan_append": (_i32, [_vp, _vp, _vp, _u32, _u32, _vp, _vp]),
     "qvkv_pool_tables": (_i32, [_vp, _vp, _u32, _u32, _vp, _u64, _P(_u64), _vp, _vp]),
     "qvkv_pool_plan_attention": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _vp, _u64, _P(_u64), _vp,
-                                        _vp, _vp, _vp, _vp, _u64, _P(_u64)]),
+                                        _vp, _vp, _vp, _vp, _u64, _P(_u64), _vp]),
     "qvkv_pool_evict_lru": (_i32, [_vp, _u64, _vp, _u32, _P(_u32)]),
-    "qvkv_pool_compact": (_i32, [_vp, _u64, _P(_u64)]),
+    "qvkv_pool_compact": (_i32, [_vp, _u64, _P(_u64), _vp]),
     "qvkv_pool_refcount": (_i32, [_vp, _u32, _P(_u32)]),
     "qvkv_prefix_create": (_i32, [_u64, _P(_vp)]),
     "qvkv_prefix_destroy": (None, [_vp]),
@@ -166,5 +173,10 @@ def check(rc):
     """Raises the ComputeError subclass for a non-zero status."""
     if rc != OK:
         _, msg = last_error()
-        raise _BY_CODE.get(rc, ComputeError)(msg)
+        exc = _BY_CODE.get(rc, ComputeError)(msg)
+        if rc == E_OOM:
+            r, u, c = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+            lib.qvkv_last_oom(ctypes.byref(r), ctypes.byref(u), ctypes.byref(c))
+            exc.requested, exc.used, exc.capacity = r.value, u.value, c.value
+        raise exc
     return rc

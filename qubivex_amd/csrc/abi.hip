@@ -21,6 +21,7 @@ namespace {
 
 thread_local std::string g_err;
 thread_local int g_err_code = QVKV_OK;
+thread_local qvkv::OomDetail g_oom;
 
 int fail(int code, const char *fmt, ...) {
     char buf[512];
@@ -30,6 +31,7 @@ int fail(int code, const char *fmt, ...) {
     va_end(ap);
     g_err = buf;
     g_err_code = code;
+    if (code != QVKV_E_OOM) g_oom = qvkv::OomDetail{};
     return code;
 }
 
@@ -43,8 +45,15 @@ int qvkv::set_error(int code, const char *fmt, ...) {
     va_end(ap);
     g_err = buf;
     g_err_code = code;
+    if (code != QVKV_E_OOM) g_oom = qvkv::OomDetail{};
     return code;
 }
+
+void qvkv::set_oom(uint64_t requested, uint64_t used, uint64_t capacity) {
+    g_oom = qvkv::OomDetail{requested, used, capacity};
+}
+
+qvkv::OomDetail qvkv::last_oom() { return g_oom; }
 
 namespace {
 
@@ -54,18 +63,33 @@ int hip_fail(hipError_t e, const char *what) {
 
 }  // namespace
 
+// What the library keeps per hipStream_t a caller launches on: the kernels' index-error
+// flag and the attention workspace.  Each stream has its own, so a caller's qvkv_check
+// reports only what its own stream's kernels latched, and split-context attention
+// launches on different streams never share partials.  Created on the first launch on
+// the stream; freed by qvkv_close.
+struct StreamState {
+    hipStream_t stream = nullptr;
+    int *d_err = nullptr;  // [0]: latched bits (ERR_*), [1]: taken by the last check
+    void *ws = nullptr;    // attention workspace (partials of context chunks)
+    uint64_t ws_bytes = 0;
+    std::mutex check_mu;   // one check at a time per stream
+};
+
 struct qvkv_dev {
     int device = 0;
-    hipStream_t stream = nullptr;
-    int *d_err = nullptr;        // latched kernel index errors (bit set)
-    void *ws = nullptr;          // attention workspace (partials of context chunks)
-    uint64_t ws_bytes = 0;
+    hipStream_t stream = nullptr;  // the host-memory entry points' own stream
+    StreamState *own = nullptr;    // its state
+    std::vector<StreamState *> streams;  // every stream seen (guarded by mu)
     void *stage = nullptr;       // device staging for the host-memory entry points
     uint64_t stage_bytes = 0;
-    std::mutex mu;               // serialises host-memory entry points and workspace growth
+    hipEvent_t order_ev = nullptr;  // orders pool copies after a caller's stream
+    hipEvent_t t0 = nullptr, t1 = nullptr;  // GPU time of a synchronous call
+    std::mutex mu;  // serialises host-memory entry points, stream states, workspace growth
     std::atomic<uint64_t> used{0}, peak{0}, refused{0};
     std::atomic<uint64_t> uploads{0}, upload_bytes{0}, downloads{0}, download_bytes{0};
-    std::atomic<uint64_t> submissions{0}, wait_ns{0};
+    std::atomic<uint64_t> submissions{0}, wait_ns{0}, timed{0}, gpu_ns{0}, last_gpu_ns{0};
+    std::atomic<uint64_t> stream_waits{0};
     char name[256] = {0};
 };
 
@@ -82,8 +106,6 @@ int set_device(qvkv_dev *dev) {
     return e == hipSuccess ? QVKV_OK : hip_fail(e, "hipSetDevice");
 }
 
-hipStream_t pick(qvkv_dev *, void *stream) { return (hipStream_t)stream; }
-
 void account_alloc(qvkv_dev *dev, uint64_t n) {
     uint64_t u = dev->used.fetch_add(n) + n;
     uint64_t p = dev->peak.load();
@@ -98,6 +120,7 @@ int dev_malloc(qvkv_dev *dev, void **p, uint64_t n) {
         dev->refused.fetch_add(1);
         size_t fr = 0, tot = 0;
         (void)hipMemGetInfo(&fr, &tot);
+        qvkv::set_oom(n, tot - fr, tot);
         return fail(QVKV_E_OOM,
                     "hip device is out of memory: %llu bytes requested, %llu of %llu in use",
                     (unsigned long long)n, (unsigned long long)(tot - fr),
@@ -113,12 +136,12 @@ void dev_free(qvkv_dev *dev, void *p, uint64_t n) {
     dev->used.fetch_sub(n);
 }
 
-// Grows a device buffer to at least `need` bytes (contents not kept).  Waits for the
-// device first, so no enqueued work still reads the old buffer.
-int ensure(qvkv_dev *dev, void **buf, uint64_t *have, uint64_t need) {
+// Grows a device buffer used only on stream `s` to at least `need` bytes (contents not
+// kept).  Waits for `s` first, so no enqueued work still reads the old buffer.
+int ensure(qvkv_dev *dev, hipStream_t s, void **buf, uint64_t *have, uint64_t need) {
     if (*have >= need) return QVKV_OK;
-    hipError_t e = hipDeviceSynchronize();
-    if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
+    hipError_t e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
     dev_free(dev, *buf, *have);
     *buf = nullptr;
     *have = 0;
@@ -128,6 +151,36 @@ int ensure(qvkv_dev *dev, void **buf, uint64_t *have, uint64_t need) {
     if (rc) return rc;
     *have = sz;
     return QVKV_OK;
+}
+
+// The state of `stream`, created on first use.  Caller holds dev->mu.
+int state_locked(qvkv_dev *dev, hipStream_t stream, StreamState **out) {
+    for (StreamState *st : dev->streams)
+        if (st->stream == stream) {
+            *out = st;
+            return QVKV_OK;
+        }
+    auto *st = new StreamState();
+    st->stream = stream;
+    if (int rc = dev_malloc(dev, (void **)&st->d_err, 256)) {
+        delete st;
+        return rc;
+    }
+    const int zero[2] = {0, 0};
+    hipError_t e = hipMemcpy(st->d_err, zero, sizeof zero, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        dev_free(dev, st->d_err, 256);
+        delete st;
+        return hip_fail(e, "hipMemcpy (error flag)");
+    }
+    dev->streams.push_back(st);
+    *out = st;
+    return QVKV_OK;
+}
+
+int state_of(qvkv_dev *dev, void *stream, StreamState **out) {
+    std::lock_guard<std::mutex> lk(dev->mu);
+    return state_locked(dev, (hipStream_t)stream, out);
 }
 
 int geometry(const qvkv_layout *l, Geometry *g) {
@@ -153,7 +206,7 @@ struct Stager {
     }
     uint64_t reserve(uint64_t len) { return add(nullptr, len); }
     int upload(qvkv_dev *dev) {
-        int rc = ensure(dev, &dev->stage, &dev->stage_bytes, total);
+        int rc = ensure(dev, dev->stream, &dev->stage, &dev->stage_bytes, total);
         if (rc) return rc;
         for (auto &p : pieces) {
             if (!p.src || !p.len) continue;
@@ -180,40 +233,76 @@ int download(qvkv_dev *dev, void *host, const void *devp, uint64_t len) {
     return QVKV_OK;
 }
 
-// Waits for the stream and turns a latched kernel index error into QVKV_E_SHAPE.
-int finish(qvkv_dev *dev, hipStream_t s) {
+// Takes a stream's latched error bits: one thread exchanges the flag with 0 (so bits a
+// kernel latches meanwhile are never lost) and keeps what it held in flag[1].
+__global__ void k_take_error(int *flag) {
+    if (threadIdx.x == 0) flag[1] = atomicExch(&flag[0], 0);
+}
+
+// The status a set of latched bits stands for.
+int status_of(int bits) {
+    if (!bits) return QVKV_OK;
+    if (bits == 16)
+        return fail(QVKV_E_UNSUPPORTED,
+                    "q8_0 prefill: a value scale above 512 (dequantised values past the f16 "
+                    "range of the MFMA prefill; QVKV_PREFILL_Q8_FAST=0 selects the form "
+                    "without that limit)");
+    return fail(QVKV_E_SHAPE, "shape mismatch in kv kernel: %s%s%s%s%s",
+                (bits & 1) ? "a block id past the pool; " : "",
+                (bits & 2) ? "a block table shorter than its positions; " : "",
+                (bits & 4) ? "a position past max_pos; " : "",
+                (bits & 8) ? "an output or query range past its bound (out_positions, q_rows); " : "",
+                (bits & 16) ? "a q8_0 value scale past the f16 prefill's range; " : "");
+}
+
+// Waits for the stream's work and turns the index errors its kernels latched into
+// QVKV_E_SHAPE (clearing them).
+int finish(qvkv_dev *dev, StreamState *st) {
+    std::lock_guard<std::mutex> lk(st->check_mu);
     auto t0 = std::chrono::steady_clock::now();
-    hipError_t e = hipStreamSynchronize(s);
+    hipLaunchKernelGGL(k_take_error, dim3(1), dim3(64), 0, st->stream, st->d_err);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "error flag launch");
+    int bits = 0;
+    e = hipMemcpyAsync(&bits, st->d_err + 1, sizeof bits, hipMemcpyDeviceToHost, st->stream);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync (error flag)");
+    e = hipStreamSynchronize(st->stream);
     dev->wait_ns.fetch_add((uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
                                std::chrono::steady_clock::now() - t0)
                                .count());
     if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
-    int bits = 0;
-    e = hipMemcpy(&bits, dev->d_err, sizeof bits, hipMemcpyDeviceToHost);
-    if (e != hipSuccess) return hip_fail(e, "hipMemcpy (error flag)");
-    if (bits) {
-        int zero = 0;
-        e = hipMemcpy(dev->d_err, &zero, sizeof zero, hipMemcpyHostToDevice);
-        if (e != hipSuccess) return hip_fail(e, "hipMemcpy (error flag reset)");
-        if (bits == 16)
-            return fail(QVKV_E_UNSUPPORTED,
-                        "q8_0 prefill: a value scale above 512 (dequantised values past the f16 "
-                        "range of the MFMA prefill; QVKV_PREFILL_Q8_FAST=0 selects the form "
-                        "without that limit)");
-        return fail(QVKV_E_SHAPE,
-                    "shape mismatch in kv kernel: %s%s%s%s",
-                    (bits & 1) ? "a block id past the pool; " : "",
-                    (bits & 2) ? "a block table shorter than its positions; " : "",
-                    (bits & 4) ? "a position past max_pos; " : "",
-                    (bits & 8) ? "an output or query range past its bound (out_positions, q_rows); " : "");
-    }
-    return QVKV_OK;
+    return status_of(bits);
 }
 
 int launched(qvkv_dev *dev, hipError_t e, const char *what) {
     if (e != hipSuccess) return hip_fail(e, what);
     dev->submissions.fetch_add(1);
     return QVKV_OK;
+}
+
+// GPU time of a synchronous call: events on the device's stream around its kernels
+// (time_start before the first launch, time_stop after the last, time_take once done).
+void time_start(qvkv_dev *dev) { (void)hipEventRecord(dev->t0, dev->stream); }
+void time_stop(qvkv_dev *dev) { (void)hipEventRecord(dev->t1, dev->stream); }
+void time_take(qvkv_dev *dev);
+
+// finish() of the device's own stream after a timed synchronous call.
+int finish_timed(qvkv_dev *dev) {
+    const int rc = finish(dev, dev->own);
+    if (rc == QVKV_OK) time_take(dev);
+    return rc;
+}
+
+void time_take(qvkv_dev *dev) {
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, dev->t0, dev->t1) != hipSuccess) {
+        (void)hipGetLastError();
+        return;
+    }
+    const uint64_t ns = (uint64_t)((double)ms * 1e6);
+    dev->last_gpu_ns.store(ns);
+    dev->gpu_ns.fetch_add(ns);
+    dev->timed.fetch_add(1);
 }
 
 }  // namespace
@@ -227,6 +316,14 @@ int qvkv_last_error(char *buf, size_t len) {
         buf[n] = 0;
     }
     return g_err_code;
+}
+
+int qvkv_last_oom(uint64_t *requested, uint64_t *used, uint64_t *capacity) {
+    const qvkv::OomDetail d = qvkv::last_oom();
+    if (requested) *requested = d.requested;
+    if (used) *used = d.used;
+    if (capacity) *capacity = d.capacity;
+    return QVKV_OK;
 }
 
 int qvkv_open(int device, qvkv_dev **out) {
@@ -249,13 +346,18 @@ int qvkv_open(int device, qvkv_dev **out) {
         delete d;
         return hip_fail(e, "hipStreamCreate");
     }
-    if (int rc = dev_malloc(d, (void **)&d->d_err, 256)) {
-        (void)hipStreamDestroy(d->stream);
-        delete d;
-        return rc;
+    if ((e = hipEventCreateWithFlags(&d->order_ev, hipEventDisableTiming)) != hipSuccess ||
+        (e = hipEventCreate(&d->t0)) != hipSuccess || (e = hipEventCreate(&d->t1)) != hipSuccess) {
+        qvkv_close(d);
+        return hip_fail(e, "hipEventCreate");
     }
-    int zero = 0;
-    (void)hipMemcpy(d->d_err, &zero, sizeof zero, hipMemcpyHostToDevice);
+    {
+        std::lock_guard<std::mutex> lk(d->mu);
+        if (int rc = state_locked(d, d->stream, &d->own)) {
+            qvkv_close(d);
+            return rc;
+        }
+    }
     *out = d;
     return QVKV_OK;
 }
@@ -263,11 +365,19 @@ int qvkv_open(int device, qvkv_dev **out) {
 void qvkv_close(qvkv_dev *dev) {
     if (!dev) return;
     (void)hipSetDevice(dev->device);
-    (void)hipStreamSynchronize(dev->stream);
-    dev_free(dev, dev->ws, dev->ws_bytes);
+    // Work may still be in flight on any stream the device's states belong to.
+    (void)hipDeviceSynchronize();
+    for (StreamState *st : dev->streams) {
+        dev_free(dev, st->ws, st->ws_bytes);
+        dev_free(dev, st->d_err, 256);
+        delete st;
+    }
+    dev->streams.clear();
     dev_free(dev, dev->stage, dev->stage_bytes);
-    dev_free(dev, dev->d_err, 256);
-    (void)hipStreamDestroy(dev->stream);
+    if (dev->order_ev) (void)hipEventDestroy(dev->order_ev);
+    if (dev->t0) (void)hipEventDestroy(dev->t0);
+    if (dev->t1) (void)hipEventDestroy(dev->t1);
+    if (dev->stream) (void)hipStreamDestroy(dev->stream);
     delete dev;
 }
 
@@ -290,6 +400,16 @@ int qvkv_usage(const qvkv_dev *dev, qvkv_usage_t *out) {
     return QVKV_OK;
 }
 
+int qvkv_max_arena(const qvkv_dev *dev, uint64_t *out) {
+    if (!dev || !out) return fail(QVKV_E_SHAPE, "null argument");
+    size_t fr = 0, tot = 0;
+    (void)hipSetDevice(dev->device);
+    hipError_t e = hipMemGetInfo(&fr, &tot);
+    if (e != hipSuccess) return hip_fail(e, "hipMemGetInfo");
+    *out = tot;
+    return QVKV_OK;
+}
+
 int qvkv_transfers(const qvkv_dev *dev, qvkv_transfers_t *out) {
     if (!dev || !out) return fail(QVKV_E_SHAPE, "null argument");
     out->uploads = dev->uploads.load();
@@ -298,6 +418,15 @@ int qvkv_transfers(const qvkv_dev *dev, qvkv_transfers_t *out) {
     out->download_bytes = dev->download_bytes.load();
     out->submissions = dev->submissions.load();
     out->wait_ns = dev->wait_ns.load();
+    out->timed = dev->timed.load();
+    out->gpu_ns = dev->gpu_ns.load();
+    out->stream_waits = dev->stream_waits.load();
+    return QVKV_OK;
+}
+
+int qvkv_timing(const qvkv_dev *dev, uint64_t *gpu_ns) {
+    if (!dev || !gpu_ns) return fail(QVKV_E_SHAPE, "null argument");
+    *gpu_ns = dev->last_gpu_ns.load();
     return QVKV_OK;
 }
 
@@ -357,7 +486,9 @@ int qvkv_read(qvkv_dev *dev, const qvkv_buf *buf, size_t offset, void *host, siz
 int qvkv_check(qvkv_dev *dev, void *stream) {
     if (!dev) return fail(QVKV_E_SHAPE, "null device");
     if (int rc = set_device(dev)) return rc;
-    return finish(dev, pick(dev, stream));
+    StreamState *st;
+    if (int rc = state_of(dev, stream, &st)) return rc;
+    return finish(dev, st);
 }
 
 int qvkv_block_bytes(const qvkv_layout *layout, uint64_t *out) {
@@ -380,8 +511,10 @@ int qvkv_append_async(qvkv_dev *dev, const qvkv_layout *layout, void *pool,
     if (n == 0) return QVKV_OK;
     if (!pool || !k || !v || !slots) return fail(QVKV_E_SHAPE, "shape mismatch in append: null pointer");
     if (int rc = set_device(dev)) return rc;
-    return launched(dev, qvkv::launch_append(g, pool, pool_blocks, k, v, slots, n, dev->d_err,
-                                             pick(dev, stream)),
+    StreamState *st;
+    if (int rc = state_of(dev, stream, &st)) return rc;
+    return launched(dev, qvkv::launch_append(g, pool, pool_blocks, k, v, slots, n, st->d_err,
+                                             st->stream),
                     "append launch");
 }
 
@@ -399,10 +532,11 @@ int qvkv_gather_async(qvkv_dev *dev, const qvkv_layout *layout, const void *pool
     if (!pool || !blocks || !table_at || !lens || !out_at || !out_k || !out_v)
         return fail(QVKV_E_SHAPE, "shape mismatch in gather: null pointer");
     if (int rc = set_device(dev)) return rc;
+    StreamState *st;
+    if (int rc = state_of(dev, stream, &st)) return rc;
     return launched(dev, qvkv::launch_gather(g, pool, pool_blocks, blocks, n_table, table_at,
                                              lens, out_at, n_items, max_len, (int)out_dtype,
-                                             out_positions, out_k, out_v, dev->d_err,
-                                             pick(dev, stream)),
+                                             out_positions, out_k, out_v, st->d_err, st->stream),
                     "gather launch");
 }
 
@@ -422,13 +556,16 @@ int qvkv_attention_async(qvkv_dev *dev, const qvkv_layout *layout, const void *p
     if (!pool || !q || !blocks || !table_at || !pos || !out)
         return fail(QVKV_E_SHAPE, "shape mismatch in attention: null pointer");
     if (int rc = set_device(dev)) return rc;
-    if (p.ws_bytes) {
-        std::lock_guard<std::mutex> lk(dev->mu);
-        if (int rc = ensure(dev, &dev->ws, &dev->ws_bytes, p.ws_bytes)) return rc;
-    }
+    // The stream's workspace is grown and handed to the launch under the device lock, so
+    // no other thread frees it in between; launches on one stream use it in turn.
+    std::lock_guard<std::mutex> lk(dev->mu);
+    StreamState *st;
+    if (int rc = state_locked(dev, (hipStream_t)stream, &st)) return rc;
+    if (p.ws_bytes)
+        if (int rc = ensure(dev, st->stream, &st->ws, &st->ws_bytes, p.ws_bytes)) return rc;
     return launched(dev, qvkv::launch_attention(g, p, pool, pool_blocks, q, blocks, n_table,
                                                 table_at, pos, n_items, heads, max_pos, out,
-                                                dev->ws, dev->d_err, pick(dev, stream)),
+                                                st->ws, st->d_err, st->stream),
                     "attention launch");
 }
 
@@ -449,9 +586,11 @@ int qvkv_prefill_attention_async(qvkv_dev *dev, const qvkv_layout *layout, const
     if (!pool || !q || !blocks || !table_at || !pos0 || !q_at || !n_tok || !out)
         return fail(QVKV_E_SHAPE, "shape mismatch in prefill attention: null pointer");
     if (int rc = set_device(dev)) return rc;
+    StreamState *st;
+    if (int rc = state_of(dev, stream, &st)) return rc;
     return launched(dev, qvkv::launch_prefill(g, pool, pool_blocks, q, blocks, n_table, table_at,
                                               pos0, q_at, n_tok, n_seg, heads, max_pos, max_tok,
-                                              q_rows, out, dev->d_err, pick(dev, stream)),
+                                              q_rows, out, st->d_err, st->stream),
                     "prefill attention launch");
 }
 
@@ -464,8 +603,10 @@ int qvkv_block_copy_async(qvkv_dev *dev, const qvkv_layout *layout, void *pool,
     if (n == 0) return QVKV_OK;
     if (!pool || !src || !dst) return fail(QVKV_E_SHAPE, "shape mismatch in block copy: null pointer");
     if (int rc = set_device(dev)) return rc;
-    return launched(dev, qvkv::launch_block_copy(g, pool, pool_blocks, src, dst, n, dev->d_err,
-                                                 pick(dev, stream)),
+    StreamState *st;
+    if (int rc = state_of(dev, stream, &st)) return rc;
+    return launched(dev, qvkv::launch_block_copy(g, pool, pool_blocks, src, dst, n, st->d_err,
+                                                 st->stream),
                     "block copy launch");
 }
 
@@ -499,13 +640,15 @@ int qvkv_append(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *pool, const 
     const uint64_t rowb = g.kv_out * 4;
     uint64_t ko = st.add(k, n * rowb), vo = st.add(v, n * rowb), so = st.add(slots, n * 4ull);
     if (int rc = st.upload(dev)) return rc;
+    time_start(dev);
     if (int rc = launched(dev, qvkv::launch_append(g, pool->ptr, held, st.at<float>(dev, ko),
                                                    st.at<float>(dev, vo),
-                                                   st.at<uint32_t>(dev, so), n, dev->d_err,
+                                                   st.at<uint32_t>(dev, so), n, dev->own->d_err,
                                                    dev->stream),
                           "append launch"))
         return rc;
-    return finish(dev, dev->stream);
+    time_stop(dev);
+    return finish_timed(dev);
 }
 
 int qvkv_gather(qvkv_dev *dev, const qvkv_layout *layout, const qvkv_buf *pool,
@@ -544,44 +687,25 @@ int qvkv_gather(qvkv_dev *dev, const qvkv_layout *layout, const qvkv_buf *pool,
              lo = st.add(lens, n_items * 4ull), oo = st.add(out_at, n_items * 8ull);
     uint64_t ko = st.reserve(ob), vo = st.reserve(ob);
     if (int rc = st.upload(dev)) return rc;
+    time_start(dev);
     if (int rc = launched(dev, qvkv::launch_gather(g, pool->ptr, held, st.at<uint32_t>(dev, bo),
                                                    n_table, st.at<uint32_t>(dev, to),
                                                    st.at<uint32_t>(dev, lo),
                                                    st.at<uint64_t>(dev, oo), n_items, max_len,
                                                    (int)out_dtype, out_positions,
                                                    st.at<void>(dev, ko), st.at<void>(dev, vo),
-                                                   dev->d_err, dev->stream),
+                                                   dev->own->d_err, dev->stream),
                           "gather launch"))
         return rc;
+    time_stop(dev);
     if (int rc = download(dev, out_k, st.at<void>(dev, ko), ob)) return rc;
     if (int rc = download(dev, out_v, st.at<void>(dev, vo), ob)) return rc;
-    return finish(dev, dev->stream);
+    return finish_timed(dev);
 }
 
 int qvkv_block_copy(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *pool,
                     const uint32_t *src, const uint32_t *dst, uint32_t n) {
-    if (!dev) return fail(QVKV_E_SHAPE, "null device");
-    Geometry g;
-    if (int rc = geometry(layout, &g)) return rc;
-    uint64_t held;
-    if (int rc = pool_of(dev, pool, g, &held)) return rc;
-    if (n && (!src || !dst)) return fail(QVKV_E_SHAPE, "shape mismatch in block copy: null pointer");
-    for (uint32_t i = 0; i < n; i++)
-        if (src[i] >= held || dst[i] >= held)
-            return fail(QVKV_E_SHAPE, "shape mismatch in block copy: a block past the pool's %llu",
-                        (unsigned long long)held);
-    if (n == 0) return QVKV_OK;
-    std::lock_guard<std::mutex> lk(dev->mu);
-    if (int rc = set_device(dev)) return rc;
-    Stager st;
-    uint64_t so = st.add(src, n * 4ull), dd = st.add(dst, n * 4ull);
-    if (int rc = st.upload(dev)) return rc;
-    if (int rc = launched(dev, qvkv::launch_block_copy(g, pool->ptr, held, st.at<uint32_t>(dev, so),
-                                                       st.at<uint32_t>(dev, dd), n, dev->d_err,
-                                                       dev->stream),
-                          "block copy launch"))
-        return rc;
-    return finish(dev, dev->stream);
+    return qvkv::block_copy_after(dev, layout, pool, src, dst, n, false, nullptr);
 }
 
 }  // extern "C"
@@ -638,9 +762,9 @@ hipError_t attend_tokens(qvkv_dev *dev, const Geometry &g, const qvkv::AttnPlan 
                                     st.at<uint32_t>(dev, ss.ta), st.at<uint32_t>(dev, ss.p0),
                                     st.at<uint32_t>(dev, ss.qa), st.at<uint32_t>(dev, ss.nt),
                                     (uint32_t)sg.n_tok.size(), heads, max_pos, sg.max_tok, s,
-                                    dout, dev->d_err, dev->stream, f16_values);
+                                    dout, dev->own->d_err, dev->stream, f16_values);
     return qvkv::launch_attention(g, plan, pool, held, dq, dblocks, n_table, dtable_at, dpos, s,
-                                  heads, max_pos, dout, dev->ws, dev->d_err, dev->stream);
+                                  heads, max_pos, dout, dev->own->ws, dev->own->d_err, dev->stream);
 }
 
 }  // namespace
@@ -697,7 +821,7 @@ int qvkv_decode_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *po
     std::lock_guard<std::mutex> lk(dev->mu);
     if (int rc = set_device(dev)) return rc;
     if (p.ws_bytes)
-        if (int rc = ensure(dev, &dev->ws, &dev->ws_bytes, p.ws_bytes)) return rc;
+        if (int rc = ensure(dev, dev->stream, &dev->own->ws, &dev->own->ws_bytes, p.ws_bytes)) return rc;
     const uint64_t rowb = g.kv_out * 4, qb = (uint64_t)s * heads * g.D * 4;
     Stager st;
     uint64_t sko = st.add(sk.data(), n_sync * rowb), svo = st.add(sv.data(), n_sync * rowb),
@@ -708,13 +832,14 @@ int qvkv_decode_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *po
     StagedSegments ss;
     ss.add(st, sg);
     if (int rc = st.upload(dev)) return rc;
+    time_start(dev);
     hipError_t e = hipSuccess;
     if (n_sync)
         e = qvkv::launch_append(g, pool->ptr, held, st.at<float>(dev, sko), st.at<float>(dev, svo),
-                                st.at<uint32_t>(dev, sto), n_sync, dev->d_err, dev->stream);
+                                st.at<uint32_t>(dev, sto), n_sync, dev->own->d_err, dev->stream);
     if (int rc = launched(dev, e, "append launch (sync rows)")) return rc;
     e = qvkv::launch_append(g, pool->ptr, held, st.at<float>(dev, kno), st.at<float>(dev, vno),
-                            st.at<uint32_t>(dev, slo), s, dev->d_err, dev->stream);
+                            st.at<uint32_t>(dev, slo), s, dev->own->d_err, dev->stream);
     if (int rc = launched(dev, e, "append launch (new rows)")) return rc;
     auto attend = [&](bool f16_values) {
         return attend_tokens(dev, g, p, sg, ss, st, pool->ptr, held, st.at<float>(dev, qo),
@@ -724,12 +849,15 @@ int qvkv_decode_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *po
     };
     e = attend(true);
     if (int rc = launched(dev, e, "attention launch")) return rc;
+    time_stop(dev);
     if (int rc = download(dev, out, st.at<void>(dev, oo), qb)) return rc;
-    int rc = finish(dev, dev->stream);
+    int rc = finish_timed(dev);
     if (rc == QVKV_E_UNSUPPORTED) {  // q8_0 values past the f16 prefill's range: f32 form
+        time_start(dev);
         if (int rc2 = launched(dev, attend(false), "attention launch")) return rc2;
+        time_stop(dev);
         if (int rc2 = download(dev, out, st.at<void>(dev, oo), qb)) return rc2;
-        rc = finish(dev, dev->stream);
+        rc = finish_timed(dev);
     }
     return rc;
 }
@@ -766,7 +894,7 @@ int qvkv_prelude_async(qvkv_dev *dev, const qvkv_layout *layout, const qvkv_prel
     if (!q || !k || !v) return fail(QVKV_E_SHAPE, "shape mismatch in prelude: null pointer");
     if (int rc = set_device(dev)) return rc;
     return launched(dev, qvkv::launch_prelude(q, k, v, s, p->heads, (uint32_t)g.G, (uint32_t)g.D,
-                                              prelude_args(p), pick(dev, stream)),
+                                              prelude_args(p), (hipStream_t)stream),
                     "prelude launch");
 }
 
@@ -819,7 +947,7 @@ int qvkv_prelude_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *p
     std::lock_guard<std::mutex> lk(dev->mu);
     if (int rc = set_device(dev)) return rc;
     if (plan.ws_bytes)
-        if (int rc = ensure(dev, &dev->ws, &dev->ws_bytes, plan.ws_bytes)) return rc;
+        if (int rc = ensure(dev, dev->stream, &dev->own->ws, &dev->own->ws_bytes, plan.ws_bytes)) return rc;
     const uint64_t q_out = (uint64_t)heads * g.D, rowb = g.kv_out * 4, qb = s * q_out * 4;
     const uint64_t nq = p->norm == QVKV_NORM_PER_HEAD ? g.D : q_out;
     const uint64_t nk = p->norm == QVKV_NORM_PER_HEAD ? g.D : g.kv_out;
@@ -846,15 +974,16 @@ int qvkv_prelude_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *p
     a.k_norm = (p->norm && p->k_norm) ? st.at<float>(dev, kno) : nullptr;
     a.rope = st.at<float>(dev, ro);
     float *dq = st.at<float>(dev, qo), *dk = st.at<float>(dev, ko), *dv = st.at<float>(dev, vo);
+    time_start(dev);
     hipError_t e = qvkv::launch_prelude(dq, dk, dv, s, heads, (uint32_t)g.G, (uint32_t)g.D, a,
                                         dev->stream);
     if (int rc = launched(dev, e, "prelude launch")) return rc;
     if (n_sync) {
         e = qvkv::launch_append(g, pool->ptr, held, st.at<float>(dev, sko), st.at<float>(dev, svo),
-                                st.at<uint32_t>(dev, sto), n_sync, dev->d_err, dev->stream);
+                                st.at<uint32_t>(dev, sto), n_sync, dev->own->d_err, dev->stream);
         if (int rc = launched(dev, e, "append launch (sync rows)")) return rc;
     }
-    e = qvkv::launch_append(g, pool->ptr, held, dk, dv, st.at<uint32_t>(dev, slo), s, dev->d_err,
+    e = qvkv::launch_append(g, pool->ptr, held, dk, dv, st.at<uint32_t>(dev, slo), s, dev->own->d_err,
                             dev->stream);
     if (int rc = launched(dev, e, "append launch (new rows)")) return rc;
     auto attend = [&](bool f16_values) {
@@ -865,18 +994,60 @@ int qvkv_prelude_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *p
     };
     e = attend(true);
     if (int rc = launched(dev, e, "attention launch")) return rc;
+    time_stop(dev);
     if (int rc = download(dev, out, st.at<void>(dev, oo), qb)) return rc;
     if (k_new)
         if (int rc = download(dev, k_new, dk, s * rowb)) return rc;
     if (v_new)
         if (int rc = download(dev, v_new, dv, s * rowb)) return rc;
-    int rc = finish(dev, dev->stream);
+    int rc = finish_timed(dev);
     if (rc == QVKV_E_UNSUPPORTED) {  // q8_0 values past the f16 prefill's range: f32 form
+        time_start(dev);
         if (int rc2 = launched(dev, attend(false), "attention launch")) return rc2;
+        time_stop(dev);
         if (int rc2 = download(dev, out, st.at<void>(dev, oo), qb)) return rc2;
-        rc = finish(dev, dev->stream);
+        rc = finish_timed(dev);
     }
     return rc;
 }
 
 }  // extern "C"
+
+// The host-memory block copy, optionally ordered after the work already queued on a
+// caller's stream: an event recorded there makes the device's own stream wait before
+// the copy kernel reads the source blocks (the pool manager's copy-on-write and
+// compaction copies, whose source rows the caller may have appended asynchronously).
+int qvkv::block_copy_after(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *pool,
+                           const uint32_t *src, const uint32_t *dst, uint32_t n, bool ordered,
+                           void *after) {
+    if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    Geometry g;
+    if (int rc = geometry(layout, &g)) return rc;
+    uint64_t held;
+    if (int rc = pool_of(dev, pool, g, &held)) return rc;
+    if (n && (!src || !dst)) return fail(QVKV_E_SHAPE, "shape mismatch in block copy: null pointer");
+    for (uint32_t i = 0; i < n; i++)
+        if (src[i] >= held || dst[i] >= held)
+            return fail(QVKV_E_SHAPE, "shape mismatch in block copy: a block past the pool's %llu",
+                        (unsigned long long)held);
+    if (n == 0) return QVKV_OK;
+    std::lock_guard<std::mutex> lk(dev->mu);
+    if (int rc = set_device(dev)) return rc;
+    Stager st;
+    uint64_t so = st.add(src, n * 4ull), dd = st.add(dst, n * 4ull);
+    if (int rc = st.upload(dev)) return rc;
+    if (ordered && (hipStream_t)after != dev->stream) {
+        hipError_t e = hipEventRecord(dev->order_ev, (hipStream_t)after);
+        if (e == hipSuccess) e = hipStreamWaitEvent(dev->stream, dev->order_ev, 0);
+        if (e != hipSuccess) return hip_fail(e, "ordering after the caller's stream");
+        dev->stream_waits.fetch_add(1);
+    }
+    time_start(dev);
+    if (int rc = launched(dev, qvkv::launch_block_copy(g, pool->ptr, held, st.at<uint32_t>(dev, so),
+                                                       st.at<uint32_t>(dev, dd), n, dev->own->d_err,
+                                                       dev->stream),
+                          "block copy launch"))
+        return rc;
+    time_stop(dev);
+    return finish_timed(dev);
+}

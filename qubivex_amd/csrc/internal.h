@@ -22,6 +22,20 @@ struct Geometry {
 // Records the calling thread's last error (returned by qvkv_last_error); returns code.
 int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 
+// Detail of the calling thread's last QVKV_E_OOM (ComputeError::OutOfDeviceMemory's
+// requested / used / capacity bytes); set together with the error, read by qvkv_last_oom.
+struct OomDetail {
+    uint64_t requested = 0, used = 0, capacity = 0;
+};
+void set_oom(uint64_t requested, uint64_t used, uint64_t capacity);
+OomDetail last_oom();
+
+// qvkv_block_copy; with `ordered`, the copy runs after the work queued on stream `after`
+// (a hipStream_t; 0 is the null stream) when the call was made.
+int block_copy_after(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *pool,
+                     const uint32_t *src, const uint32_t *dst, uint32_t n, bool ordered,
+                     void *after);
+
 // Validates a layout and fills the geometry; returns a QVKV_* status and a message.
 int make_geometry(const qvkv_layout *l, Geometry *g, const char **why);
 

@@ -54,6 +54,15 @@ namespace {
 
 int err(int code, const char *msg) { return qvkv::set_error(code, "%s", msg); }
 
+// A dry free list: QVKV_E_OOM with the blocks asked for, in use and held, in bytes.
+int dry(qvkv_pool *p, uint64_t need) {
+    p->full++;
+    const uint64_t bb = p->g.block_bytes;
+    err(QVKV_E_OOM, "hip device is out of memory: the KV pool has no free block");
+    qvkv::set_oom(need * bb, (p->n_blocks - p->free.size()) * bb, p->n_blocks * bb);
+    return QVKV_E_OOM;
+}
+
 Seq *seq_of(qvkv_pool *p, uint32_t s) {
     return (s < p->seqs.size() && p->seqs[s].live) ? &p->seqs[s] : nullptr;
 }
@@ -98,8 +107,10 @@ uint64_t release(qvkv_pool *p, uint32_t h) {
     return returned;
 }
 
-// Copies block pairs on the device, in one launch, before returning.
-int copy_blocks(qvkv_pool *p, const std::vector<uint32_t> &src, const std::vector<uint32_t> &dst) {
+// Copies block pairs on the device, in one launch, after the work already queued on the
+// caller's `stream` (which wrote the source rows), before returning.
+int copy_blocks(qvkv_pool *p, const std::vector<uint32_t> &src, const std::vector<uint32_t> &dst,
+                void *stream) {
     if (src.empty()) return QVKV_OK;
     if (!p->dev) {
         p->log_src.insert(p->log_src.end(), src.begin(), src.end());
@@ -108,7 +119,8 @@ int copy_blocks(qvkv_pool *p, const std::vector<uint32_t> &src, const std::vecto
         p->log_dst.push_back(UINT32_MAX);
         return QVKV_OK;
     }
-    return qvkv_block_copy(p->dev, &p->layout, p->buf, src.data(), dst.data(), (uint32_t)src.size());
+    return qvkv::block_copy_after(p->dev, &p->layout, p->buf, src.data(), dst.data(),
+                                  (uint32_t)src.size(), true, stream);
 }
 
 uint64_t splitmix(uint64_t &x) {
@@ -247,7 +259,7 @@ int qvkv_seq_touch(qvkv_pool *p, uint32_t seq) {
 }
 
 int qvkv_pool_plan_append(qvkv_pool *p, const uint32_t *seqs, const uint32_t *count,
-                          uint32_t n_seqs, uint32_t layer, uint32_t *slots_out) {
+                          uint32_t n_seqs, uint32_t layer, uint32_t *slots_out, void *stream) {
     if (!p || (n_seqs && (!seqs || !count || !slots_out)))
         return err(QVKV_E_SHAPE, "shape mismatch in pool: null argument");
     std::lock_guard<std::mutex> lk(p->mu);
@@ -275,10 +287,7 @@ int qvkv_pool_plan_append(qvkv_pool *p, const uint32_t *seqs, const uint32_t *co
             }
         }
     }
-    if (need > p->free.size()) {
-        p->full++;
-        return err(QVKV_E_OOM, "hip device is out of memory: the KV pool has no free block");
-    }
+    if (need > p->free.size()) return dry(p, need);
     std::vector<uint32_t> src, dst;
     uint64_t o = 0;
     for (uint32_t i = 0; i < n_seqs; i++) {
@@ -313,7 +322,7 @@ int qvkv_pool_plan_append(qvkv_pool *p, const uint32_t *seqs, const uint32_t *co
     }
     p->layers++;
     // A shared block's filled slots are copied before the caller writes into the copy.
-    return copy_blocks(p, src, dst);
+    return copy_blocks(p, src, dst, stream);
 }
 
 int qvkv_pool_plan_attention(qvkv_pool *p, const uint32_t *seqs, const uint32_t *pos,
@@ -321,7 +330,8 @@ int qvkv_pool_plan_attention(qvkv_pool *p, const uint32_t *seqs, const uint32_t 
                              uint32_t *blocks_out, uint64_t blocks_cap, uint64_t *n_table_out,
                              uint32_t *table_at_out, uint32_t *new_slot_out,
                              uint32_t *sync_to_out, uint32_t *sync_item_out,
-                             uint32_t *sync_pos_out, uint64_t sync_cap, uint64_t *n_sync_out) {
+                             uint32_t *sync_pos_out, uint64_t sync_cap, uint64_t *n_sync_out,
+                             void *stream) {
     if (!p || !n_table_out || !n_sync_out ||
         (n_seqs && (!seqs || !pos || !epochs || !table_at_out || !new_slot_out)))
         return err(QVKV_E_SHAPE, "shape mismatch in pool: null argument");
@@ -356,9 +366,8 @@ int qvkv_pool_plan_attention(qvkv_pool *p, const uint32_t *seqs, const uint32_t 
             const uint32_t old = tab[bi];
             if (p->refs[old] > 1) {
                 if (p->free.empty()) {
-                    p->full++;
-                    copy_blocks(p, src, dst);
-                    return err(QVKV_E_OOM, "hip device is out of memory: the KV pool has no free block");
+                    copy_blocks(p, src, dst, stream);
+                    return dry(p, 1);
                 }
                 const uint32_t nb = p->free.back();
                 p->free.pop_back();
@@ -373,9 +382,8 @@ int qvkv_pool_plan_attention(qvkv_pool *p, const uint32_t *seqs, const uint32_t 
         const uint64_t need = (uint64_t)pos[i] / B + 1;  // discrete.rs:988-994
         while (tab.size() < need) {
             if (p->free.empty()) {
-                p->full++;
-                copy_blocks(p, src, dst);
-                return err(QVKV_E_OOM, "hip device is out of memory: the KV pool has no free block");
+                copy_blocks(p, src, dst, stream);
+                return dry(p, need - tab.size());
             }
             const uint32_t nb = p->free.back();
             p->free.pop_back();
@@ -402,7 +410,7 @@ int qvkv_pool_plan_attention(qvkv_pool *p, const uint32_t *seqs, const uint32_t 
     *n_sync_out = ns;
     p->layers++;
     p->rows += ns;
-    return copy_blocks(p, src, dst);
+    return copy_blocks(p, src, dst, stream);
 }
 
 int qvkv_pool_tables(const qvkv_pool *p, const uint32_t *seqs, uint32_t n_seqs, uint32_t layer,
@@ -454,7 +462,7 @@ int qvkv_pool_evict_lru(qvkv_pool *p, uint64_t target_blocks, uint32_t *released
     return QVKV_OK;
 }
 
-int qvkv_pool_compact(qvkv_pool *p, uint64_t seed, uint64_t *moved) {
+int qvkv_pool_compact(qvkv_pool *p, uint64_t seed, uint64_t *moved, void *stream) {
     if (!p) return err(QVKV_E_SHAPE, "shape mismatch in pool: null argument");
     std::lock_guard<std::mutex> lk(p->mu);
     const uint64_t N = p->n_blocks;
@@ -497,8 +505,11 @@ int qvkv_pool_compact(qvkv_pool *p, uint64_t seed, uint64_t *moved) {
         if (src.empty()) {
             // Every remaining dst holds data still to move: only cycles are left.  Park
             // one member of as many cycles as there are spares.
-            if (spares.empty())
-                return err(QVKV_E_OOM, "hip device is out of memory: compaction of a full pool needs one free block");
+            if (spares.empty()) {
+                err(QVKV_E_OOM, "hip device is out of memory: compaction of a full pool needs one free block");
+                qvkv::set_oom(p->g.block_bytes, N * p->g.block_bytes, N * p->g.block_bytes);
+                return QVKV_E_OOM;
+            }
             std::vector<uint8_t> in_batch(N, 0);
             rest.clear();
             for (auto &m : pending) {
@@ -516,7 +527,7 @@ int qvkv_pool_compact(qvkv_pool *p, uint64_t seed, uint64_t *moved) {
                 }
             }
         }
-        if (int rc = copy_blocks(p, src, dst)) return rc;
+        if (int rc = copy_blocks(p, src, dst, stream)) return rc;
         copies += src.size();
         for (size_t i = 0; i < src.size(); i++) {
             occupied[src[i]] = 0;

@@ -149,6 +149,18 @@ class HipDevice:
     def stream(self):
         return lib.qvkv_stream(self.handle)
 
+    def timing(self):
+        """GPU nanoseconds of the last synchronous (host-memory) call."""
+        ns = ctypes.c_uint64()
+        check(lib.qvkv_timing(self.handle, ctypes.byref(ns)))
+        return ns.value
+
+    def max_arena(self):
+        """DiscreteDevice::max_arena: the largest buffer one call can address."""
+        n = ctypes.c_uint64()
+        check(lib.qvkv_max_arena(self.handle, ctypes.byref(n)))
+        return n.value
+
     def check(self, stream=None):
         """Waits for `stream` and raises ShapeError for an index error a kernel latched
         (UnsupportedError for a q8_0 value scale past the range of the MFMA prefill)."""
@@ -438,15 +450,23 @@ class KvPool:
     def touch(self, seq):
         check(lib.qvkv_seq_touch(self.handle, seq))
 
-    def plan_append(self, seqs, counts, layer):
+    def _copy_stream(self, stream):
+        """The stream the pool's copies are ordered after: the given torch stream, else
+        torch's current stream (None for a host-only pool)."""
+        return None if self.dev is None else _stream(stream)
+
+    def plan_append(self, seqs, counts, layer, stream=None):
+        """Slots for counts[i] new positions of seqs[i]; copy-on-write copies run after the
+        work queued on `stream` (default: torch's current stream)."""
         s, sp = _np(seqs, np.uint32)
         c, cp = _np(counts, np.uint32)
         out = np.zeros(int(c.sum()), np.uint32)
         check(lib.qvkv_pool_plan_append(self.handle, sp, cp, s.size, layer,
-                                        out.ctypes.data_as(ctypes.c_void_p)))
+                                        out.ctypes.data_as(ctypes.c_void_p),
+                                        self._copy_stream(stream)))
         return out
 
-    def plan_attention(self, seqs, pos, epochs, layer):
+    def plan_attention(self, seqs, pos, epochs, layer, stream=None):
         """attention_plan of one pass (qvkv_pool_plan_attention): returns a dict with
         blocks, table_at, pos, new_slot, sync_to, sync_item, sync_pos."""
         s, sp = _np(seqs, np.uint32)
@@ -465,7 +485,8 @@ class KvPool:
         check(lib.qvkv_pool_plan_attention(self.handle, sp, pp, ep, s.size, layer, vp(blocks),
                                            blocks.size, ctypes.byref(nt), vp(table_at),
                                            vp(new_slot), vp(sync_to), vp(sync_item), vp(sync_pos),
-                                           sync_to.size, ctypes.byref(ns)))
+                                           sync_to.size, ctypes.byref(ns),
+                                           self._copy_stream(stream)))
         n = ns.value
         return {"blocks": blocks[:nt.value], "table_at": table_at, "pos": p, "new_slot": new_slot,
                 "sync_to": sync_to[:n], "sync_item": sync_item[:n], "sync_pos": sync_pos[:n]}
@@ -492,9 +513,10 @@ class KvPool:
                                       out.ctypes.data_as(ctypes.c_void_p), cap, ctypes.byref(n)))
         return out[:min(n.value, cap)].tolist()
 
-    def compact(self, seed=0):
+    def compact(self, seed=0, stream=None):
         moved = ctypes.c_uint64()
-        check(lib.qvkv_pool_compact(self.handle, seed, ctypes.byref(moved)))
+        check(lib.qvkv_pool_compact(self.handle, seed, ctypes.byref(moved),
+                                    self._copy_stream(stream)))
         return moved.value
 
     def refcount(self, block):

@@ -271,6 +271,11 @@ def test_cfg4_prefix_sharing_cow_eviction_compaction(hip):
     def as_heads(x):
         return x.view(-1, G, D).permute(1, 0, 2).half().contiguous()
 
+    # Grow the library's staging buffer first, so no allocation inside the copy-on-write
+    # calls below waits for the device: the copies must be ordered after the prefix
+    # appends (queued on torch's stream) by the event the pool manager waits on alone.
+    hip.gather_host(layout, pool.buffer, [0], [0], [16], [0], 8192)
+    waits0 = hip.transfers()["stream_waits"]
     parent = pool.create()
     prefix = [append([parent], [PREFIX], l) for l in range(L)]
     kids = [pool.fork(parent, PREFIX) for _ in range(S)]
@@ -280,6 +285,7 @@ def test_cfg4_prefix_sharing_cow_eviction_compaction(hip):
     hip.check()
     st = pool.stats()
     assert st["cow_copies"] == S * L, st  # the shared partial block, once per child and layer
+    assert hip.transfers()["stream_waits"] - waits0 == L  # one ordered COW batch per layer
     # every child reads the shared prefix, then its own rows; the parent is unchanged
     for l in r.choice(L, 3, replace=False):
         pk, pv = read(parent, l)

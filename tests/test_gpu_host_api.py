@@ -60,6 +60,12 @@ def test_host_append_gather_copy_match_the_oracle(hip, dtype):
     assert np.array_equal(gk2, gk)
     tr = hip.transfers()
     assert tr["submissions"] > 0 and tr["upload_bytes"] > k.nbytes
+    # GPU time of the synchronous calls (TransferStats::timed / gpu_ns)
+    hip.append_host(L, buf, k, v, slots)
+    t1 = hip.transfers()
+    assert t1["timed"] == tr["timed"] + 1 and t1["gpu_ns"] > tr["gpu_ns"]
+    assert 0 < hip.timing() < 10**9
+    assert hip.max_arena() >= hip.usage()["capacity"] // 2
     buf.close()
 
 
@@ -185,6 +191,66 @@ def test_concurrent_callers_on_one_device(hip):
     for t in threads:
         t.join()
     assert not errors, errors
+
+
+def test_split_context_attention_on_concurrent_streams(hip):
+    """Four threads, each on its own stream, run attention over one item of 3-5 k
+    positions: launches that split the context into chunks, so each needs the partials
+    workspace, grown concurrently (the trait is Send + Sync, discrete.rs:433).  Each result
+    matches its own oracle.  One thread also passes a block id past its pool on its second
+    launch: only its own stream's check reports it."""
+    import torch
+
+    from qubivex_amd import KvLayout, ShapeError
+
+    L = KvLayout("f16", 4, 128, 16)
+    H = 32
+    errors, reported = [], {}
+
+    def worker(seed):
+        try:
+            r = np.random.default_rng(seed)
+            st = torch.cuda.Stream()
+            n = int(r.integers(3000, 5000))
+            N = n // 16 + 9
+            blocks, table_at = random_tables(r, [n], 16, N)
+            k = r.standard_normal((n, L.kv_out)).astype(np.float32)
+            v = r.standard_normal((n, L.kv_out)).astype(np.float32)
+            q = r.standard_normal((1, H, 128)).astype(np.float32)
+            slots = slots_of(blocks, table_at, 0, np.arange(n), 16)
+            with torch.cuda.stream(st):
+                pool = torch.zeros(N * L.block_bytes, dtype=torch.uint8, device="cuda")
+                t32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.uint32).view(np.int32)).cuda()  # noqa: E731
+                dk, dv, dq = (torch.from_numpy(x).cuda() for x in (k, v, q))
+                db, dt, dp = t32(blocks), t32(table_at), t32([n - 1])
+                bad = t32(np.where(np.arange(blocks.size) == 3, N + 5, blocks))
+                out = torch.empty((1, H, 128), device="cuda")
+                hip.append(L, pool, N, dk, dv, t32(slots), stream=st)
+                sim = oracle.SimPool(N, 4, 128, 16, oracle.F16)
+                sim.store(k, v, slots)
+                want = sim.attention(q, H, blocks, table_at, np.array([n - 1], np.uint32))
+                for it in range(6):
+                    out.fill_(float("nan"))
+                    tab = bad if (seed == 2 and it == 1) else db
+                    hip.attention(L, pool, N, dq, tab, dt, dp, H, n - 1, out, stream=st)
+                    try:
+                        hip.check(st)
+                    except ShapeError:
+                        reported[(seed, it)] = True
+                        continue
+                    e = attn_errors(out.cpu().numpy(), want)
+                    if not (e[0] <= MAX_ABS and e[1] <= REL_L2):
+                        errors.append((seed, it, e))
+        except Exception as ex:  # noqa: BLE001 - reported below
+            errors.append((seed, repr(ex)))
+
+    threads = [threading.Thread(target=worker, args=(s,)) for s in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    assert reported == {(2, 1): True}, reported
 
 
 def test_host_entry_points_reject_null_arrays(hip):

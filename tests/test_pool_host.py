@@ -1,6 +1,8 @@
 """The host pool manager (block pool, block tables, sharing, COW, eviction, compaction) on
 a host-only pool: no GPU.  Block copies the pool issues are applied to the oracle's
 simulated pool, so every check is on the logical keys and values each sequence reads."""
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -213,6 +215,63 @@ def test_a_dry_pool_declines_and_changes_nothing():
     assert p.stats()["full"] == 1
     assert (p.tables([a], 0)[0].tolist(), p.stats()["free"]) == before
     assert p.length(b, 0) == 0
+
+
+def test_a_dry_pool_reports_requested_used_and_capacity():
+    """QVKV_E_OOM carries ComputeError::OutOfDeviceMemory's fields
+    (crates/qubivex-compute/src/lib.rs:64-75): the blocks asked for, the blocks in use and
+    the pool, in bytes; a later failure of another kind clears them."""
+    from qubivex_amd import OutOfDeviceMemory, ShapeError, _lib
+
+    p = host_pool(5)
+    bb = p.layout.block_bytes
+    a, b = p.create(), p.create()
+    p.plan_append([a], [3 * B], 0)
+    with pytest.raises(OutOfDeviceMemory) as ei:
+        p.plan_append([a, b], [1, 2 * B], 0)  # 3 blocks asked, 3 of 5 in use
+    assert (ei.value.requested, ei.value.used, ei.value.capacity) == (3 * bb, 3 * bb, 5 * bb)
+    with pytest.raises(ShapeError):
+        p.plan_append([a], [1], 7)  # no such layer
+    r, u, c = (ctypes.c_uint64(9) for _ in range(3))
+    _lib.lib.qvkv_last_oom(ctypes.byref(r), ctypes.byref(u), ctypes.byref(c))
+    assert (r.value, u.value, c.value) == (0, 0, 0)
+
+
+def test_device_pools_order_their_copies_after_the_callers_stream(monkeypatch):
+    """The binding hands the pool manager torch's current stream (or the one given), which
+    the library's copy-on-write and compaction copies wait for; host-only pools pass none.
+    (The device side, an event recorded on that stream and waited for by the copy, is
+    exercised on the GPU by the copy-on-write configuration test.)"""
+    from qubivex_amd import kv
+
+    p = host_pool(64, 2)
+    seen = []
+    real = {n: getattr(kv.lib, n) for n in ("qvkv_pool_plan_append", "qvkv_pool_plan_attention",
+                                            "qvkv_pool_compact")}
+
+    def spy(name):
+        def f(*args):
+            seen.append((name, args[-1]))
+            return real[name](*args)
+        return f
+
+    for n in real:
+        monkeypatch.setattr(kv.lib, n, spy(n))
+    s = p.create()
+    p.plan_append([s], [5], 0)
+    p.compact()
+    assert [a for _, a in seen] == [None, None]
+    seen.clear()
+    fake = ctypes.c_void_p(0xABC0)
+    monkeypatch.setattr(kv, "_stream", lambda stream: fake if stream is None else stream)
+    p.dev = "a device"  # the Python side only: the C pool stays host-only
+    p.plan_append([s], [5], 0)
+    p.plan_attention([s], [12], [0], 1)
+    p.compact()
+    mine = ctypes.c_void_p(0xDEF0)
+    p.plan_append([s], [1], 0, stream=mine)
+    assert [a.value for _, a in seen] == [0xABC0, 0xABC0, 0xABC0, 0xDEF0]
+    p.dev = None
 
 
 def test_fork_shares_blocks_and_copies_on_write():
