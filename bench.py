@@ -1,24 +1,31 @@
 """Benchmark of the paged KV-cache hot path on one MI355X.
 
-Default workload ("cfg5"): Qwen3-30B-A3B-like KV, 48 layers,
+Headline workload ("cfg5"): Qwen3-30B-A3B-like KV, 48 layers,
 4 KV heads, head_dim 128, 32 query heads (GQA 8:1), f16 storage, block 16, 128 sequences
 at 8192 context (~103 GB of KV resident).  Block tables come from the library's pool
 manager after seeded alloc/free churn (fragmented).  The pool is filled by bulk
 prefill-appends of 512 tokens x all sequences x all layers per call (the timed append leg).
 
 One step = one decode step: one append per sequence on every layer (its newest position)
-plus paged decode attention of every query head over the whole context on every layer;
-value = tokens/s = sequences / step time.  Inputs are resident in HBM before the timed
-region.  Also reported: block-table gather and batched block copy GB/s, and the CPU
-baseline: the oracle's restatement of the reference CPU path (gather + `attend`, OpenMP
-over heads) on a sample of (sequence, layer) items, scaled to a whole step.
-
---config cfg2 / cfg3 run the Llama-3-8B-like batched decode (contexts U[256, 4096]) and the
-q8_0 configuration (64 x 2048, 1 % x8 outliers) the same way.
+plus paged decode attention of every query head over the whole context on every layer,
+as one attention launch over all (sequence, layer) items; value = tokens/s = sequences /
+step time.  Inputs are resident in HBM before the timed region.  Also timed:
+  * the same step in model order: per layer, append + attention over that layer's 128
+    items (layer l+1's query depends on layer l), 48 launch pairs per step;
+  * block-table gather, batched block copy, paged prefill attention and the prelude;
+  * the CPU baseline: the oracle's restatement of the reference CPU path (gather +
+    `attend`, OpenMP over heads) on 8 seeded (sequence, layer) items of the timed step,
+    whose K/V are read back raw from the pool; the same leg checks the timed GPU output
+    of those items against it (the line carries "validated").
+Then the other BASELINE.json configurations run in the same process (keys under
+"configs"): cfg1 (latency loop), cfg2 (batched decode, ragged contexts), cfg3 (q8_0),
+cfg4 (prefix sharing: copy-on-write, LRU eviction, compaction on 64 KiB blocks).
+`--config cfgN` makes another configuration the headline; `--only` skips the others.
 """
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -40,7 +47,12 @@ CONFIGS = {
     "cfg3": dict(layers=32, kv_heads=8, head_dim=128, q_heads=32, seqs=64, ctx=2048,
                  dtype="q8_0", outliers=0.01,
                  name="cfg3 (q8_0 KV, 64 seqs x 2048, 1% x8 outliers)"),
+    "cfg4": dict(layers=32, kv_heads=8, head_dim=128, seqs=64, prefix=2047, divergent=256,
+                 dtype="f16", name="cfg4 (prefix sharing: 64 seqs on a 2047-token prefix)"),
+    "cfg1": dict(layers=16, kv_heads=8, head_dim=64, q_heads=32, prefill=512, decode=128,
+                 dtype="f16", name="cfg1 (small Llama-like KV, one sequence)"),
 }
+DECODE_CONFIGS = ("cfg5", "cfg2", "cfg3")
 
 
 def parse():
@@ -48,37 +60,61 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="cfg5", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="cfg5", choices=DECODE_CONFIGS)
+    ap.add_argument("--only", action="store_true", help="skip the other configurations")
     ap.add_argument("--seqs", type=int, default=None, help="override the config's sequences")
     ap.add_argument("--ctx", type=int, default=None, help="override the config's context")
     ap.add_argument("--layers", type=int, default=None, help="override the config's layers")
     ap.add_argument("--seed", type=int, default=2026)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--legs", default="append,decode,gather,copy,prefill,prelude")
+    ap.add_argument("--legs", default="append,decode,layers,gather,copy,prefill,prelude")
     return ap.parse_args()
 
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); this build has no "
-              "multi-GPU path (the paged KV path shards by sequence with no exchange).",
-              file=sys.stderr)
-        sys.exit(2)
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Timer:
+    """HIP events on the stream the timed kernels run on (torch's current stream, which
+    the bindings launch on)."""
+
+    def __init__(self, torch, stream):
+        self.torch, self.stream = torch, stream
+
+    def __call__(self, fn, reps):
+        ev = self.torch.cuda.Event
+        e0, e1 = ev(enable_timing=True), ev(enable_timing=True)
+        e0.record(self.stream)
+        for _ in range(reps):
+            fn()
+        e1.record(self.stream)
+        self.torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+
+def cu32(torch, a):
+    import numpy as np
+
+    return torch.from_numpy(np.ascontiguousarray(a, np.uint32).view(np.int32)).cuda()
+
+
+# --------------------------------------------------------------------------------------
+# decode configurations (cfg5 headline, cfg2, cfg3)
+# --------------------------------------------------------------------------------------
+
+def run_decode(name, args, dev, legs, steps, warmup, cpu):
     import numpy as np
     import torch
 
-    from qubivex_amd import HipDevice, KvLayout, KvPool
+    from qubivex_amd import KvLayout, KvPool
 
-    assert torch.cuda.is_available(), "bench.py needs the GPU"
-    torch.cuda.init()
-    cfg = dict(CONFIGS[args.config])
-    for key in ("seqs", "ctx", "layers"):
-        if getattr(args, key) is not None:
-            cfg[key] = getattr(args, key)
-    dev = HipDevice(0)
-    legs = set(args.legs.split(","))
+    cfg = dict(CONFIGS[name])
+    if name == args.config:
+        for key in ("seqs", "ctx", "layers"):
+            if getattr(args, key) is not None:
+                cfg[key] = getattr(args, key)
     S, NL = cfg["seqs"], cfg["layers"]
     G, D, H, B = cfg["kv_heads"], cfg["head_dim"], cfg["q_heads"], 16
     dtype = cfg["dtype"]
@@ -92,17 +128,15 @@ def main():
         ctx = np.full(S, cfg["ctx"])
     real_blocks = int(sum((int(c) + B - 1) // B for c in ctx)) * NL
     n_blocks = int(real_blocks * 1.25) + 1024
-    log = lambda *a: print(*a, file=sys.stderr, flush=True)  # noqa: E731
-    log(f"[bench] {dev.describe()}; {cfg['name']}; pool {n_blocks} blocks x {L.block_bytes} B = "
+    log(f"[bench] {cfg['name']}; pool {n_blocks} blocks x {L.block_bytes} B = "
         f"{n_blocks * L.block_bytes / 1e9:.1f} GB")
     pool = KvPool(dev, L, n_blocks, NL)
     mem = pool.memory
-
-    def cu32(a):
-        return torch.from_numpy(np.ascontiguousarray(a, np.uint32).view(np.int32)).cuda()
+    stream = torch.cuda.current_stream()
+    timer = Timer(torch, stream)
+    c32 = lambda a: cu32(torch, a)  # noqa: E731
 
     # ---- seeded churn: scatter the free list before the real sequences allocate
-    t0 = time.time()
     dummies, used = [], 0
     while used < int(n_blocks * 0.2):
         s = pool.create()
@@ -115,33 +149,28 @@ def main():
         pool.release(dummies[i])
     keep = [dummies[i] for i in order[len(order) // 2:]]
     seqs = [pool.create() for _ in range(S)]
-    log(f"[bench] churn: {len(dummies)} sequences, half released ({time.time() - t0:.1f}s)")
 
     # ---- fill: bulk prefill-append of up to CHUNK tokens per sequence, all layers per call
     CHUNK = 512
     gen = torch.Generator(device="cuda").manual_seed(args.seed)
-    stream = torch.cuda.current_stream()
     append_ms, append_bytes = [], []
     fill_to = ctx - 1  # the decode step writes each sequence's position ctx-1
     filled = np.zeros(S, np.int64)
+    t0 = time.time()
     while (filled < fill_to).any():
         counts = np.minimum(CHUNK, fill_to - filled).astype(np.uint32)
         slots = np.concatenate([pool.plan_append(seqs, counts, l) for l in range(NL)])
         n_rows = slots.size
-        sl = cu32(slots)
+        sl = c32(slots)
         k = torch.randn((n_rows, kv_out), generator=gen, device="cuda", dtype=torch.float32)
         v = torch.randn((n_rows, kv_out), generator=gen, device="cuda", dtype=torch.float32)
         if cfg["outliers"]:
             for x in (k, v):
                 x[torch.rand(x.shape, generator=gen, device="cuda") < cfg["outliers"]] *= 8.0
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        dev.append(L, mem, n_blocks, k, v, sl)
-        e1.record(stream)
-        torch.cuda.synchronize()
+        ms = timer(lambda: dev.append(L, mem, n_blocks, k, v, sl), 1)
         dev.check()
         if (counts == CHUNK).all():
-            append_ms.append(e0.elapsed_time(e1))
+            append_ms.append(ms)
             append_bytes.append(n_rows * kv_out * (4 * 2 + 2 * bytes_per_value) + n_rows * 4)
         filled += counts
         del k, v, sl
@@ -159,7 +188,7 @@ def main():
     items = pos.size
     assert items == S * NL and np.array_equal(pos, np.tile(ctx - 1, NL))
     frag = float(np.mean(np.diff(blocks.astype(np.int64)) != 1))
-    d_slots, d_blocks, d_tat, d_pos = cu32(slots), cu32(blocks), cu32(table_at), cu32(pos)
+    d_slots, d_blocks, d_tat, d_pos = c32(slots), c32(blocks), c32(table_at), c32(pos)
     kn = torch.randn((items, kv_out), generator=gen, device="cuda")
     vn = torch.randn((items, kv_out), generator=gen, device="cuda")
     q = torch.randn((items, H, D), generator=gen, device="cuda")
@@ -182,29 +211,73 @@ def main():
         if ev is not None:
             ev[1].record(stream)
 
-    result = {}
+    res = {}
     if "decode" in legs:
-        for _ in range(args.warmup):
+        for _ in range(warmup):
             step()
         torch.cuda.synchronize()
         dev.check()
         evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-               for _ in range(args.steps)]
+               for _ in range(steps)]
         torch.cuda.synchronize()
         t_start = time.perf_counter()
-        for i in range(args.steps):
+        for i in range(steps):
             step(evs[i])
         torch.cuda.synchronize()
         wall = time.perf_counter() - t_start
         dev.check()
         attn_ms = float(np.mean([a.elapsed_time(b) for a, b in evs]))
-        ms_step = wall * 1e3 / args.steps
-        result.update(ms_per_step=ms_step, tokens_per_s=S / (ms_step / 1e3), attn_ms=attn_ms,
-                      attn_gbs=attn_bytes / (attn_ms / 1e3) / 1e9,
-                      attn_tflops=flops / (attn_ms / 1e3) / 1e12,
-                      attn_mfma_tflops=mfma_flops / (attn_ms / 1e3) / 1e12)
-        log(f"[bench] decode step {ms_step:.3f} ms ({S / (ms_step / 1e3):.0f} tok/s); attention "
-            f"{attn_ms:.3f} ms = {result['attn_gbs']:.0f} GB/s")
+        ms_step = wall * 1e3 / steps
+        res.update(ms_per_step=ms_step, tokens_per_s=S / (ms_step / 1e3), attn_ms=attn_ms,
+                   attn_gbs=attn_bytes / (attn_ms / 1e3) / 1e9,
+                   attn_tflops=flops / (attn_ms / 1e3) / 1e12,
+                   attn_mfma_tflops=mfma_flops / (attn_ms / 1e3) / 1e12)
+        log(f"[bench] {name} decode step {ms_step:.3f} ms ({S / (ms_step / 1e3):.0f} tok/s); "
+            f"attention {attn_ms:.3f} ms = {res['attn_gbs']:.0f} GB/s")
+
+    if cpu and "decode" in legs:
+        # Read back the timed step's output before the other legs reuse `out`.
+        sample = np.sort(np.random.default_rng(args.seed + 7).choice(items, 8, replace=False))
+        got = out[torch.from_numpy(sample).cuda()].cpu().numpy()
+
+    if "layers" in legs:
+        # Model order: layer l's append and attention over its S items, layer after layer
+        # (items of layer l are rows l*S .. l*S+S-1 of every array above).
+        per_layer = []
+        for l in range(NL):
+            a, b = l * S, (l + 1) * S
+            per_layer.append((kn[a:b], vn[a:b], d_slots[a:b], q[a:b], d_tat[a:b], d_pos[a:b],
+                              out[a:b]))
+        lay_ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(NL)]
+
+        def layer_step(timed=False):
+            for l, (k_, v_, s_, q_, t_, p_, o_) in enumerate(per_layer):
+                dev.append(L, mem, n_blocks, k_, v_, s_)
+                if timed:
+                    lay_ev[l][0].record(stream)
+                dev.attention(L, mem, n_blocks, q_, d_blocks, t_, p_, H, max_pos, o_)
+                if timed:
+                    lay_ev[l][1].record(stream)
+
+        for _ in range(warmup):
+            layer_step()
+        torch.cuda.synchronize()
+        dev.check()
+        t_start = time.perf_counter()
+        for _ in range(steps):
+            layer_step()
+        torch.cuda.synchronize()
+        lwall = (time.perf_counter() - t_start) * 1e3 / steps
+        layer_step(timed=True)
+        torch.cuda.synchronize()
+        dev.check()
+        la_ms = float(sum(a.elapsed_time(b) for a, b in lay_ev))
+        res.update(layers_ms_per_step=lwall, layers_tokens_per_s=S / (lwall / 1e3),
+                   layers_attn_ms=la_ms, layers_attn_gbs=attn_bytes / (la_ms / 1e3) / 1e9)
+        log(f"[bench] {name} decode in model order ({NL} x append+attention over {S} items): "
+            f"{lwall:.3f} ms/step ({S / (lwall / 1e3):.0f} tok/s); attention {la_ms:.3f} ms = "
+            f"{res['layers_attn_gbs']:.0f} GB/s")
 
     if "gather" in legs:
         # Gather up to 8 layers' items (all positions) into contiguous [G][n][d] per item.
@@ -217,25 +290,19 @@ def main():
         ok = torch.empty(tot * kv_out, dtype=gdt, device="cuda")
         ov = torch.empty_like(ok)
         nt = int(table_at[gi]) if gi < items else blocks.size
-        d_gb, d_gl = cu32(blocks[:nt]), cu32(lens)
+        d_gb, d_gl = c32(blocks[:nt]), c32(lens)
         d_go = torch.from_numpy(out_at.view(np.int64)).cuda()
         od = "f16" if dtype == "f16" else "f32"
-        for _ in range(2):
-            dev.gather(L, mem, n_blocks, d_gb, d_tat[:gi], d_gl, d_go, int(lens.max()), ok, ov, od)
-        torch.cuda.synchronize()
-        reps = 5
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(reps):
-            dev.gather(L, mem, n_blocks, d_gb, d_tat[:gi], d_gl, d_go, int(lens.max()), ok, ov, od)
-        e1.record(stream)
-        torch.cuda.synchronize()
+        g = lambda: dev.gather(L, mem, n_blocks, d_gb, d_tat[:gi], d_gl, d_go,  # noqa: E731
+                               int(lens.max()), ok, ov, od)
+        timer(g, 2)
+        g_ms = timer(g, 5)
         dev.check()
-        g_ms = e0.elapsed_time(e1) / reps
         g_bytes = (tot * kv_out * 2 * bytes_per_value + 2 * ok.numel() * ok.element_size()
                    + nt * 4 + gi * 16)
-        result.update(gather_ms=g_ms, gather_gbs=g_bytes / (g_ms / 1e3) / 1e9)
-        log(f"[bench] gather {NGL} layers ({od} out): {g_ms:.3f} ms = {result['gather_gbs']:.0f} GB/s")
+        res.update(gather_ms=g_ms, gather_gbs=g_bytes / (g_ms / 1e3) / 1e9)
+        log(f"[bench] {name} gather {NGL} layers ({od} out): {g_ms:.3f} ms = "
+            f"{res['gather_gbs']:.0f} GB/s")
         del ok, ov
 
     if "copy" in legs:
@@ -245,22 +312,14 @@ def main():
         live = np.zeros(n_blocks, bool)
         live[blocks] = True
         dst = np.nonzero(~live)[0][:ncp].astype(np.uint32)
-        d_src, d_dst = cu32(src), cu32(dst)
-        for _ in range(2):
-            dev.block_copy(L, mem, n_blocks, d_src, d_dst)
-        reps = 5
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        e0.record(stream)
-        for _ in range(reps):
-            dev.block_copy(L, mem, n_blocks, d_src, d_dst)
-        e1.record(stream)
-        torch.cuda.synchronize()
+        d_src, d_dst = c32(src), c32(dst)
+        cp = lambda: dev.block_copy(L, mem, n_blocks, d_src, d_dst)  # noqa: E731
+        timer(cp, 2)
+        c_ms = timer(cp, 5)
         dev.check()
-        c_ms = e0.elapsed_time(e1) / reps
         c_bytes = 2.0 * ncp * L.block_bytes + ncp * 8
-        result.update(copy_ms=c_ms, copy_gbs=c_bytes / (c_ms / 1e3) / 1e9)
-        log(f"[bench] block copy {ncp} blocks: {c_ms:.3f} ms = {result['copy_gbs']:.0f} GB/s")
+        res.update(copy_ms=c_ms, copy_gbs=c_bytes / (c_ms / 1e3) / 1e9)
+        log(f"[bench] {name} block copy {ncp} blocks: {c_ms:.3f} ms = {res['copy_gbs']:.0f} GB/s")
 
     if "prefill" in legs:
         # Paged prefill attention: a chunk of PF tokens at the end of every sequence's
@@ -272,21 +331,14 @@ def main():
         q_at = (np.arange(S, dtype=np.uint32) * PF).astype(np.uint32)
         qp = torch.randn((S * PF, H, D), generator=gen, device="cuda")
         op = torch.empty_like(qp)
-        d_pb, d_pt, d_pp, d_qa, d_nt = cu32(b0), cu32(t0_), cu32(seg_pos0), cu32(q_at), cu32(n_tok)
+        d_pb, d_pt, d_pp, d_qa, d_nt = c32(b0), c32(t0_), c32(seg_pos0), c32(q_at), c32(n_tok)
         pmax = int(seg_pos0.max()) + PF - 1
-        for _ in range(2):
-            dev.prefill_attention(L, mem, n_blocks, qp, d_pb, d_pt, d_pp, d_qa, d_nt, H, pmax, PF, op)
-        torch.cuda.synchronize()
+        pf = lambda: dev.prefill_attention(L, mem, n_blocks, qp, d_pb, d_pt, d_pp,  # noqa: E731
+                                           d_qa, d_nt, H, pmax, PF, op)
+        timer(pf, 2)
         dev.check()
-        reps = 5
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(reps):
-            dev.prefill_attention(L, mem, n_blocks, qp, d_pb, d_pt, d_pp, d_qa, d_nt, H, pmax, PF, op)
-        e1.record(stream)
-        torch.cuda.synchronize()
+        p_ms = timer(pf, 5)
         dev.check()
-        p_ms = e0.elapsed_time(e1) / reps
         seen = float(np.sum([PF * (int(p) + 1) + PF * (PF - 1) / 2 for p in seg_pos0]))
         p_flops = 4.0 * H * D * seen
         # MFMA work the f16 prefill kernel issues: per wave (16 query rows) and 32-position
@@ -298,12 +350,12 @@ def main():
         last_tok = np.minimum(PF - 1, (w_first + 15) // GS)
         tiles = sum(float(np.sum((int(p0) + last_tok + 1 + 31) // 32)) for p0 in seg_pos0) * G
         p_mfma = tiles * (4 * (D // 32) + 2 * (D // 16)) * 16384.0
-        result.update(prefill_ms=p_ms, prefill_tok_s=S * PF / (p_ms / 1e3),
-                      prefill_tflops=p_flops / (p_ms / 1e3) / 1e12)
+        res.update(prefill_ms=p_ms, prefill_tok_s=S * PF / (p_ms / 1e3),
+                   prefill_tflops=p_flops / (p_ms / 1e3) / 1e12)
         if dtype == "f16" and D in (64, 128):  # the LDS-staged 16x16x32 kernel
-            result.update(prefill_mfma_tflops=p_mfma / (p_ms / 1e3) / 1e12)
-        log(f"[bench] prefill {S} x {PF} tokens (1 layer, ctx {int(ctx.min())}..{int(ctx.max())}): "
-            f"{p_ms:.3f} ms = {result['prefill_tok_s']:.0f} tok/s, {result['prefill_tflops']:.1f} TFLOP/s")
+            res.update(prefill_mfma_tflops=p_mfma / (p_ms / 1e3) / 1e12)
+        log(f"[bench] {name} prefill {S} x {PF} tokens (1 layer): {p_ms:.3f} ms = "
+            f"{res['prefill_tok_s']:.0f} tok/s, {res['prefill_tflops']:.1f} TFLOP/s")
         del qp, op
 
     if "prelude" in legs:
@@ -321,99 +373,407 @@ def main():
         kb, vb = (torch.randn(kv_out, generator=gen, device="cuda") for _ in range(2))
         wn = D if norm == "per_head" else None
         qn = torch.rand(wn, generator=gen, device="cuda") + 0.5 if wn else None
-        kn = torch.rand(wn, generator=gen, device="cuda") + 0.5 if wn else None
-
-        def pre():
-            dev.prelude(L, H, xq, xk, xv, rope, norm=norm, q_bias=qb, k_bias=kb, v_bias=vb,
-                        q_norm=qn, k_norm=kn)
-        for _ in range(2):
-            pre()
-        torch.cuda.synchronize()
-        reps = 5
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(reps):
-            pre()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        r_ms = e0.elapsed_time(e1) / reps
+        knw = torch.rand(wn, generator=gen, device="cuda") + 0.5 if wn else None
+        pre = lambda: dev.prelude(L, H, xq, xk, xv, rope, norm=norm, q_bias=qb,  # noqa: E731
+                                  k_bias=kb, v_bias=vb, q_norm=qn, k_norm=knw)
+        timer(pre, 2)
+        r_ms = timer(pre, 5)
         r_bytes = PT * (H + 2 * G) * D * 4 * 2 + PT * D * 4
-        result.update(prelude_ms=r_ms, prelude_gbs=r_bytes / (r_ms / 1e3) / 1e9)
-        log(f"[bench] prelude {PT} tokens ({norm} QK norm): {r_ms:.3f} ms = "
-            f"{result['prelude_gbs']:.0f} GB/s")
+        res.update(prelude_ms=r_ms, prelude_gbs=r_bytes / (r_ms / 1e3) / 1e9)
+        log(f"[bench] {name} prelude {PT} tokens ({norm} QK norm): {r_ms:.3f} ms = "
+            f"{res['prelude_gbs']:.0f} GB/s")
         del xq, xk, xv, rope
 
     if append_ms:
         a_ms = float(np.mean(append_ms))
         a_gbs = float(np.mean(append_bytes)) / (a_ms / 1e3) / 1e9
-        result.update(append_ms=a_ms, append_gbs=a_gbs)
-        log(f"[bench] bulk append ({CHUNK} tok x {S} seqs x {NL} layers): {a_ms:.3f} ms = {a_gbs:.0f} GB/s")
+        res.update(append_ms=a_ms, append_gbs=a_gbs)
+        log(f"[bench] {name} bulk append ({CHUNK} tok x {S} seqs x {NL} layers): {a_ms:.3f} ms "
+            f"= {a_gbs:.0f} GB/s")
 
-    cpu = None
-    if not args.no_cpu and "decode" in legs:
-        cpu = cpu_baseline(args, dtype, G, D, H, B, int(ctx.max()), positions, S,
-                           result["ms_per_step"], log)
+    baseline = None
+    if cpu and "decode" in legs:
+        baseline = cpu_baseline(args, dev, pool, L, H, blocks, table_at, pos, sample, got,
+                                q[torch.from_numpy(sample).cuda()].cpu().numpy(), positions, S,
+                                res["ms_per_step"])
 
-    stats = pool.stats()
+    info = dict(cfg=cfg, S=S, NL=NL, G=G, D=D, H=H, B=B, dtype=dtype, ctx=ctx, frag=frag,
+                n_blocks=n_blocks, block_bytes=L.block_bytes, attn_bytes=attn_bytes,
+                stats=pool.stats(), cpu=baseline)
+    del kn, vn, q, out
+    pool.close()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return res, info
+
+
+def cpu_baseline(args, dev, pool, L, H, blocks, table_at, pos, sample, got, q, positions_per_step,
+                 S, gpu_ms):
+    """The reference CPU path restated (oracle, test infrastructure used only as the
+    checker and the CPU baseline here): gather through the block table + `attend` per
+    (item, head), OpenMP over heads.  Runs on 8 seeded (sequence, layer) items of the
+    timed step: their K/V are read back raw from the pool blocks (no GPU kernel involved)
+    and decoded from the f16 layout; the GPU's timed output of those items must match
+    within the attention tolerance.  Timed for ~cpu_seconds and scaled by positions to one
+    whole step."""
+    import numpy as np
+
+    import oracle
+
+    G, D, B = L.kv_heads, L.head_dim, L.block
+    if L.dtype != "f16":
+        return None
+    nproc = int(subprocess.run(["nproc"], capture_output=True, text=True).stdout.strip() or 1)
+    threads = int(os.environ.get("QVKV_CPU_THREADS", nproc))
+    buf = pool.buffer
+    bb = L.block_bytes
+    ks, vs, lens = [], [], []
+    for t in sample:
+        n = int(pos[t]) + 1
+        ids = blocks[int(table_at[t]):int(table_at[t]) + (n + B - 1) // B]
+        raw = np.frombuffer(b"".join(dev.read(buf, int(b) * bb, bb) for b in ids), np.uint16)
+        raw = raw.reshape(len(ids), 2, G, B, D)  # per block: K [G][B][d] | V [G][B][d]
+        for arr, dst in ((raw[:, 0], ks), (raw[:, 1], vs)):
+            rows = arr.transpose(0, 2, 1, 3).reshape(len(ids) * B, G * D)[:n]
+            dst.append(rows.view(np.float16).astype(np.float32))
+        lens.append(n)
+    n_items = len(sample)
+    bpl = [(n + B - 1) // B for n in lens]
+    nb = int(sum(bpl))
+    sim = oracle.SimPool(nb, G, D, B, oracle.F16)
+    c_blocks = np.arange(nb, dtype=np.uint32)
+    c_tat = np.concatenate([[0], np.cumsum(bpl)[:-1]]).astype(np.uint32)
+    c_pos = (np.array(lens) - 1).astype(np.uint32)
+    for t in range(n_items):
+        p = np.arange(lens[t])
+        slots = (c_blocks[c_tat[t] + p // B].astype(np.int64) * B + p % B).astype(np.uint32)
+        sim.store(ks[t], vs[t], slots, threads=threads)
+    done, positions, t0 = 0, 0, time.perf_counter()
+    while True:
+        want = sim.attention(q, H, c_blocks, c_tat, c_pos, threads=threads)
+        done += n_items
+        positions += int(np.sum(c_pos.astype(np.int64) + 1))
+        if time.perf_counter() - t0 >= args.cpu_seconds:
+            break
+    per_position = (time.perf_counter() - t0) / positions
+    step_s = per_position * positions_per_step
+    tok_s = S / step_s
+    diff = got.astype(np.float64) - want
+    max_abs = float(np.max(np.abs(diff)))
+    rel = float(np.linalg.norm(diff) / np.linalg.norm(want))
+    ok = bool(max_abs <= 2e-3 and rel <= 1e-3 and np.isfinite(got).all())
+    log(f"[bench] CPU baseline: {per_position * 8192 * 1e3:.1f} ms per 8192 positions on "
+        f"{threads} threads -> {step_s:.1f} s per step, {tok_s:.3f} tok/s "
+        f"(GPU/CPU {step_s * 1e3 / gpu_ms:.0f}x); timed output of items {sample.tolist()} vs "
+        f"the CPU path: max-abs {max_abs:.2e}, rel-L2 {rel:.2e} -> {'ok' if ok else 'MISMATCH'}")
+    return {"value": round(tok_s, 4), "unit": "tokens/s", "cores": threads, "nproc": nproc,
+            "kind": "port",
+            "sample": f"{done} (sequence, layer) item-attentions of gather + attend over "
+                      f"{int(c_pos.max()) + 1} positions: 8 seeded items of the timed step "
+                      f"(K/V read back raw from their fragmented pool blocks), {H} heads each, "
+                      f"scaled by positions to one step ({int(positions_per_step)} positions); "
+                      "oracle restatement of SimDevice::attention + math::attend",
+            "validation": {"items": sample.tolist(), "max_abs": max_abs, "rel_l2": rel,
+                           "tolerance": [2e-3, 1e-3], "ok": ok}}
+
+
+# --------------------------------------------------------------------------------------
+# cfg4: prefix sharing, copy-on-write, LRU eviction, compaction
+# --------------------------------------------------------------------------------------
+
+def run_cfg4(args, dev):
+    import numpy as np
+    import torch
+
+    from qubivex_amd import KvLayout, KvPool
+
+    cfg = CONFIGS["cfg4"]
+    NL, G, D, S = cfg["layers"], cfg["kv_heads"], cfg["head_dim"], cfg["seqs"]
+    PREFIX, DIV, B = cfg["prefix"], cfg["divergent"], 16
+    L = KvLayout("f16", G, D, B)
+    bb = L.block_bytes
+    need = NL * ((PREFIX + B - 1) // B + S * ((PREFIX % B + DIV + B - 1) // B))
+    N = int(need * 1.25) + 64
+    pool = KvPool(dev, L, N, NL)
+    mem = pool.memory
+    stream = torch.cuda.current_stream()
+    timer = Timer(torch, stream)
+    gen = torch.Generator(device="cuda").manual_seed(args.seed + 4)
+    r = np.random.default_rng(args.seed + 4)
+    dev.gather_host(L, pool.buffer, [0], [0], [16], [0], 1 << 14)  # grow the staging once
+    parent = pool.create()
+    for l in range(NL):
+        sl = cu32(torch, pool.plan_append([parent], [PREFIX], l))
+        k = torch.randn((PREFIX, G * D), generator=gen, device="cuda")
+        dev.append(L, mem, N, k, torch.randn_like(k), sl)
+    kids = [pool.fork(parent, PREFIX) for _ in range(S)]
+    # Divergent appends: the first write of each child into the shared partial block
+    # copies it (64 copies of a 64 KiB block per layer, one launch each, ordered after the
+    # appends above).  GPU time of those copy launches from the library's own events.
+    cow_ns, app_ms, app_rows = 0, 0.0, 0
+    for l in range(NL):
+        before = dev.transfers()["gpu_ns"]
+        slots = pool.plan_append(kids, [DIV] * S, l)
+        cow_ns += dev.transfers()["gpu_ns"] - before
+        sl = cu32(torch, slots)
+        k = torch.randn((slots.size, G * D), generator=gen, device="cuda")
+        v = torch.randn_like(k)
+        app_ms += timer(lambda: dev.append(L, mem, N, k, v, sl), 1)
+        app_rows += slots.size
+    dev.check()
+    st = pool.stats()
+    cow = st["cow_copies"]
+    assert cow == S * NL, st
+    # The same copy-on-write batch as one launch (all layers' pairs at once): what a
+    # runtime that plans every layer of a step together would issue.
+    free = np.zeros(N, bool)
+    refs = np.array([pool.refcount(b) for b in range(N)])
+    free[refs == 0] = True
+    shared = np.nonzero(refs > 1)[0][: S * NL].astype(np.uint32)
+    dst = np.nonzero(free)[0][: shared.size].astype(np.uint32)
+    d_s, d_d = cu32(torch, shared), cu32(torch, dst)
+    bc = lambda: dev.block_copy(L, mem, N, d_s, d_d)  # noqa: E731
+    timer(bc, 2)
+    bat_ms = timer(bc, 5)
+    dev.check()
+    # LRU eviction of 25 % of the blocks in use, then compaction under a seeded remap.
+    for i in r.permutation(S):
+        pool.touch(kids[int(i)])
+    used = N - pool.stats()["free"]
+    t0 = time.perf_counter()
+    released = pool.evict_lru(used // 4)
+    evict_s = time.perf_counter() - t0
+    comp = {}
+    for mode in ("fill", "permute"):
+        # "fill": the blocks past the live count into the vacant ids below it (one batch);
+        # "permute": every live block under a seeded permutation (dependent batches).
+        before = dev.transfers()["gpu_ns"]
+        t0 = time.perf_counter()
+        moved = pool.compact(seed=args.seed + 44, mode=mode)
+        wall = time.perf_counter() - t0
+        ns = dev.transfers()["gpu_ns"] - before
+        comp[mode] = {"moves": int(moved), "gpu_ms": ns / 1e6, "wall_ms": wall * 1e3,
+                      "gbs": 2.0 * moved * bb / ns if ns else None}
+    st = pool.stats()
+    res = {
+        "cow_copies": int(cow), "cow_block_bytes": bb,
+        "cow_per_layer_gbs": 2.0 * cow * bb / cow_ns if cow_ns else None,
+        "cow_per_layer_us": cow_ns / NL / 1e3,
+        "cow_batched_ms": bat_ms, "cow_batched_gbs": 2.0 * shared.size * bb / (bat_ms / 1e3) / 1e9,
+        "divergent_append_gbs": app_rows * G * D * (8 + 4) / (app_ms / 1e3) / 1e9,
+        "evicted_seqs": len(released), "evicted_blocks": int(st["evicted_blocks"]),
+        "evict_host_ms": evict_s * 1e3,
+        "compaction_moves": comp["fill"]["moves"], "compaction_gpu_ms": comp["fill"]["gpu_ms"],
+        "compaction_gbs": comp["fill"]["gbs"], "compaction_wall_ms": comp["fill"]["wall_ms"],
+        "compaction_frac": (comp["fill"]["gbs"] or 0) / PEAK_HBM_GBS,
+        "compaction_permute": comp["permute"],
+    }
+    log(f"[bench] cfg4: {cow} COW copies of {bb // 1024} KiB: {res['cow_per_layer_us']:.1f} us per "
+        f"layer launch ({res['cow_per_layer_gbs']:.0f} GB/s), batched {bat_ms:.3f} ms = "
+        f"{res['cow_batched_gbs']:.0f} GB/s; evicted {res['evicted_blocks']} blocks; compaction "
+        f"(fill) {comp['fill']['moves']} moves in {comp['fill']['gpu_ms']:.3f} ms GPU = "
+        f"{comp['fill']['gbs']:.0f} GB/s ({comp['fill']['wall_ms']:.0f} ms wall); (permute) "
+        f"{comp['permute']['moves']} moves in {comp['permute']['gpu_ms']:.3f} ms = "
+        f"{comp['permute']['gbs']:.0f} GB/s")
+    pool.close()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return res
+
+
+# --------------------------------------------------------------------------------------
+# cfg1: one sequence, latency-bound
+# --------------------------------------------------------------------------------------
+
+def run_cfg1(args, dev):
+    import numpy as np
+    import torch
+
+    from qubivex_amd import KvLayout, KvPool
+
+    cfg = CONFIGS["cfg1"]
+    NL, G, D, H, B = cfg["layers"], cfg["kv_heads"], cfg["head_dim"], cfg["q_heads"], 16
+    P, T = cfg["prefill"], cfg["decode"]
+    L = KvLayout("f16", G, D, B)
+    N = NL * ((P + T) // B + 1) + 64
+    pool = KvPool(dev, L, N, NL)
+    mem = pool.memory
+    gen = torch.Generator(device="cuda").manual_seed(args.seed + 1)
+    s = pool.create()
+    stream = torch.cuda.current_stream()
+    c32 = lambda a: cu32(torch, a)  # noqa: E731
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    sl = c32(np.concatenate([pool.plan_append([s], [P], l) for l in range(NL)]))
+    k = torch.randn((NL * P, G * D), generator=gen, device="cuda")
+    dev.append(L, mem, N, k, torch.randn_like(k), sl)
+    torch.cuda.synchronize()
+    prefill_ms = (time.perf_counter() - t0) * 1e3
+    q = torch.randn((NL, H, D), generator=gen, device="cuda")
+    out = torch.empty_like(q)
+    kn = torch.randn((NL, G * D), generator=gen, device="cuda")
+    ok = torch.empty(NL * (P + T) * G * D, dtype=torch.float16, device="cuda")
+    ov = torch.empty_like(ok)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for step in range(T):
+        sl = np.concatenate([pool.plan_append([s], [1], l) for l in range(NL)])
+        tabs = [pool.tables([s], l) for l in range(NL)]
+        blocks = np.concatenate([t[0] for t in tabs])
+        tat = np.cumsum([0] + [t[0].size for t in tabs[:-1]]).astype(np.uint32)
+        pos = np.concatenate([t[2] for t in tabs]).astype(np.uint32)
+        n = int(pos[0]) + 1
+        d_b, d_t, d_p = c32(blocks), c32(tat), c32(pos)
+        dev.append(L, mem, N, kn, kn, c32(sl))
+        out_at = torch.from_numpy((np.arange(NL, dtype=np.int64) * n)).cuda()
+        dev.gather(L, mem, N, d_b, d_t, c32(pos + 1), out_at, n, ok, ov, "f16")
+        dev.attention(L, mem, N, q, d_b, d_t, d_p, H, int(pos.max()), out)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3
+    gpu = e0.elapsed_time(e1)
+    dev.check()
+    pool.close()
+    res = {"prefill_append_ms": prefill_ms, "decode_steps": T, "decode_total_ms": wall,
+           "decode_step_us": wall / T * 1e3, "decode_gpu_stream_ms": gpu,
+           "note": "latency-bound: per step 16 layers x (append 1 + gather + attention), host "
+                   "planning included; no roofline claim"}
+    log(f"[bench] cfg1: prefill-append {P} x {NL} layers {prefill_ms:.2f} ms; {T} decode steps "
+        f"(append + gather + attention, all layers) {wall:.1f} ms = {wall / T * 1e3:.0f} us/step")
+    return res
+
+
+# --------------------------------------------------------------------------------------
+
+def roofline_of(config, res, info):
+    if "attn_ms" not in res:
+        return None
+    return {
+        "bound": "hbm",
+        "achieved": round(res["attn_gbs"], 1),
+        "peak": PEAK_HBM_GBS,
+        "unit": "GB/s",
+        "frac": round(res["attn_gbs"] / PEAK_HBM_GBS, 4),
+        "traffic": traffic_from_profile(config, info["attn_bytes"]),
+        "traffic_note": "FETCH_SIZE and WRITE_SIZE per launch from profiles/attention_<cfg>_pmc.json, "
+                        "scaled by the copy-kernel calibration there: an estimate",
+        "kernel": f"k_attn_mfma<{info['D']},{info['dtype']}>",
+        "algorithmic_bytes_per_launch": info["attn_bytes"],
+        "avg_launch_ms": round(res["attn_ms"], 4),
+    }
+
+
+def summary(res, info):
+    keep = ("ms_per_step", "tokens_per_s", "attn_ms", "attn_gbs", "layers_ms_per_step",
+            "layers_tokens_per_s", "layers_attn_gbs", "gather_gbs", "copy_gbs", "append_gbs",
+            "prefill_tflops", "prelude_gbs")
+    out = {k: round(res[k], 4) for k in keep if k in res}
+    for k in ("attn_gbs", "layers_attn_gbs", "gather_gbs", "copy_gbs", "append_gbs"):
+        if k in res:
+            out[k.replace("_gbs", "_frac")] = round(res[k] / PEAK_HBM_GBS, 4)
+    out["workload"] = workload_text(info)
+    return out
+
+
+def workload_text(info):
+    cfg, S, ctx = info["cfg"], info["S"], info["ctx"]
     ctx_desc = (f"{S} seqs x {int(ctx[0])} ctx" if (ctx == ctx[0]).all()
                 else f"{S} seqs x ctx U[{cfg['ctx'][0]},{cfg['ctx'][1]}] (sum {int(ctx.sum())})")
+    return (f"{cfg['name']}: {info['NL']} layers, {info['G']} KV heads, d {info['D']}, "
+            f"{info['H']} q heads (GQA {info['H'] // info['G']}:1), {info['dtype']} KV, block "
+            f"{info['B']}, {ctx_desc}; step = 1 append/seq/layer + paged decode attention over "
+            "all layers")
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); this build has no "
+              "multi-GPU path (the paged KV path shards by sequence with no exchange).",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from qubivex_amd import HipDevice
+
+    assert torch.cuda.is_available(), "bench.py needs the GPU"
+    torch.cuda.init()
+    dev = HipDevice(0)
+    log(f"[bench] {dev.describe()}")
+    legs = set(args.legs.split(","))
+    res, info = run_decode(args.config, args, dev, legs, args.steps, args.warmup,
+                           cpu=not args.no_cpu)
+    others = {}
+    if not args.only:
+        for name in DECODE_CONFIGS:
+            if name == args.config:
+                continue
+            r2, i2 = run_decode(name, args, dev, {"decode", "layers", "gather", "copy"},
+                                max(5, args.steps // 2), 2, cpu=False)
+            others[name] = summary(r2, i2)
+            others[name]["roofline"] = roofline_of(name, r2, i2)
+        others["cfg4"] = run_cfg4(args, dev)
+        others["cfg1"] = run_cfg1(args, dev)
+
+    cpu = info["cpu"]
     line = {
         "metric": "paged decode-attn tokens/s at 128x8k (Qwen3-30B-A3B-like KV); "
                   "KV append/gather HBM GB/s",
-        "value": round(result.get("tokens_per_s", 0.0), 1),
+        "value": round(res.get("tokens_per_s", 0.0), 1),
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(result.get("ms_per_step", 0.0), 4),
+        "ms_per_step": round(res.get("ms_per_step", 0.0), 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": dtype,
+        "dtype": info["dtype"],
         "data": "synthetic N(0,1) K/V/Q from a seeded generator; fragmented block tables",
         "config": {
-            "workload": f"{cfg['name']}: {NL} layers, {G} KV heads, d {D}, {H} q heads "
-                        f"(GQA {H // G}:1), {dtype} KV, block {B}, {ctx_desc}; step = 1 append/"
-                        "seq/layer + paged decode attention over all layers",
-            "seqs": S, "layers": NL, "kv_heads": G, "head_dim": D, "q_heads": H, "block": B,
-            "context_positions_per_layer": int(ctx.sum()), "pool_blocks": n_blocks,
-            "pool_gb": round(n_blocks * L.block_bytes / 1e9, 1),
-            "table_discontinuity": round(frag, 3), "seed": args.seed,
+            "workload": workload_text(info),
+            "seqs": info["S"], "layers": info["NL"], "kv_heads": info["G"],
+            "head_dim": info["D"], "q_heads": info["H"], "block": info["B"],
+            "context_positions_per_layer": int(info["ctx"].sum()),
+            "pool_blocks": info["n_blocks"],
+            "pool_gb": round(info["n_blocks"] * info["block_bytes"] / 1e9, 1),
+            "table_discontinuity": round(info["frag"], 3), "seed": args.seed,
         },
-        "roofline": None,
+        "roofline": roofline_of(args.config, res, info),
         "cpu_baseline": cpu,
-        "legs": {k: round(v, 4) for k, v in result.items()},
-        "pool": {k: stats[k] for k in ("blocks", "free", "layers", "synced_rows")},
+        "validated": (cpu or {}).get("validation", {}).get("ok"),
+        "legs": {k: round(v, 4) for k, v in res.items()},
+        "pool": {k: info["stats"][k] for k in ("blocks", "free", "layers", "synced_rows")},
     }
-    if "attn_ms" in result:
-        line["roofline"] = {
-            "bound": "hbm",
-            "achieved": round(result["attn_gbs"], 1),
-            "peak": PEAK_HBM_GBS,
-            "unit": "GB/s",
-            "frac": round(result["attn_gbs"] / PEAK_HBM_GBS, 4),
-            "traffic": traffic_from_profile(args.config, attn_bytes),
-            "kernel": f"k_attn_mfma<{D},{'q8_0' if dtype == 'q8_0' else 'f16'}>",
-            "algorithmic_bytes_per_launch": attn_bytes,
-            "avg_launch_ms": round(result["attn_ms"], 4),
+    if "attn_ms" in res:
+        line["model_order"] = {
+            "what": "per layer: append + attention over that layer's items, layer after layer",
+            "ms_per_step": round(res.get("layers_ms_per_step", 0.0), 4),
+            "tokens_per_s": round(res.get("layers_tokens_per_s", 0.0), 1),
+            "attention_frac": round(res.get("layers_attn_gbs", 0.0) / PEAK_HBM_GBS, 4),
         }
         line["fraction_of_roofline"] = {
-            "attention": round(result["attn_gbs"] / PEAK_HBM_GBS, 4),
-            "append": round(result.get("append_gbs", 0) / PEAK_HBM_GBS, 4),
-            "gather": round(result.get("gather_gbs", 0) / PEAK_HBM_GBS, 4),
-            "block_copy": round(result.get("copy_gbs", 0) / PEAK_HBM_GBS, 4),
-            "prelude": round(result.get("prelude_gbs", 0) / PEAK_HBM_GBS, 4),
+            "attention": round(res["attn_gbs"] / PEAK_HBM_GBS, 4),
+            "attention_per_layer": round(res.get("layers_attn_gbs", 0) / PEAK_HBM_GBS, 4),
+            "append": round(res.get("append_gbs", 0) / PEAK_HBM_GBS, 4),
+            "gather": round(res.get("gather_gbs", 0) / PEAK_HBM_GBS, 4),
+            "block_copy": round(res.get("copy_gbs", 0) / PEAK_HBM_GBS, 4),
+            "prelude": round(res.get("prelude_gbs", 0) / PEAK_HBM_GBS, 4),
         }
         # MFMA issue rate against the dense f16 peak (2.5 PFLOP/s): decode attention is
         # HBM-bound and uses the matrix cores only for the GQA group contraction.
         line["mfma_utilisation"] = {
             "peak_tflops": PEAK_F16_TFLOPS,
-            "attention": round(result["attn_mfma_tflops"] / PEAK_F16_TFLOPS, 4),
-            "prefill": round(result.get("prefill_mfma_tflops", 0) / PEAK_F16_TFLOPS, 4),
+            "attention": round(res["attn_mfma_tflops"] / PEAK_F16_TFLOPS, 4),
+            "prefill": round(res.get("prefill_mfma_tflops", 0) / PEAK_F16_TFLOPS, 4),
         }
+    if others:
+        line["configs"] = others
     print(json.dumps(line), flush=True)
-    pool.close()
     dev.close()
+    if cpu is not None and not cpu["validation"]["ok"]:
+        sys.exit(1)  # the timed output does not match the CPU path
 
 
 def traffic_from_profile(config, algorithmic):
@@ -428,49 +788,6 @@ def traffic_from_profile(config, algorithmic):
     if abs(p.get("algorithmic_bytes", 0) - algorithmic) > 1e-6 * algorithmic:
         return None
     return p.get("traffic_bytes")
-
-
-def cpu_baseline(args, dtype, G, D, H, B, CTX, positions_per_step, S, gpu_ms, log):
-    """The reference CPU path restated (oracle): gather through the block table + `attend`
-    per (item, head), OpenMP over heads, on a sample of (sequence, layer) items at CTX
-    positions; scaled by positions to one whole step."""
-    import numpy as np
-
-    import oracle
-
-    threads = int(os.environ.get("QVKV_CPU_THREADS", min(16, os.cpu_count() or 1)))
-    n_items = 16
-    r = np.random.default_rng(args.seed + 1)
-    bpl = (CTX + B - 1) // B
-    nb = n_items * bpl
-    sim = oracle.SimPool(nb, G, D, B, oracle.F16 if dtype == "f16" else oracle.Q8_0)
-    blocks = r.permutation(nb).astype(np.uint32)
-    table_at = (np.arange(n_items) * bpl).astype(np.uint32)
-    pos = np.full(n_items, CTX - 1, np.uint32)
-    for t in range(n_items):
-        p = np.arange(CTX)
-        slots = (blocks[table_at[t] + p // B].astype(np.int64) * B + p % B).astype(np.uint32)
-        k = r.standard_normal((CTX, G * D), dtype=np.float32)
-        v = r.standard_normal((CTX, G * D), dtype=np.float32)
-        sim.store(k, v, slots, threads=threads)
-    q = r.standard_normal((n_items, H, D), dtype=np.float32)
-    done, t0 = 0, time.perf_counter()
-    while True:
-        sim.attention(q, H, blocks, table_at, pos, threads=threads)
-        done += n_items
-        if time.perf_counter() - t0 >= args.cpu_seconds:
-            break
-    per_position = (time.perf_counter() - t0) / (done * CTX)
-    step_s = per_position * positions_per_step
-    tok_s = S / step_s
-    log(f"[bench] CPU baseline: {per_position * CTX * 1e3:.1f} ms per {CTX}-position item on "
-        f"{threads} threads -> {step_s:.1f} s per step, {tok_s:.3f} tok/s "
-        f"(GPU/CPU {step_s * 1e3 / gpu_ms:.0f}x)")
-    return {"value": round(tok_s, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{done} (sequence, layer) items of gather + attend over {CTX} positions "
-                      f"({n_items} distinct, {H} heads each), scaled by positions to one step "
-                      f"({int(positions_per_step)} positions); oracle restatement of "
-                      "SimDevice::attention + math::attend"}
 
 
 if __name__ == "__main__":

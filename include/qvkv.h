@@ -371,11 +371,18 @@ int qvkv_pool_tables(const qvkv_pool *pool, const uint32_t *seqs, uint32_t n_seq
  * released handles to released_out (cap entries) and their count. */
 int qvkv_pool_evict_lru(qvkv_pool *pool, uint64_t target_blocks, uint32_t *released_out,
                         uint32_t cap, uint32_t *n_released);
-/* Moves every live block into the ids 0..live-1 in the order of a permutation drawn
- * from `seed` (seed 0: ascending by current id), rewriting every table and the free
- * list, with cycle-safe batches of the block-copy kernel, ordered after `stream` as in
- * qvkv_pool_plan_append.  *moved receives the blocks moved. */
-int qvkv_pool_compact(qvkv_pool *pool, uint64_t seed, uint64_t *moved, void *stream);
+/* Compaction modes. */
+#define QVKV_COMPACT_PERMUTE 0 /* every live block to the position a seeded permutation of
+                                  0..live-1 gives it (seed 0: ascending by current id) */
+#define QVKV_COMPACT_FILL 1    /* live blocks below `live` stay; those above move into the
+                                  vacant ids below `live`, matched in a seeded order: the
+                                  fewest moves, all in one batch */
+/* Moves every live block into the ids 0..live-1 under a remap drawn from `seed` (`mode`:
+ * QVKV_COMPACT_*), rewriting every table and the free list, with cycle-safe batches of
+ * the block-copy kernel, ordered after `stream` as in qvkv_pool_plan_append.  *moved
+ * receives the blocks moved. */
+int qvkv_pool_compact(qvkv_pool *pool, uint32_t mode, uint64_t seed, uint64_t *moved,
+                      void *stream);
 /* Reference count of one block (0 = free). */
 int qvkv_pool_refcount(const qvkv_pool *pool, uint32_t block, uint32_t *out);
 

@@ -63,6 +63,7 @@ class PoolStats(ctypes.Structure):
 
 
 NORM_NONE, NORM_FULL, NORM_PER_HEAD = 0, 1, 2
+COMPACT_PERMUTE, COMPACT_FILL = 0, 1
 
 
 class Prelude(ctypes.Structure):
@@ -145,7 +146,7 @@ SIGNATURES = {
     "qvkv_pool_plan_attention": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _vp, _u64, _P(_u64), _vp,
                                         _vp, _vp, _vp, _vp, _u64, _P(_u64), _vp]),
     "qvkv_pool_evict_lru": (_i32, [_vp, _u64, _vp, _u32, _P(_u32)]),
-    "qvkv_pool_compact": (_i32, [_vp, _u64, _P(_u64), _vp]),
+    "qvkv_pool_compact": (_i32, [_vp, _u32, _u64, _P(_u64), _vp]),
     "qvkv_pool_refcount": (_i32, [_vp, _u32, _P(_u32)]),
     "qvkv_prefix_create": (_i32, [_u64, _P(_vp)]),
     "qvkv_prefix_destroy": (None, [_vp]),

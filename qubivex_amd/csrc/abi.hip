@@ -153,6 +153,12 @@ int ensure(qvkv_dev *dev, hipStream_t s, void **buf, uint64_t *have, uint64_t ne
     return QVKV_OK;
 }
 
+// The attention workspace of a stream grown for a plan (partials of context chunks).
+int ensure_attention(qvkv_dev *dev, StreamState *st, const qvkv::AttnPlan &p) {
+    if (!p.ws_bytes) return QVKV_OK;
+    return ensure(dev, st->stream, &st->ws, &st->ws_bytes, p.ws_bytes);
+}
+
 // The state of `stream`, created on first use.  Caller holds dev->mu.
 int state_locked(qvkv_dev *dev, hipStream_t stream, StreamState **out) {
     for (StreamState *st : dev->streams)
@@ -561,8 +567,7 @@ int qvkv_attention_async(qvkv_dev *dev, const qvkv_layout *layout, const void *p
     std::lock_guard<std::mutex> lk(dev->mu);
     StreamState *st;
     if (int rc = state_locked(dev, (hipStream_t)stream, &st)) return rc;
-    if (p.ws_bytes)
-        if (int rc = ensure(dev, st->stream, &st->ws, &st->ws_bytes, p.ws_bytes)) return rc;
+    if (int rc = ensure_attention(dev, st, p)) return rc;
     return launched(dev, qvkv::launch_attention(g, p, pool, pool_blocks, q, blocks, n_table,
                                                 table_at, pos, n_items, heads, max_pos, out,
                                                 st->ws, st->d_err, st->stream),
@@ -820,8 +825,7 @@ int qvkv_decode_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *po
     }
     std::lock_guard<std::mutex> lk(dev->mu);
     if (int rc = set_device(dev)) return rc;
-    if (p.ws_bytes)
-        if (int rc = ensure(dev, dev->stream, &dev->own->ws, &dev->own->ws_bytes, p.ws_bytes)) return rc;
+    if (int rc = ensure_attention(dev, dev->own, p)) return rc;
     const uint64_t rowb = g.kv_out * 4, qb = (uint64_t)s * heads * g.D * 4;
     Stager st;
     uint64_t sko = st.add(sk.data(), n_sync * rowb), svo = st.add(sv.data(), n_sync * rowb),
@@ -946,8 +950,7 @@ int qvkv_prelude_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *p
     }
     std::lock_guard<std::mutex> lk(dev->mu);
     if (int rc = set_device(dev)) return rc;
-    if (plan.ws_bytes)
-        if (int rc = ensure(dev, dev->stream, &dev->own->ws, &dev->own->ws_bytes, plan.ws_bytes)) return rc;
+    if (int rc = ensure_attention(dev, dev->own, plan)) return rc;
     const uint64_t q_out = (uint64_t)heads * g.D, rowb = g.kv_out * 4, qb = s * q_out * 4;
     const uint64_t nq = p->norm == QVKV_NORM_PER_HEAD ? g.D : q_out;
     const uint64_t nk = p->norm == QVKV_NORM_PER_HEAD ? g.D : g.kv_out;

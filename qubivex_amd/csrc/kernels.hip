@@ -1212,8 +1212,14 @@ int plan_attention(const Geometry &g, uint32_t n_items, uint32_t heads, uint32_t
     const uint64_t units = (uint64_t)n_items * g.G * p->hc;
     const uint64_t max_tiles = ((uint64_t)max_pos + 1 + 15) / 16;
     // workgroups to aim for: 8 per CU keeps all 256 CUs busy
-    const uint64_t target = (uint64_t)tune("QVKV_ATTN_TARGET", 2048);
-    uint64_t nch = units >= target ? 1 : (target + units - 1) / units;
+    // Split the context into chunks only when the launch is too small to fill the chip
+    // with one workgroup per unit (below 2 per CU); then aim for about 6 per CU.
+    // Measured per layer (one launch per layer): the 512 units of 128 x 8k (4 KV heads)
+    // and of cfg3's 64 x 2048 q8_0 (8 KV heads) run best unsplit; cfg2's 256 ragged units
+    // best near 1536 chunks.
+    const uint64_t full = (uint64_t)tune("QVKV_ATTN_FULL", 512);
+    const uint64_t target = (uint64_t)tune("QVKV_ATTN_TARGET", 1536);
+    uint64_t nch = units >= full ? 1 : (target + units - 1) / units;
     const uint64_t cap = (max_tiles + 3) / 4;  // at least one tile per wave
     if (nch > cap) nch = cap;
     if (nch < 1) nch = 1;

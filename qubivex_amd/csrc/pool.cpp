@@ -462,23 +462,43 @@ int qvkv_pool_evict_lru(qvkv_pool *p, uint64_t target_blocks, uint32_t *released
     return QVKV_OK;
 }
 
-int qvkv_pool_compact(qvkv_pool *p, uint64_t seed, uint64_t *moved, void *stream) {
+int qvkv_pool_compact(qvkv_pool *p, uint32_t mode, uint64_t seed, uint64_t *moved,
+                      void *stream) {
     if (!p) return err(QVKV_E_SHAPE, "shape mismatch in pool: null argument");
+    if (mode != QVKV_COMPACT_PERMUTE && mode != QVKV_COMPACT_FILL)
+        return err(QVKV_E_SHAPE, "shape mismatch in pool: no such compaction mode");
     std::lock_guard<std::mutex> lk(p->mu);
     const uint64_t N = p->n_blocks;
     std::vector<uint32_t> live;
     for (uint64_t b = 0; b < N; b++)
         if (p->refs[b]) live.push_back((uint32_t)b);
     const uint64_t K = live.size();
-    // New id of each live block: position j of the (seeded) permutation of 0..K-1.
-    std::vector<uint32_t> perm(K);
-    std::iota(perm.begin(), perm.end(), 0u);
-    if (seed) {
-        uint64_t st = seed;
-        for (uint64_t i = K; i > 1; i--) std::swap(perm[i - 1], perm[splitmix(st) % i]);
-    }
     std::vector<int64_t> newid(N, -1);
-    for (uint64_t j = 0; j < K; j++) newid[live[j]] = perm[j];
+    if (mode == QVKV_COMPACT_PERMUTE) {
+        // New id of each live block: position j of the (seeded) permutation of 0..K-1.
+        std::vector<uint32_t> perm(K);
+        std::iota(perm.begin(), perm.end(), 0u);
+        if (seed) {
+            uint64_t st = seed;
+            for (uint64_t i = K; i > 1; i--) std::swap(perm[i - 1], perm[splitmix(st) % i]);
+        }
+        for (uint64_t j = 0; j < K; j++) newid[live[j]] = perm[j];
+    } else {
+        // Live blocks below K keep their ids; those at K or above take the vacant ids
+        // below K, matched in a seeded order (ascending for seed 0).  Every destination
+        // is vacant, so the moves are one batch.
+        std::vector<uint32_t> holes, movers;
+        for (uint64_t b = 0; b < N; b++) {
+            if (b < K && !p->refs[b]) holes.push_back((uint32_t)b);
+            if (b >= K && p->refs[b]) movers.push_back((uint32_t)b);
+            if (b < K && p->refs[b]) newid[b] = (int64_t)b;
+        }
+        if (seed) {
+            uint64_t st = seed;
+            for (uint64_t i = holes.size(); i > 1; i--) std::swap(holes[i - 1], holes[splitmix(st) % i]);
+        }
+        for (size_t j = 0; j < movers.size(); j++) newid[movers[j]] = holes[j];
+    }
     // Pending moves (src -> dst).  A move runs when its dst is vacant; a batch never
     // reads a block another move of the batch writes.  Cycles are broken through a
     // spare block (a free id >= K).

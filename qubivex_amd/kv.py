@@ -513,9 +513,13 @@ class KvPool:
                                       out.ctypes.data_as(ctypes.c_void_p), cap, ctypes.byref(n)))
         return out[:min(n.value, cap)].tolist()
 
-    def compact(self, seed=0, stream=None):
+    def compact(self, seed=0, mode="permute", stream=None):
+        """Moves the live blocks to the front (qvkv_pool_compact): mode "permute" (a seeded
+        permutation of every live block) or "fill" (blocks past the live count into the
+        vacant ids below it, one batch); returns the blocks moved."""
         moved = ctypes.c_uint64()
-        check(lib.qvkv_pool_compact(self.handle, seed, ctypes.byref(moved),
+        m = {"permute": _lib.COMPACT_PERMUTE, "fill": _lib.COMPACT_FILL}[mode]
+        check(lib.qvkv_pool_compact(self.handle, m, seed, ctypes.byref(moved),
                                     self._copy_stream(stream)))
         return moved.value
 

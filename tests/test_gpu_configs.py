@@ -308,17 +308,19 @@ def test_cfg4_prefix_sharing_cow_eviction_compaction(hip):
     released = pool.evict_lru(used // 4)
     freed = pool.stats()["evicted_blocks"]
     assert freed >= used // 4 and parent not in released
-    moved = pool.compact(seed=4242)
-    assert moved > 0
-    st = pool.stats()
-    live = N - st["free"]
-    for s in survivors_probe:
-        if s in released:
-            continue
-        for l in (0, L // 2, L - 1):
-            k, v = read(s, l)
-            assert torch.equal(k, before[(s, l)][0]) and torch.equal(v, before[(s, l)][1]), (s, l)
-            assert pool.tables([s], l)[0].max() < live
+    # first the fewest moves (one batch into the vacant ids), then a full seeded permutation
+    for mode, seed in (("fill", 4242), ("permute", 4243)):
+        moved = pool.compact(seed=seed, mode=mode)
+        assert moved > 0
+        st = pool.stats()
+        live = N - st["free"]
+        for s in survivors_probe:
+            if s in released:
+                continue
+            for l in (0, L // 2, L - 1):
+                k, v = read(s, l)
+                assert torch.equal(k, before[(s, l)][0]) and torch.equal(v, before[(s, l)][1]), (mode, s, l)
+                assert pool.tables([s], l)[0].max() < live
     print(f"  cfg4: {st['cow_copies']} COW copies, {freed} blocks evicted, {moved} moved", flush=True)
     pool.close()
 

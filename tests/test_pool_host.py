@@ -33,8 +33,8 @@ class Data:
         self.sim = oracle.SimPool(pool.n_blocks, L.kv_heads, L.head_dim, L.block, oracle.F16)
         self.r = np.random.default_rng(99)
 
-    def sync_copies(self):
-        for src, dst in self.pool.take_batches():
+    def sync_copies(self, batches=None):
+        for src, dst in (self.pool.take_batches() if batches is None else batches):
             assert not set(src.tolist()) & set(dst.tolist()), "a batch reads what it writes"
             assert len(set(dst.tolist())) == dst.size, "a batch writes a block twice"
             w = 2 * self.sim.B * self.sim.kv_out
@@ -347,8 +347,9 @@ def test_lru_eviction_releases_the_oldest_first():
     assert p.stats()["free"] == free + 1  # its second block only; the first is the kid's
 
 
+@pytest.mark.parametrize("mode", ["permute", "fill"])
 @pytest.mark.parametrize("seed", [0, 1, 7, 12345])
-def test_compaction_moves_live_blocks_to_the_front(seed):
+def test_compaction_moves_live_blocks_to_the_front(seed, mode):
     r = np.random.default_rng(seed + 3)
     p = host_pool(300, 2)
     data = Data(p)
@@ -366,9 +367,18 @@ def test_compaction_moves_live_blocks_to_the_front(seed):
     live = [s for s in seqs if s not in seqs[::3]] + kids
     before = {(s, l): data.read(s, l) for s in live for l in range(2)}
     refs_before = sorted(p.refcount(b) for b in range(300) if p.refcount(b))
-    moved = p.compact(seed)
-    data.sync_copies()
     K = len(refs_before)
+    above = sum(1 for b in range(K, 300) if p.refcount(b))
+    stay = {b: p.refcount(b) for b in range(K) if p.refcount(b)}
+    moved = p.compact(seed, mode=mode)
+    if mode == "fill":
+        # the fewest moves (only blocks past the live count), one launch, nothing below K moved
+        batches = p.take_batches()
+        assert moved == above and len(batches) == 1 and len(batches[0][0]) == above
+        assert all(int(x) >= K for x in batches[0][0]) and all(int(x) < K for x in batches[0][1])
+        assert all(p.refcount(b) == r for b, r in stay.items())
+        data.sync_copies(batches)
+    data.sync_copies()
     assert sorted(p.refcount(b) for b in range(K)) == refs_before
     assert all(p.refcount(b) == 0 for b in range(K, 300))
     assert p.stats()["moved_blocks"] == moved and moved > 0
