@@ -168,6 +168,23 @@ int qvkv_attention_async(qvkv_dev *dev, const qvkv_layout *layout, const void *p
                          uint32_t n_items, uint32_t heads, uint32_t max_pos, float *out,
                          void *stream);
 
+/* qvkv_attention_async without any allocation: no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments and results.  A launch that
+ * splits the context keeps its partial results in a file-scope device array of
+ * QVKV_NOALLOC_SCRATCH_BYTES (one per GPU, held until the process ends) instead of the
+ * stream's workspace; a launch needing more returns QVKV_E_SHAPE before it starts.  Every
+ * call on one GPU shares that array (the last call's contents stay in it): calls that
+ * overlap on one GPU, on any streams or device handles, race.  Index errors its kernels
+ * latch go to a device-wide flag in the same array, reported (and cleared) by the next
+ * qvkv_check on any stream of the device. */
+#define QVKV_NOALLOC_SCRATCH_BYTES (32ull << 20)
+int qvkv_attention_noalloc_async(qvkv_dev *dev, const qvkv_layout *layout, const void *pool,
+                                 uint64_t pool_blocks, const float *q, const uint32_t *blocks,
+                                 uint64_t n_table, const uint32_t *table_at, const uint32_t *pos,
+                                 uint32_t n_items, uint32_t heads, uint32_t max_pos, float *out,
+                                 void *stream);
+
 /* Paged prefill attention: segment i holds n_tok[i] consecutive tokens of one sequence
  * whose rows are already stored; token j of it sits at position pos0[i] + j and reads
  * q row q_at[i] + j ([q_rows][heads][d] f32) and writes the same out row.  It attends

@@ -90,6 +90,8 @@ struct qvkv_dev {
     std::atomic<uint64_t> uploads{0}, upload_bytes{0}, downloads{0}, download_bytes{0};
     std::atomic<uint64_t> submissions{0}, wait_ns{0}, timed{0}, gpu_ns{0}, last_gpu_ns{0};
     std::atomic<uint64_t> stream_waits{0};
+    uint8_t *scratch = nullptr;  // this device's copy of `scratch` (allocation-free entry)
+    int *scratch_err = nullptr;  // its error flag (the first 256 bytes)
     char name[256] = {0};
 };
 
@@ -98,6 +100,12 @@ struct qvkv_buf {
     void *ptr;
     size_t len;
 };
+
+// Scratch of the allocation-free attention entry point: the error flag of its kernels
+// (the first 256 bytes) and the partial results of split-context launches.  Each GPU
+// holds its own copy for the life of the process; host code reaches it only through
+// the address hipGetSymbolAddress returns for the device (qvkv_dev::scratch).
+static __device__ __align__(256) uint8_t scratch[QVKV_NOALLOC_SCRATCH_BYTES + 256];
 
 namespace {
 
@@ -239,10 +247,14 @@ int download(qvkv_dev *dev, void *host, const void *devp, uint64_t len) {
     return QVKV_OK;
 }
 
-// Takes a stream's latched error bits: one thread exchanges the flag with 0 (so bits a
-// kernel latches meanwhile are never lost) and keeps what it held in flag[1].
-__global__ void k_take_error(int *flag) {
-    if (threadIdx.x == 0) flag[1] = atomicExch(&flag[0], 0);
+// Takes latched error bits: one thread exchanges each flag with 0 (so bits a kernel
+// latches meanwhile are never lost) and keeps what it held in flag[1].  `other` is the
+// device-wide flag of the allocation-free entry point (may be null).
+__global__ void k_take_error(int *flag, int *other) {
+    if (threadIdx.x == 0) {
+        flag[1] = atomicExch(&flag[0], 0);
+        if (other) other[1] = atomicExch(&other[0], 0);
+    }
 }
 
 // The status a set of latched bits stands for.
@@ -266,18 +278,21 @@ int status_of(int bits) {
 int finish(qvkv_dev *dev, StreamState *st) {
     std::lock_guard<std::mutex> lk(st->check_mu);
     auto t0 = std::chrono::steady_clock::now();
-    hipLaunchKernelGGL(k_take_error, dim3(1), dim3(64), 0, st->stream, st->d_err);
+    int *other = dev->scratch_err;
+    hipLaunchKernelGGL(k_take_error, dim3(1), dim3(64), 0, st->stream, st->d_err, other);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "error flag launch");
-    int bits = 0;
+    int bits = 0, more = 0;
     e = hipMemcpyAsync(&bits, st->d_err + 1, sizeof bits, hipMemcpyDeviceToHost, st->stream);
+    if (e == hipSuccess && other)
+        e = hipMemcpyAsync(&more, other + 1, sizeof more, hipMemcpyDeviceToHost, st->stream);
     if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync (error flag)");
     e = hipStreamSynchronize(st->stream);
     dev->wait_ns.fetch_add((uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
                                std::chrono::steady_clock::now() - t0)
                                .count());
     if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
-    return status_of(bits);
+    return status_of(bits | more);
 }
 
 int launched(qvkv_dev *dev, hipError_t e, const char *what) {
@@ -363,6 +378,21 @@ int qvkv_open(int device, qvkv_dev **out) {
             qvkv_close(d);
             return rc;
         }
+    }
+    // This device's copy of the scratch array (device `device` is current), with its
+    // error flag cleared.
+    if ((e = hipGetSymbolAddress((void **)&d->scratch, HIP_SYMBOL(scratch))) != hipSuccess) {
+        d->scratch = nullptr;
+        qvkv_close(d);
+        return hip_fail(e, "hipGetSymbolAddress (scratch)");
+    }
+    {
+        const int zero[2] = {0, 0};
+        if ((e = hipMemcpy(d->scratch, zero, sizeof zero, hipMemcpyHostToDevice)) != hipSuccess) {
+            qvkv_close(d);
+            return hip_fail(e, "hipMemcpy (scratch error flag)");
+        }
+        d->scratch_err = (int *)d->scratch;
     }
     *out = d;
     return QVKV_OK;
@@ -571,6 +601,36 @@ int qvkv_attention_async(qvkv_dev *dev, const qvkv_layout *layout, const void *p
     return launched(dev, qvkv::launch_attention(g, p, pool, pool_blocks, q, blocks, n_table,
                                                 table_at, pos, n_items, heads, max_pos, out,
                                                 st->ws, st->d_err, st->stream),
+                    "attention launch");
+}
+
+int qvkv_attention_noalloc_async(qvkv_dev *dev, const qvkv_layout *layout, const void *pool,
+                                 uint64_t pool_blocks, const float *q, const uint32_t *blocks,
+                                 uint64_t n_table, const uint32_t *table_at, const uint32_t *pos,
+                                 uint32_t n_items, uint32_t heads, uint32_t max_pos, float *out,
+                                 void *stream) {
+    if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    Geometry g;
+    if (int rc = geometry(layout, &g)) return rc;
+    qvkv::AttnPlan p;
+    const char *why = "";
+    if (int rc = qvkv::plan_attention(g, n_items, heads, max_pos, &p, &why))
+        return fail(rc, "shape mismatch in attention: %s", why);
+    if (p.ws_bytes > QVKV_NOALLOC_SCRATCH_BYTES)
+        return fail(QVKV_E_SHAPE,
+                    "shape mismatch in attention: the launch needs %llu bytes of scratch for its "
+                    "context-chunk partials, past the allocation-free form's %llu",
+                    (unsigned long long)p.ws_bytes,
+                    (unsigned long long)QVKV_NOALLOC_SCRATCH_BYTES);
+    if (n_items == 0) return QVKV_OK;
+    if (!pool || !q || !blocks || !table_at || !pos || !out)
+        return fail(QVKV_E_SHAPE, "shape mismatch in attention: null pointer");
+    if (!dev->scratch) return fail(QVKV_E_DEVICE, "hip device error: no scratch address");
+    if (int rc = set_device(dev)) return rc;
+    return launched(dev, qvkv::launch_attention(g, p, pool, pool_blocks, q, blocks, n_table,
+                                                table_at, pos, n_items, heads, max_pos, out,
+                                                dev->scratch + 256, dev->scratch_err,
+                                                (hipStream_t)stream),
                     "attention launch");
 }
 
