@@ -342,14 +342,14 @@ def run_decode(name, args, dev, legs, steps, warmup, cpu):
         seen = float(np.sum([PF * (int(p) + 1) + PF * (PF - 1) / 2 for p in seg_pos0]))
         p_flops = 4.0 * H * D * seen
         # MFMA work the f16 prefill kernel issues: per wave (16 query rows) and 32-position
-        # tile up to its last row's position, 2*(d/32)*2 + (d/16)*2 v_mfma_f32_16x16x32_f16
-        # (q and p as f16 high part + residual), 8192 FMA each.
+        # tile up to its last row's position, 2*(d/32)*2 + (d/16) v_mfma_f32_16x16x32_f16
+        # (q as f16 high part + residual, P as one f16), 8192 FMA each.
         GS = H // G
         rows = PF * GS
         w_first = np.arange(0, rows, 16)
         last_tok = np.minimum(PF - 1, (w_first + 15) // GS)
         tiles = sum(float(np.sum((int(p0) + last_tok + 1 + 31) // 32)) for p0 in seg_pos0) * G
-        p_mfma = tiles * (4 * (D // 32) + 2 * (D // 16)) * 16384.0
+        p_mfma = tiles * (4 * (D // 32) + (D // 16)) * 16384.0
         res.update(prefill_ms=p_ms, prefill_tok_s=S * PF / (p_ms / 1e3),
                    prefill_tflops=p_flops / (p_ms / 1e3) / 1e12)
         if dtype == "f16" and D in (64, 128):  # the LDS-staged 16x16x32 kernel

@@ -182,7 +182,10 @@ __device__ __forceinline__ uint32_t vswz(uint32_t r) {
 
 // DMA: the register budget of 3 waves/SIMD (170 VGPRs; the DMA form holds no staging
 // registers): 392 vs 369 TFLOP/s at 2 waves (cfg5).
-template <int D, bool DMA>
+// PS: P carried as f16 high part + residual (P.V exact in f32, two MFMAs per d block);
+// without it P is one RNE f16 (one MFMA per d block) and the row sums add the rounded
+// probabilities, so the weights the output is normalised by are exactly those applied.
+template <int D, bool DMA, bool PS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DMA ? 3 : 1)))
 void k_prefill_f16(QV_PREFILL_PARAMS) {
     constexpr int TP = PrefillLds<D>::TP;
@@ -413,6 +416,28 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
         float pr[8];
 #pragma unroll
         for (int e = 0; e < 8; e++) pr[e] = __builtin_amdgcn_exp2f(sc[e]);
+        if constexpr (!PS) {
+            // one f16 per probability; the row sum takes the rounded values, pairwise in
+            // f32 (v_dot2 with ones)
+            uint32_t pw[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                pw[k] = __builtin_bit_cast(uint32_t, h2{(_Float16)pr[2 * k], (_Float16)pr[2 * k + 1]});
+            const h2 one = h2{(_Float16)1.0f, (_Float16)1.0f};
+            float psum = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, pw[0]), one, 0.0f, false);
+#pragma unroll
+            for (int k = 1; k < 4; k++)
+                psum = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, pw[k]), one, psum, false);
+            l += psum;
+            const h8 ph = __builtin_bit_cast(h8, u4v{pw[0], pw[1], pw[2], pw[3]});
+#pragma unroll
+            for (int j = 0; j < NDB; j += 2) {
+                const h8 b0 = vread(j), b1 = vread(j + 1);
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, b0, acc[j], 0, 0, 0);
+                acc[j + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, b1, acc[j + 1], 0, 0, 0);
+            }
+            return;
+        }
         float psum = pr[0];  // (0 + p0 = p0: the same sum without the first add)
 #pragma unroll
         for (int e = 1; e < 8; e++) psum += pr[e];
@@ -1025,13 +1050,18 @@ hipError_t launch_prefill(const Geometry &g, const void *pool, uint64_t pool_blo
     if (!q8 && (g.D == 64 || g.D == 128) && tune("QVKV_PREFILL_V2", 1)) {
         const uint32_t n_qb = (uint32_t)(((uint64_t)max_tok * GS + 63) / 64);
         const unsigned grid2 = (unsigned)((uint64_t)n_seg * g.G * n_qb);
-#define QV_PF2(DD, DMA)                                                                        \
-    hipLaunchKernelGGL((k_prefill_f16<DD, DMA>), dim3(grid2), dim3(256), 0, s, pp, pool_blocks, \
-                       q, blocks, n_table, table_at, pos0, q_at, n_tok, n_seg, heads, max_pos, \
-                       max_tok, q_rows, n_qb, out, geo, err)
-        if (g.D == 64) { QV_PF2(64, false); }
-        else if (tune("QVKV_PREFILL_DMA", 1)) { QV_PF2(128, true); }
-        else { QV_PF2(128, false); }
+#define QV_PF2(DD, DMA, PS)                                                                    \
+    hipLaunchKernelGGL((k_prefill_f16<DD, DMA, PS>), dim3(grid2), dim3(256), 0, s, pp,           \
+                       pool_blocks, q, blocks, n_table, table_at, pos0, q_at, n_tok, n_seg,     \
+                       heads, max_pos, max_tok, q_rows, n_qb, out, geo, err)
+        // P as one f16 (the default) or as high part + residual (QVKV_PREFILL_EXACT_P=1)
+        const bool ps = tune("QVKV_PREFILL_EXACT_P", 0) != 0;
+        if (g.D == 64) { if (ps) QV_PF2(64, false, true); else QV_PF2(64, false, false); }
+        else if (tune("QVKV_PREFILL_DMA", 1)) {
+            if (ps) QV_PF2(128, true, true); else QV_PF2(128, true, false);
+        } else {
+            if (ps) QV_PF2(128, false, true); else QV_PF2(128, false, false);
+        }
 #undef QV_PF2
         return hipGetLastError();
     }

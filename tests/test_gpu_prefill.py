@@ -83,9 +83,14 @@ def test_prefill_within_tolerance(hip, dtype, H, G, D, segs):
     assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)
 
 
-def test_prefill_equals_decode_kernel_per_token(hip):
+@pytest.mark.parametrize("exact_p", [True, False])
+def test_prefill_equals_decode_kernel_per_token(hip, exact_p, monkeypatch):
     """The prefill kernel and the decode kernel (one item per token) agree to float
-    rounding on the same pool: the same tiles, scores and softmax, another order."""
+    rounding on the same pool: the same tiles, scores and softmax, another order (with
+    the prefill's P as high part + residual); with P as one f16 (the default prefill)
+    to its rounding, 2^-11 relative per probability."""
+    if exact_p:
+        monkeypatch.setenv("QVKV_PREFILL_EXACT_P", "1")
     r = rng(31)
     L = layout(F16, 8, 128)
     H = 32
@@ -104,7 +109,7 @@ def test_prefill_equals_decode_kernel_per_token(hip):
                   H, 699, b)
     hip.check()
     d = (a - b).abs().max().item()
-    assert d < 1e-5, d
+    assert d < (1e-5 if exact_p else 2e-4), d
 
 
 @pytest.mark.parametrize("dtype,D", [(F16, 64), (F16, 128), (Q8_0, 128), (Q8_0, 64)])
@@ -195,13 +200,18 @@ def _f64_attention(k16, v16, q, g_of, npos):
     return p @ v16[:npos, g_of] / p.sum()
 
 
-@pytest.mark.parametrize("kind", ["prefill", "decode"])
-def test_f16_paths_track_float64_closely(hip, kind):
-    """With f16 K/V the products q.k and p.v are exact in the MFMAs (q and p carried as
-    f16 high part + residual), so both attention paths sit within ~1e-6 of float64.
-    Pins the split: a high part and residual taken from two different roundings of
-    the same product (a contraction into v_fma_mix for one of them) leaves one-ulp
-    errors that show up here as ~1e-5, far inside the reference tolerance."""
+@pytest.mark.parametrize("kind", ["prefill", "prefill_exact_p", "decode"])
+def test_f16_paths_track_float64_closely(hip, kind, monkeypatch):
+    """With f16 K/V the products q.k and p.v are exact in the MFMAs when q and p are
+    carried as f16 high part + residual (decode, and the prefill with
+    QVKV_PREFILL_EXACT_P=1): those paths sit within ~1e-6 of float64.  Pins the split: a
+    high part and residual taken from two different roundings of the same product (a
+    contraction into v_fma_mix for one of them) leaves one-ulp errors that show up here
+    as ~1e-5.  The default prefill carries P as one f16 (relative error 2^-11 per
+    probability, normalised by the sum of the rounded values): about 2e-5 here, held
+    under 2e-4, ten times inside the reference tolerance of 2e-3."""
+    if kind == "prefill_exact_p":
+        monkeypatch.setenv("QVKV_PREFILL_EXACT_P", "1")
     r = rng(77)
     G, D, H = 4, 128, 32
     L = layout(F16, G, D)
@@ -218,7 +228,7 @@ def test_f16_paths_track_float64_closely(hip, kind):
         v16[p] = dec["v"][b, :, o].view(np.float16).astype(np.float64)
     q = normal(r, (nt, H, D))
     out = torch.zeros(nt * H * D, dtype=torch.float32, device="cuda")
-    if kind == "prefill":
+    if kind.startswith("prefill"):
         hip.prefill_attention(L, pool, N, cf32(q), cu32(blocks), cu32(table_at),
                               cu32([n - nt]), cu32([0]), cu32([nt]), H, n - 1, nt, out)
     else:
@@ -233,7 +243,7 @@ def test_f16_paths_track_float64_closely(hip, kind):
             worst = max(worst, np.abs(got[j, h] - _f64_attention(k16, v16, q[j, h], h // (H // G),
                                                                  n - nt + j + 1)).max())
     print(f"  {kind}: max |got - f64| = {worst:.2e}", flush=True)
-    assert worst < 1e-5, worst
+    assert worst < (2e-4 if kind == "prefill" else 1e-5), worst
 
 
 @pytest.mark.parametrize("kind", ["prefill", "decode"])
@@ -262,7 +272,7 @@ def test_q8_0_paths_track_float64_closely(hip, kind):
         vd[p] = dec["v"][b, :, o].astype(np.float64) * vs[:, grp]
     q = normal(r, (nt, H, D))
     out = torch.zeros(nt * H * D, dtype=torch.float32, device="cuda")
-    if kind == "prefill":
+    if kind.startswith("prefill"):
         hip.prefill_attention(L, pool, N, cf32(q), cu32(blocks), cu32(table_at),
                               cu32([n - nt]), cu32([0]), cu32([nt]), H, n - 1, nt, out)
     else:
