@@ -61,6 +61,116 @@ __device__ __forceinline__ float lane_tree_x(float a) {
     return dpp_add<0x4E>(a);  // quad_perm [2,3,0,1]
 }
 
+// lane_tree_x for HB heads at once (HB = 4, 8 or 16; a[h] = lane l's partial sum of head
+// h).  The trees are interleaved so that one cross-lane move serves two heads: at each
+// width w = 32, 16, 8, 4 two registers X, Y (each holding heads in blocks of lanes that
+// the step keeps apart) become one, the lanes whose block comes from X computing X's
+// a[i] + a[i +- w] and the others Y's.  Every head gets exactly lane_tree's sums (each is
+// one IEEE addition of the same two values), in 2 (HB - 1) + a few instructions instead
+// of 6 HB dependent moves.  Head h's total ends in the lanes of the quad starting at
+// head_lane<HB>(h).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float a) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, a), CTRL,
+                                                             0xF, 0xF, true));
+}
+__device__ __forceinline__ float xor4(float a) {
+    // ds_swizzle bit-mask mode: lane ^ 4 within each group of 32 lanes
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, a),
+                                                                 0x101F));
+}
+
+// Which lanes hold which head after each step (the map the device code follows).
+template <int HB>
+struct TreeMap {
+    int head[64];
+    constexpr TreeMap() : head() {
+        int map[16][64] = {};
+        int valid[64] = {};
+        for (int r = 0; r < HB; r++)
+            for (int i = 0; i < 64; i++) map[r][i] = r;
+        for (int i = 0; i < 64; i++) valid[i] = 1;
+        int n = HB;
+        bool paired8 = false;
+        for (int w = 32; w >= 4; w /= 2) {
+            if (n >= 2) {
+                for (int r = 0; r < n / 2; r++)
+                    for (int i = 0; i < 64; i++) {
+                        const bool from_x = w == 32 ? i < 32
+                                          : w == 16 ? ((i >> 4) & 1) == 0
+                                          : w == 8 ? (i & 8) == 0
+                                                   : (i & 4) == 0;
+                        map[r][i] = from_x ? map[2 * r][i] : map[2 * r + 1][i];
+                    }
+                n /= 2;
+                if (w == 8) paired8 = true;
+            } else if (w == 4 && paired8) {
+                for (int i = 0; i < 64; i++)
+                    if (i & 4) valid[i] = 0;  // their rotation partner lies in another head
+            }
+        }
+        for (int i = 0; i < 64; i++) head[i] = valid[i] && i % 4 == 0 ? map[0][i] : -1;
+    }
+};
+template <int HB>
+__device__ constexpr int head_lane(int h) {
+    constexpr TreeMap<HB> m;
+    for (int i = 0; i < 64; i++)
+        if (m.head[i] == h) return i;
+    return -1;
+}
+
+template <int HB>
+__device__ __forceinline__ float head_trees(const float (&a)[HB], uint32_t lane) {
+    static_assert(HB == 4 || HB == 8 || HB == 16, "heads per wave");
+    float r[HB];
+#pragma unroll
+    for (int h = 0; h < HB; h++) r[h] = a[h];
+    // w = 32: X' = [X_lo, Y_lo], Y' = [X_hi, Y_hi]
+#pragma unroll
+    for (int m = 0; m < HB / 2; m++) {
+        const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, r[2 * m]),
+                                                         __builtin_bit_cast(uint32_t, r[2 * m + 1]),
+                                                         false, false);
+        const uint32_t p0 = p[0], p1 = p[1];
+        r[m] = __builtin_bit_cast(float, p0) + __builtin_bit_cast(float, p1);
+    }
+    // w = 16: rows [X0 Y0 X2 Y2] + [X1 Y1 X3 Y3]
+#pragma unroll
+    for (int m = 0; m < HB / 4; m++) {
+        const auto p = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, r[2 * m]),
+                                                         __builtin_bit_cast(uint32_t, r[2 * m + 1]),
+                                                         false, false);
+        const uint32_t p0 = p[0], p1 = p[1];
+        r[m] = __builtin_bit_cast(float, p0) + __builtin_bit_cast(float, p1);
+    }
+    const bool hi8 = (lane & 8u) != 0, hi4 = (lane & 4u) != 0;
+    float x;
+    if constexpr (HB >= 8) {
+        // w = 8, paired: lanes with bit 3 clear take X's pair, the others Y's
+#pragma unroll
+        for (int m = 0; m < HB / 8; m++) {
+            const float t = hi8 ? r[2 * m + 1] : r[2 * m];
+            const float u = hi8 ? r[2 * m] : r[2 * m + 1];
+            r[m] = t + dpp_mov<0x128>(u);  // row_ror:8: the partner is lane i ^ 8
+        }
+        if constexpr (HB == 16) {
+            // w = 4, paired: lanes with bit 2 clear take X's pair, the others Y's
+            const float t = hi4 ? r[1] : r[0];
+            const float u = hi4 ? r[0] : r[1];
+            x = t + xor4(u);
+        } else {
+            // w = 4 on one register: lanes with bit 2 clear get a[i] + a[i + 4]
+            x = r[0] + dpp_mov<0x124>(r[0]);  // row_ror:4
+        }
+    } else {
+        x = r[0] + dpp_mov<0x128>(r[0]);  // row_ror:8 (rows hold one head)
+        x = x + dpp_mov<0x124>(x);        // row_ror:4, as lane_tree_x
+    }
+    x = x + dpp_mov<0xB1>(x);  // quad_perm [1,0,3,2]
+    return x + dpp_mov<0x4E>(x);  // quad_perm [2,3,0,1]
+}
+
 // rms_scale_of: correctly rounded division and square root, in this order.
 __device__ __forceinline__ float rms_scale_of(float ss, float n, float eps) {
     return 1.0f / sqrtf(ss / n + eps);
@@ -124,47 +234,36 @@ __global__ __launch_bounds__(64) void k_prelude(float *__restrict__ q, float *__
 // one lane (d = 128, 256) or in lanes l and l ^ 32 (d = 64, exchanged by a lane swap).
 // Loads and stores are dword-coalesced 256-byte runs; no LDS, no barriers, 4 independent
 // waves per workgroup.  Measured against the LDS kernel at 65 536 tokens, 32 query heads:
-// d = 128 with per-head norms 2.66 -> 0.60 ms, without norms 1.86 -> 0.52 ms.
+// d = 128 with per-head norms 2.66 -> 0.60 ms, without norms 1.86 -> 0.52 ms; then with
+// the heads' trees interleaved (head_trees) and a scalar wave index 0.68 -> 0.57 ms, and
+// with non-temporal row loads and stores 0.51 ms (5.3 TB/s).
 // FULL: one norm over each whole row (QkNorm::Full): the wave takes the whole q, k or v row
 // (up to 4096 values, 64 per lane), whose element order h*d + 64j + l is lane l's order
 // of the reference's reduction.
-template <int D, bool FULL, int VPW = 1024>
-__global__ __launch_bounds__(256) void k_prelude_r(float *__restrict__ q, float *__restrict__ k,
-                                                   float *__restrict__ v, uint32_t s,
-                                                   uint32_t heads, uint32_t kvh, uint32_t uq,
-                                                   uint32_t ukv, PreludeArgs a) {
-    // heads per wave: 1024 values was the best of 512, 1024, 2048 without a full norm
-    constexpr uint32_t HB = (FULL ? 4096 : VPW) / D;
+// One wave's share of a row: HB heads from h0 (nh of them present) of token t's q (part
+// 0), k (1) or v (2) row at x.
+template <int D, bool FULL, uint32_t HB>
+__device__ __forceinline__ void prelude_heads(float *__restrict__ x, const float *bias,
+                                              uint32_t h0, uint32_t nh, uint32_t part,
+                                              uint32_t t, uint32_t lane, const PreludeArgs &a) {
     constexpr uint32_t J = D >= 64 ? D / 64 : 1;
-    const uint32_t per_tok = uq + 2 * ukv;
-    const uint32_t u = blockIdx.x * 4u + (threadIdx.x >> 6);
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t t = u / per_tok;
-    if (t >= s) return;
-    const uint32_t r = u - t * per_tok;
-    const uint32_t part = r < uq ? 0u : (r < uq + ukv ? 1u : 2u);
-    const uint32_t h0 = (part == 0 ? r : part == 1 ? r - uq : r - uq - ukv) * HB;
-    const uint32_t row_heads = part == 0 ? heads : kvh;
-    const uint32_t nh = min(HB, row_heads - h0);
-    float *x = (part == 0 ? q : part == 1 ? k : v) + ((uint64_t)t * row_heads + h0) * D;
-    const float *bias = part == 0 ? a.q_bias : part == 1 ? a.k_bias : a.v_bias;
-
+    // Heads past nh (a partial batch) hold zeros and are neither loaded nor stored; every
+    // other step runs on all HB heads, so the heads' work interleaves freely.
     float z[HB][J];
 #pragma unroll
     for (uint32_t h = 0; h < HB; h++)
-        if (h < nh)
 #pragma unroll
-            for (uint32_t j = 0; j < J; j++) z[h][j] = x[h * D + 64 * j + lane];
+        for (uint32_t j = 0; j < J; j++)  // streamed once: non-temporal (+11 % at cfg5)
+            z[h][j] = h < nh ? __builtin_nontemporal_load(&x[h * D + 64 * j + lane]) : 0.0f;
 #pragma unroll
     for (uint32_t h = 0; h < HB; h++)
-        if (h < nh)
 #pragma unroll
-            for (uint32_t j = 0; j < J; j++) {
-                float y = z[h][j];
-                if (bias) y = y + bias[(h0 + h) * D + 64 * j + lane];
-                if (a.has_clip) y = y < -a.clip ? -a.clip : (y > a.clip ? a.clip : y);
-                z[h][j] = y;
-            }
+        for (uint32_t j = 0; j < J; j++) {
+            float y = z[h][j];
+            if (bias && h < nh) y = y + bias[(h0 + h) * D + 64 * j + lane];
+            if (a.has_clip) y = y < -a.clip ? -a.clip : (y > a.clip ? a.clip : y);
+            z[h][j] = y;
+        }
     if (part != 2) {
         const float *w = part == 0 ? a.q_norm : a.k_norm;
         if (FULL && w) {
@@ -181,30 +280,29 @@ __global__ __launch_bounds__(256) void k_prelude_r(float *__restrict__ q, float 
 #pragma unroll
                     for (uint32_t j = 0; j < J; j++)
                         z[h][j] = (z[h][j] * rs) * w[h * D + 64 * j + lane];
-        } else if (!FULL && a.norm == QVKV_NORM_PER_HEAD && w) {
-            // head h's sum of squares to lane h; one rms_scale_of for all heads
-            float tot = 0.0f;
+        } else if constexpr (!FULL) {
+          if (a.norm == QVKV_NORM_PER_HEAD && w) {
+            // every head's sum of squares in one interleaved pass; one rms_scale_of
+            float acc[HB];
 #pragma unroll
             for (uint32_t h = 0; h < HB; h++) {
-                if (h < nh) {  // nh is wave-uniform: the tree's moves see every lane
-                    float acc = 0.0f;
+                acc[h] = 0.0f;
 #pragma unroll
-                    for (uint32_t j = 0; j < J; j++) acc = fmaf(z[h][j], z[h][j], acc);
-                    const float t = lane_tree_x(acc);
-                    tot = lane == h ? t : tot;
-                }
+                for (uint32_t j = 0; j < J; j++) acc[h] = fmaf(z[h][j], z[h][j], acc[h]);
             }
-            const float rsv = rms_scale_of(tot, (float)D, a.eps);
+            const float rsv = rms_scale_of(head_trees<HB>(acc, lane), (float)D, a.eps);
+            float wj[J];
+#pragma unroll
+            for (uint32_t j = 0; j < J; j++) wj[j] = w[64 * j + lane];
 #pragma unroll
             for (uint32_t h = 0; h < HB; h++) {
-                if (h < nh) {
-                    const float rs = __builtin_bit_cast(
-                        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, rsv), h));
+                const float rs = __builtin_bit_cast(
+                    float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, rsv),
+                                                     head_lane<HB>((int)h)));
 #pragma unroll
-                    for (uint32_t j = 0; j < J; j++)
-                        z[h][j] = (z[h][j] * rs) * w[64 * j + lane];
-                }
+                for (uint32_t j = 0; j < J; j++) z[h][j] = (z[h][j] * rs) * wj[j];
             }
+          }
         }
         const float *cs = a.rope + (uint64_t)t * D;
         if constexpr (D == 64) {
@@ -213,7 +311,7 @@ __global__ __launch_bounds__(256) void k_prelude_r(float *__restrict__ q, float 
             const bool first = lane < 32;
 #pragma unroll
             for (uint32_t h = 0; h < HB; h++) {
-                if (h < nh) {
+                {
                     // v_permlane32_swap of z with itself: lanes l and l ^ 32 both get
                     // (x[l mod 32], x[l mod 32 + 32]) = (x1, x2) of their pair
                     const uint32_t zu = __builtin_bit_cast(uint32_t, z[h][0]);
@@ -235,7 +333,6 @@ __global__ __launch_bounds__(256) void k_prelude_r(float *__restrict__ q, float 
             }
 #pragma unroll
             for (uint32_t h = 0; h < HB; h++)
-                if (h < nh)
 #pragma unroll
                     for (uint32_t jj = 0; jj < JH; jj++) {
                         const float x1 = z[h][jj], x2 = z[h][jj + JH];
@@ -250,7 +347,33 @@ __global__ __launch_bounds__(256) void k_prelude_r(float *__restrict__ q, float 
     for (uint32_t h = 0; h < HB; h++)
         if (h < nh)
 #pragma unroll
-            for (uint32_t j = 0; j < J; j++) x[h * D + 64 * j + lane] = z[h][j];
+            for (uint32_t j = 0; j < J; j++)
+                __builtin_nontemporal_store(z[h][j], &x[h * D + 64 * j + lane]);
+}
+
+// One wave per (token, q|k|v, batch of HB heads).  (Fewer heads per wave on k and v rows
+// with few KV heads, 4 instead of 16 at cfg5's 4 KV heads, measured 17 % slower.)
+template <int D, bool FULL, int VPW = 1024>
+__global__ __launch_bounds__(256) void k_prelude_r(float *__restrict__ q, float *__restrict__ k,
+                                                   float *__restrict__ v, uint32_t s,
+                                                   uint32_t heads, uint32_t kvh, uint32_t uq,
+                                                   uint32_t ukv, PreludeArgs a) {
+    // heads per wave: 1024 values was the best of 512, 1024, 2048 without a full norm
+    constexpr uint32_t HB = (FULL ? 4096 : VPW) / D;
+    const uint32_t per_tok = uq + 2 * ukv;
+    // the wave index as a scalar: every per-head branch below is then a scalar branch
+    const uint32_t u = blockIdx.x * 4u + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t t = u / per_tok;
+    if (t >= s) return;
+    const uint32_t r = u - t * per_tok;
+    const uint32_t part = r < uq ? 0u : (r < uq + ukv ? 1u : 2u);
+    const uint32_t h0 = (part == 0 ? r : part == 1 ? r - uq : r - uq - ukv) * HB;
+    const uint32_t row_heads = part == 0 ? heads : kvh;
+    const uint32_t nh = min(HB, row_heads - h0);
+    float *x = (part == 0 ? q : part == 1 ? k : v) + ((uint64_t)t * row_heads + h0) * D;
+    const float *bias = part == 0 ? a.q_bias : part == 1 ? a.k_bias : a.v_bias;
+    prelude_heads<D, FULL, HB>(x, bias, h0, nh, part, t, lane, a);
 }
 
 hipError_t launch_prelude(float *q, float *k, float *v, uint32_t s, uint32_t heads,
@@ -268,24 +391,20 @@ hipError_t launch_prelude(float *q, float *k, float *v, uint32_t s, uint32_t hea
         const uint64_t waves = (uint64_t)s * (uq + 2 * ukv);
         const uint64_t grid = (waves + 3) / 4;
         if (waves > 0xffffffffull || grid > 0x7fffffffull) return hipErrorInvalidValue;
-#define QV_PRE1(DD, FF)                                                                         \
-    hipLaunchKernelGGL((k_prelude_r<DD, FF>), dim3((unsigned)grid), dim3(256), 0, st, q, k, v,   \
-                       s, heads, kvh, uq, ukv, a)
-#define QV_PRE1W(DD)                                                                            \
-    hipLaunchKernelGGL((k_prelude_r<DD, false, (DD == 128 ? 2048 : 1024)>), dim3((unsigned)grid), \
-                       dim3(256), 0, st, q, k, v, s, heads, kvh, uq, ukv, a)
+#define QV_PRE_L(DD, FF, VPW)                                                                   \
+    hipLaunchKernelGGL((k_prelude_r<DD, FF, VPW>), dim3((unsigned)grid), dim3(256), 0, st, q, k, \
+                       v, s, heads, kvh, uq, ukv, a)
 #define QV_PRE(DD)                                                                              \
     do {                                                                                        \
-        if (full) QV_PRE1(DD, true);                                                            \
-        else if (wide && DD == 128) QV_PRE1W(DD);                                               \
-        else QV_PRE1(DD, false);                                                                \
+        if (full) QV_PRE_L(DD, true, 1024);                                                     \
+        else if (wide && DD == 128) QV_PRE_L(DD, false, (DD == 128 ? 2048 : 1024));            \
+        else QV_PRE_L(DD, false, 1024);                                                         \
     } while (0)
         if (d == 64) QV_PRE(64);
         else if (d == 128) QV_PRE(128);
         else QV_PRE(256);
 #undef QV_PRE
-#undef QV_PRE1
-#undef QV_PRE1W
+#undef QV_PRE_L
         return hipGetLastError();
     }
     const uint64_t lds = (uint64_t)(heads > kvh ? heads : kvh) * d * 4;
