@@ -326,28 +326,57 @@ def test_cfg4_prefix_sharing_cow_eviction_compaction(hip):
 
 
 def test_cfg5_sampled(hip):
-    """The bench workload's shape (48 layers, 4 KV heads, GQA 8:1, 8192 positions) on a
-    sample of 24 (sequence, layer) items, against the oracle."""
-    from qubivex_amd import KvLayout
+    """The bench workload's shape and construction at a smaller batch: 48 layers, 4 KV
+    heads, GQA 8:1, 8192 positions, tables from the pool manager after seeded alloc/free
+    churn (fragmented, as bench.py builds them), one attention launch over every (sequence,
+    layer) item of 4 sequences (192 items); 8 sampled items against the oracle."""
+    from qubivex_amd import KvLayout, KvPool
 
     print("cfg5 sampled", flush=True)
-    G, D, H, B, CTX, ITEMS = 4, 128, 32, 16, 8192, 24
+    NL, G, D, H, B, CTX, S = 48, 4, 128, 32, 16, 8192, 4
     layout = KvLayout("f16", G, D, B)
     r = np.random.default_rng(505)
-    N = ITEMS * CTX // B + 100
-    blocks, table_at = random_tables(r, [CTX] * ITEMS, B, N)
-    pool = torch.zeros(N * layout.block_bytes, dtype=torch.uint8, device="cuda")
+    N = int(S * NL * CTX // B * 1.3) + 512
+    pool = KvPool(hip, layout, N, NL)
+    mem = pool.memory
+    dummies, used = [], 0
+    while used < int(N * 0.2):  # churn: scatter the free list
+        d = pool.create()
+        n = int(r.integers(16, 16 * 64))
+        pool.plan_append([d], [n], int(r.integers(NL)))
+        used += (n + B - 1) // B
+        dummies.append(d)
+    for i in r.permutation(len(dummies))[: len(dummies) // 2]:
+        pool.release(dummies[int(i)])
+    seqs = [pool.create() for _ in range(S)]
     gen = torch.Generator(device="cuda").manual_seed(505)
-    src = fill_layerwise(hip, layout, pool, N, blocks, table_at, ITEMS, 1, np.full(ITEMS, CTX), gen)
-    q = torch.randn((ITEMS, H, D), generator=gen, device="cuda")
-    out = torch.empty((ITEMS, H, D), device="cuda")
-    pos = np.full(ITEMS, CTX - 1, np.uint32)
-    hip.attention(layout, pool, N, q, t32(blocks), t32(table_at), t32(pos), H, CTX - 1, out)
+    src = []
+    for l in range(NL):
+        slots = pool.plan_append(seqs, [CTX] * S, l)
+        k = torch.randn((slots.size, G * D), generator=gen, device="cuda")
+        v = torch.randn((slots.size, G * D), generator=gen, device="cuda")
+        hip.append(layout, mem, N, k, v, t32(slots))
+        src.append((k, v))
     hip.check()
-    k, v = src[0]
-    for t in range(0, ITEMS, 6):
-        kh = k[t * CTX:(t + 1) * CTX].view(CTX, G, D).permute(1, 0, 2).half().float().cpu().numpy()
-        vh = v[t * CTX:(t + 1) * CTX].view(CTX, G, D).permute(1, 0, 2).half().float().cpu().numpy()
-        want = oracle_attention(kh, vh, q[t].cpu().numpy(), CTX)
-        e = attn_errors(out[t].cpu().numpy(), want)
-        assert e[0] <= MAX_ABS and e[1] <= REL_L2, (t, e)
+    tabs = [pool.tables(seqs, l) for l in range(NL)]
+    blocks = np.concatenate([t[0] for t in tabs])
+    offs = np.cumsum([0] + [t[0].size for t in tabs[:-1]])
+    table_at = np.concatenate([t[1] + o for t, o in zip(tabs, offs)]).astype(np.uint32)
+    pos = np.concatenate([t[2] for t in tabs]).astype(np.uint32)
+    assert np.array_equal(pos, np.full(S * NL, CTX - 1))
+    assert np.mean(np.diff(blocks.astype(np.int64)) != 1) > 0.01  # fragmented tables
+    items = S * NL
+    q = torch.randn((items, H, D), generator=gen, device="cuda")
+    out = torch.empty((items, H, D), device="cuda")
+    hip.attention(layout, mem, N, q, t32(blocks), t32(table_at), t32(pos), H, CTX - 1, out)
+    hip.check()
+    for it in np.sort(r.choice(items, 8, replace=False)):
+        l, s = divmod(int(it), S)  # items are layer-major, sequences within a layer
+        k, v = src[l]
+        kh = k[s * CTX:(s + 1) * CTX].view(CTX, G, D).permute(1, 0, 2).half().float().cpu().numpy()
+        vh = v[s * CTX:(s + 1) * CTX].view(CTX, G, D).permute(1, 0, 2).half().float().cpu().numpy()
+        want = oracle_attention(kh, vh, q[it].cpu().numpy(), CTX)
+        e = attn_errors(out[it].cpu().numpy(), want)
+        print(f"  cfg5 item {it} (layer {l}, seq {s}): max_abs={e[0]:.2e} rel_l2={e[1]:.2e}", flush=True)
+        assert e[0] <= MAX_ABS and e[1] <= REL_L2, (it, e)
+    pool.close()
