@@ -62,6 +62,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="cfg5", choices=DECODE_CONFIGS)
     ap.add_argument("--only", action="store_true", help="skip the other configurations")
+    ap.add_argument("--configs", default="cfg2,cfg3,cfg4,cfg1",
+                    help="the other configurations to run after the headline (comma list)")
     ap.add_argument("--seqs", type=int, default=None, help="override the config's sequences")
     ap.add_argument("--ctx", type=int, default=None, help="override the config's context")
     ap.add_argument("--layers", type=int, default=None, help="override the config's layers")
@@ -384,6 +386,17 @@ def run_decode(name, args, dev, legs, steps, warmup, cpu):
             f"{res['prelude_gbs']:.0f} GB/s")
         del xq, xk, xv, rope
 
+    if "calib" in legs:
+        # A plain device copy of known size (torch's copy kernel, none of this library's):
+        # the reference the PMC traffic summaries scale FETCH_SIZE and WRITE_SIZE by.
+        src = torch.empty(1 << 30, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        src.fill_(1.0)
+        c_ms = timer(lambda: dst.copy_(src), 3)
+        res.update(calib_copy_bytes=2.0 * src.numel() * 4, calib_copy_ms=c_ms)
+        log(f"[bench] calibration copy of {src.numel() * 4 / 2**30:.0f} GiB: {c_ms:.3f} ms")
+        del src, dst
+
     if append_ms:
         a_ms = float(np.mean(append_ms))
         a_gbs = float(np.mean(append_bytes)) / (a_ms / 1e3) / 1e9
@@ -705,16 +718,18 @@ def main():
     res, info = run_decode(args.config, args, dev, legs, args.steps, args.warmup,
                            cpu=not args.no_cpu)
     others = {}
-    if not args.only:
-        for name in DECODE_CONFIGS:
-            if name == args.config:
-                continue
+    for name in ([] if args.only else [c for c in args.configs.split(",") if c]):
+        if name == args.config:
+            continue
+        if name in DECODE_CONFIGS:
             r2, i2 = run_decode(name, args, dev, {"decode", "layers", "gather", "copy"},
                                 max(5, args.steps // 2), 2, cpu=False)
             others[name] = summary(r2, i2)
             others[name]["roofline"] = roofline_of(name, r2, i2)
-        others["cfg4"] = run_cfg4(args, dev)
-        others["cfg1"] = run_cfg1(args, dev)
+        elif name == "cfg4":
+            others["cfg4"] = run_cfg4(args, dev)
+        elif name == "cfg1":
+            others["cfg1"] = run_cfg1(args, dev)
 
     cpu = info["cpu"]
     line = {
