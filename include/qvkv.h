@@ -355,6 +355,13 @@ int qvkv_seq_touch(qvkv_pool *pool, uint32_t seq);
  * `stream`. */
 int qvkv_pool_plan_append(qvkv_pool *pool, const uint32_t *seqs, const uint32_t *count,
                           uint32_t n_seqs, uint32_t layer, uint32_t *slots_out, void *stream);
+/* qvkv_pool_plan_append on layers layer0 .. layer0+n_layers-1 at once (a decode step's or
+ * a prompt chunk's rows of every layer): slots_out is layer-major, then seq-major.  A dry
+ * free list fails the whole call with nothing changed; every layer's copy-on-write pairs
+ * go to the device in one block-copy launch. */
+int qvkv_pool_plan_append_layers(qvkv_pool *pool, const uint32_t *seqs, const uint32_t *count,
+                                 uint32_t n_seqs, uint32_t layer0, uint32_t n_layers,
+                                 uint32_t *slots_out, void *stream);
 /* The attention plan of one decode pass on `layer` with a host-authoritative cache:
  * attention_plan (crates/qubivex-runtime/src/discrete.rs:951-1009).  For each seqs[i] with
  * the host's newest position pos[i] and cache epoch epochs[i]: a sequence whose epoch

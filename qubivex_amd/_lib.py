@@ -144,6 +144,7 @@ SIGNATURES = {
     "qvkv_seq_len": (_i32, [_vp, _u32, _u32, _P(_u32)]),
     "qvkv_seq_touch": (_i32, [_vp, _u32]),
     "qvkv_pool_plan_append": (_i32, [_vp, _vp, _vp, _u32, _u32, _vp, _vp]),
+    "qvkv_pool_plan_append_layers": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _vp, _vp]),
     "qvkv_pool_tables": (_i32, [_vp, _vp, _u32, _u32, _vp, _u64, _P(_u64), _vp, _vp]),
     "qvkv_pool_plan_attention": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _vp, _u64, _P(_u64), _vp,
                                         _vp, _vp, _vp, _vp, _u64, _P(_u64), _vp]),

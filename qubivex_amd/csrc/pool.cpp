@@ -258,71 +258,85 @@ int qvkv_seq_touch(qvkv_pool *p, uint32_t seq) {
     return QVKV_OK;
 }
 
-int qvkv_pool_plan_append(qvkv_pool *p, const uint32_t *seqs, const uint32_t *count,
-                          uint32_t n_seqs, uint32_t layer, uint32_t *slots_out, void *stream) {
-    if (!p || (n_seqs && (!seqs || !count || !slots_out)))
+int qvkv_pool_plan_append_layers(qvkv_pool *p, const uint32_t *seqs, const uint32_t *count,
+                                 uint32_t n_seqs, uint32_t layer0, uint32_t n_layers,
+                                 uint32_t *slots_out, void *stream) {
+    if (!p || (n_seqs && n_layers && (!seqs || !count || !slots_out)))
         return err(QVKV_E_SHAPE, "shape mismatch in pool: null argument");
     std::lock_guard<std::mutex> lk(p->mu);
-    if (layer >= p->n_layers) return err(QVKV_E_SHAPE, "shape mismatch in pool: no such layer");
+    if (layer0 >= p->n_layers || n_layers > p->n_layers - layer0)
+        return err(QVKV_E_SHAPE, "shape mismatch in pool: no such layer");
     const uint32_t B = p->layout.block;
-    // Dry run: blocks this call takes (growth + copies of shared partial blocks), with
-    // the reference counts as they will be when each sequence's turn comes.
+    // Dry run over every layer: blocks this call takes (growth + copies of shared partial
+    // blocks), with the reference counts as they will be when each sequence's turn comes.
+    // A block belongs to one layer's tables, so one count of drops serves all layers.
     std::unordered_map<uint32_t, uint32_t> drops;
     uint64_t need = 0;
     for (uint32_t i = 0; i < n_seqs; i++) {
-        const Seq *s = seq_of(p, seqs[i]);
-        if (!s) return err(QVKV_E_SHAPE, "shape mismatch in pool: no such sequence");
+        if (!seq_of(p, seqs[i])) return err(QVKV_E_SHAPE, "shape mismatch in pool: no such sequence");
         for (uint32_t j = 0; j < i; j++)
             if (seqs[j] == seqs[i]) return err(QVKV_E_SHAPE, "shape mismatch in pool: a sequence twice in one plan");
-        const uint64_t len = s->len[layer];
-        if (len + count[i] > 0xffffffffull) return err(QVKV_E_SHAPE, "shape mismatch in pool: too many positions");
-        const uint64_t want = (len + count[i] + B - 1) / B;
-        if (want > s->blocks[layer].size()) need += want - s->blocks[layer].size();
-        if (count[i] && len % B != 0) {
-            const uint32_t b = s->blocks[layer][len / B];
-            const uint32_t live = p->refs[b] - drops[b];
-            if (live > 1) {
-                need++;
-                drops[b]++;
+    }
+    for (uint32_t layer = layer0; layer < layer0 + n_layers; layer++)
+        for (uint32_t i = 0; i < n_seqs; i++) {
+            const Seq *s = seq_of(p, seqs[i]);
+            const uint64_t len = s->len[layer];
+            if (len + count[i] > 0xffffffffull) return err(QVKV_E_SHAPE, "shape mismatch in pool: too many positions");
+            const uint64_t want = (len + count[i] + B - 1) / B;
+            if (want > s->blocks[layer].size()) need += want - s->blocks[layer].size();
+            if (count[i] && len % B != 0) {
+                const uint32_t b = s->blocks[layer][len / B];
+                const uint32_t live = p->refs[b] - drops[b];
+                if (live > 1) {
+                    need++;
+                    drops[b]++;
+                }
             }
         }
-    }
     if (need > p->free.size()) return dry(p, need);
     std::vector<uint32_t> src, dst;
     uint64_t o = 0;
-    for (uint32_t i = 0; i < n_seqs; i++) {
-        Seq &s = p->seqs[seqs[i]];
-        auto &tab = s.blocks[layer];
-        const uint32_t len = s.len[layer];
-        if (count[i] && len % B != 0 && p->refs[tab[len / B]] > 1) {
-            const uint32_t old = tab[len / B];
-            const uint32_t nb = p->free.back();
-            p->free.pop_back();
-            p->refs[nb] = 1;
-            p->refs[old]--;
-            tab[len / B] = nb;
-            src.push_back(old);
-            dst.push_back(nb);
-            p->cow++;
+    for (uint32_t layer = layer0; layer < layer0 + n_layers; layer++) {
+        for (uint32_t i = 0; i < n_seqs; i++) {
+            Seq &s = p->seqs[seqs[i]];
+            auto &tab = s.blocks[layer];
+            const uint32_t len = s.len[layer];
+            if (count[i] && len % B != 0 && p->refs[tab[len / B]] > 1) {
+                const uint32_t old = tab[len / B];
+                const uint32_t nb = p->free.back();
+                p->free.pop_back();
+                p->refs[nb] = 1;
+                p->refs[old]--;
+                tab[len / B] = nb;
+                src.push_back(old);
+                dst.push_back(nb);
+                p->cow++;
+            }
+            const uint64_t want = ((uint64_t)len + count[i] + B - 1) / B;
+            while (tab.size() < want) {
+                const uint32_t nb = p->free.back();
+                p->free.pop_back();
+                p->refs[nb] = 1;
+                tab.push_back(nb);
+            }
+            for (uint32_t k = 0; k < count[i]; k++) {
+                const uint32_t pos = len + k;
+                slots_out[o++] = tab[pos / B] * B + pos % B;
+            }
+            s.len[layer] = len + count[i];
+            s.used = ++p->clock;
+            p->rows += count[i];
         }
-        const uint64_t want = ((uint64_t)len + count[i] + B - 1) / B;
-        while (tab.size() < want) {
-            const uint32_t nb = p->free.back();
-            p->free.pop_back();
-            p->refs[nb] = 1;
-            tab.push_back(nb);
-        }
-        for (uint32_t k = 0; k < count[i]; k++) {
-            const uint32_t pos = len + k;
-            slots_out[o++] = tab[pos / B] * B + pos % B;
-        }
-        s.len[layer] = len + count[i];
-        s.used = ++p->clock;
-        p->rows += count[i];
+        p->layers++;
     }
-    p->layers++;
-    // A shared block's filled slots are copied before the caller writes into the copy.
+    // A shared block's filled slots are copied (one launch for every layer) before the
+    // caller writes into the copies.
     return copy_blocks(p, src, dst, stream);
+}
+
+int qvkv_pool_plan_append(qvkv_pool *p, const uint32_t *seqs, const uint32_t *count,
+                          uint32_t n_seqs, uint32_t layer, uint32_t *slots_out, void *stream) {
+    return qvkv_pool_plan_append_layers(p, seqs, count, n_seqs, layer, 1, slots_out, stream);
 }
 
 int qvkv_pool_plan_attention(qvkv_pool *p, const uint32_t *seqs, const uint32_t *pos,

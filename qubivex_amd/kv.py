@@ -466,6 +466,17 @@ class KvPool:
                                         self._copy_stream(stream)))
         return out
 
+    def plan_append_layers(self, seqs, counts, layer0, n_layers, stream=None):
+        """plan_append on n_layers layers from layer0 at once: slots layer-major, then
+        seq-major; one copy-on-write launch for every layer."""
+        s, sp = _np(seqs, np.uint32)
+        c, cp = _np(counts, np.uint32)
+        out = np.zeros(int(c.sum()) * n_layers, np.uint32)
+        check(lib.qvkv_pool_plan_append_layers(self.handle, sp, cp, s.size, layer0, n_layers,
+                                               out.ctypes.data_as(ctypes.c_void_p),
+                                               self._copy_stream(stream)))
+        return out
+
     def plan_attention(self, seqs, pos, epochs, layer, stream=None):
         """attention_plan of one pass (qvkv_pool_plan_attention): returns a dict with
         blocks, table_at, pos, new_slot, sync_to, sync_item, sync_pos."""

@@ -309,3 +309,61 @@ def test_a_dropped_sync_row_is_caught(hip):
     e = attn_errors(got, want)
     assert not (e[0] <= MAX_ABS and e[1] <= REL_L2), e
     buf.close()
+
+
+def test_copy_on_write_over_layers_in_one_launch(hip):
+    """Children forked from a prefix whose last block is partly filled append on every
+    layer through one qvkv_pool_plan_append_layers call: one copy-on-write launch,
+    ordered after the prefix appends on torch's stream (one stream wait); every child then
+    reads the prefix and its own rows bit for bit, and the parent is unchanged."""
+    import torch
+
+    from qubivex_amd import KvLayout, KvPool
+
+    NL, G, D, B = 4, 8, 128, 16
+    L = KvLayout("f16", G, D, B)
+    N = 256
+    pool = KvPool(hip, L, N, NL)
+    mem = pool.memory
+    gen = torch.Generator(device="cuda").manual_seed(9)
+    hip.gather_host(L, pool.buffer, [0], [0], [16], [0], 4096)  # grow the staging first
+
+    def t32(a):
+        return torch.from_numpy(np.ascontiguousarray(a, np.uint32).view(np.int32)).cuda()
+
+    def read(seq, l):
+        blocks, table_at, pos = pool.tables([seq], l)
+        n = int(pos[0]) + 1
+        ok = torch.empty(n * G * D, dtype=torch.float16, device="cuda")
+        ov = torch.empty_like(ok)
+        hip.gather(L, mem, N, t32(blocks), t32(table_at), t32([n]),
+                   torch.zeros(1, dtype=torch.int64, device="cuda"), n, ok, ov, out_dtype="f16")
+        hip.check()
+        return ok.view(G, n, D), ov.view(G, n, D)
+
+    def heads(x):
+        return x.view(-1, G, D).permute(1, 0, 2).half()
+
+    P, DIV, S = 2 * B + 7, 20, 3
+    parent = pool.create()
+    slots = pool.plan_append_layers([parent], [P], 0, NL)
+    pk = torch.randn((slots.size, G * D), generator=gen, device="cuda")
+    pv = torch.randn_like(pk)
+    hip.append(L, mem, N, pk, pv, t32(slots))  # queued: the copies must wait for it
+    kids = [pool.fork(parent, P) for _ in range(S)]
+    waits = hip.transfers()["stream_waits"]
+    slots = pool.plan_append_layers(kids, [DIV] * S, 0, NL)
+    assert hip.transfers()["stream_waits"] == waits + 1
+    assert pool.stats()["cow_copies"] == S * NL
+    kk = torch.randn((slots.size, G * D), generator=gen, device="cuda")
+    kv = torch.randn_like(kk)
+    hip.append(L, mem, N, kk, kv, t32(slots))
+    for l in range(NL):
+        rk, rv = read(parent, l)
+        assert torch.equal(rk, heads(pk[l * P:(l + 1) * P])) and torch.equal(rv, heads(pv[l * P:(l + 1) * P]))
+        for i, c in enumerate(kids):
+            ck, cv = read(c, l)
+            own = slice((l * S + i) * DIV, (l * S + i + 1) * DIV)
+            assert torch.equal(ck[:, :P], rk) and torch.equal(cv[:, :P], rv), (l, i)
+            assert torch.equal(ck[:, P:], heads(kk[own])) and torch.equal(cv[:, P:], heads(kv[own])), (l, i)
+    pool.close()

@@ -401,3 +401,36 @@ def test_compaction_of_a_full_pool_with_cycles_needs_a_spare():
     with pytest.raises(OutOfDeviceMemory):
         p.compact(seed=5)  # a permutation of a full pool has cycles and no spare
     assert p.compact(seed=0) == 0  # ascending order: nothing to move
+
+
+def test_plan_over_layers_equals_per_layer_plans_in_one_batch():
+    """qvkv_pool_plan_append_layers gives the slots and copy-on-write pairs of one
+    plan_append per layer (layer-major), with every layer's copies in one batch; on a dry
+    pool it fails with nothing changed."""
+    from qubivex_amd import OutOfDeviceMemory
+
+    NL = 3
+    a, b = host_pool(200, NL), host_pool(200, NL)
+    for p in (a, b):
+        par = p.create()
+        for l in range(NL):
+            p.plan_append([par], [2 * B + 5], l)  # a shared partial last block per layer
+        kids = [p.fork(par, 2 * B + 5) for _ in range(3)]
+        p.take_batches()
+    kids = [1, 2, 3]
+    counts = [4, 20, 1]
+    per_layer = np.concatenate([a.plan_append(kids, counts, l) for l in range(NL)])
+    batches_a = a.take_batches()
+    together = b.plan_append_layers(kids, counts, 0, NL)
+    batches_b = b.take_batches()
+    assert np.array_equal(per_layer, together)
+    assert len(batches_a) == NL and len(batches_b) == 1
+    assert np.array_equal(np.concatenate([s for s, _ in batches_a]), batches_b[0][0])
+    assert np.array_equal(np.concatenate([d for _, d in batches_a]), batches_b[0][1])
+    for l in range(NL):
+        assert [x.tolist() for x in a.tables(kids, l)] == [x.tolist() for x in b.tables(kids, l)]
+    # dry: the last layer cannot grow, so no layer changes
+    before = [b.tables(kids, l)[0].tolist() for l in range(NL)], b.stats()["free"]
+    with pytest.raises(OutOfDeviceMemory):
+        b.plan_append_layers(kids, [B * 60] * 3, 0, NL)
+    assert ([b.tables(kids, l)[0].tolist() for l in range(NL)], b.stats()["free"]) == before
