@@ -63,9 +63,9 @@ hipError_t launch_prelude(float *q, float *k, float *v, uint32_t s, uint32_t hea
 
 // Attention: the launch plan decides the split over the context and the workspace.
 struct AttnPlan {
-    int kind;           // 0: MFMA kernel, 1: generic kernel
+    int kind;           // 0: MFMA kernel, 1: generic kernel, 2: MFMA split by work
     uint32_t hc;        // head chunks of <= 8 query heads per KV head
-    uint32_t n_chunks;  // context chunks per (item, kv head, head chunk)
+    uint32_t n_chunks;  // context chunks per (item, kv head, head chunk); kind 2: workgroups
     uint32_t tpc;       // 16-position tiles per chunk
     uint64_t ws_bytes;  // workspace for partial results (0 when n_chunks == 1)
 };

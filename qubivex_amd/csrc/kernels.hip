@@ -791,6 +791,14 @@ __global__ __launch_bounds__(256) void k_block_copy(uint8_t *__restrict__ pool,
 
 template <int D, bool Q8, bool NT, bool PK>
 __device__ __forceinline__ void attn_body(QV_ATTN_PARAMS);
+template <int D, bool Q8, bool NT, bool PK>
+__device__ __forceinline__ void attn_unit(const uint8_t *__restrict__ pool, uint64_t pool_blocks,
+                                          const float *__restrict__ q,
+                                          const uint32_t *__restrict__ blocks, uint32_t H,
+                                          const Geo &geo, int *err, uint32_t item, uint32_t g,
+                                          uint32_t hc, uint32_t n, uint32_t tab, uint32_t t_begin,
+                                          uint32_t t_end, float *o_base, uint64_t o_stride,
+                                          float *ml_base, uint64_t ml_stride);
 
 template <int D, bool Q8, bool NT, bool PK>
 __global__ __launch_bounds__(256) void k_attn_mfma(QV_ATTN_PARAMS) {
@@ -806,10 +814,6 @@ void k_attn_mfma_w(QV_ATTN_PARAMS) {
 
 template <int D, bool Q8, bool NT, bool PK>
 __device__ __forceinline__ void attn_body(QV_ATTN_PARAMS) {
-    constexpr int NJ = D / 16;  // MFMA steps over d
-    __shared__ float sm[4][8], sl[4][8];
-    __shared__ float so[4][8][D];
-
     const uint32_t G = (uint32_t)geo.G, B = (uint32_t)geo.B;
     const uint32_t GS = H / G;
     // Workgroups are dealt to the 8 XCDs round-robin (id % 8).  With xcd_map set, logical
@@ -844,6 +848,37 @@ __device__ __forceinline__ void attn_body(QV_ATTN_PARAMS) {
     const uint32_t t_end = min(ntiles, t_begin + tpc);
     if (t_begin >= t_end) return;
 
+    const uint64_t oh0 = (uint64_t)item * H + (uint64_t)g * GS + hc * 8;
+    if (n_chunks == 1) {
+        attn_unit<D, Q8, NT, PK>(pool, pool_blocks, q, blocks, H, geo, err, item, g, hc, n, tab,
+                                 t_begin, t_end, out + oh0 * D, D, nullptr, 0);
+    } else {
+        float *ml = ws + (uint64_t)n_items * H * n_chunks * D;
+        attn_unit<D, Q8, NT, PK>(pool, pool_blocks, q, blocks, H, geo, err, item, g, hc, n, tab,
+                                 t_begin, t_end, ws + (oh0 * n_chunks + chunk) * D,
+                                 (uint64_t)n_chunks * D, ml + (oh0 * n_chunks + chunk) * 2,
+                                 (uint64_t)n_chunks * 2);
+    }
+}
+
+// One unit's attention: KV head g of item `item` (positions 0..n-1, table at `tab`), query
+// heads hc*8 .. hc*8+7 of its group, over 16-position tiles t_begin .. t_end-1 shared out to
+// the 4 waves.  Head hh's result goes to o_base[hh * o_stride + d]: the output (ml_base
+// null) or, for part of the context, the unnormalised partial with its max and sum at
+// ml_base[hh * ml_stride] (log2 domain).
+template <int D, bool Q8, bool NT, bool PK>
+__device__ __forceinline__ void attn_unit(const uint8_t *__restrict__ pool, uint64_t pool_blocks,
+                                          const float *__restrict__ q,
+                                          const uint32_t *__restrict__ blocks, uint32_t H,
+                                          const Geo &geo, int *err, uint32_t item, uint32_t g,
+                                          uint32_t hc, uint32_t n, uint32_t tab, uint32_t t_begin,
+                                          uint32_t t_end, float *o_base, uint64_t o_stride,
+                                          float *ml_base, uint64_t ml_stride) {
+    constexpr int NJ = D / 16;  // MFMA steps over d
+    __shared__ float sm[4][8], sl[4][8];
+    __shared__ float so[4][8][D];
+    const uint32_t G = (uint32_t)geo.G, B = (uint32_t)geo.B;
+    const uint32_t GS = H / G;
     const uint32_t lane = threadIdx.x & 63u;
     // q8_0: the wave index is made scalar so the tile loop and its address arithmetic run
     // on the scalar unit, leaving the vector ALUs to the dequantisation (cfg3 +8 %).  The
@@ -944,17 +979,205 @@ __device__ __forceinline__ void attn_body(QV_ATTN_PARAMS) {
             L = fmaf(sl[x][hh], f, L);
             O = fmaf(so[x][hh][d], f, O);
         }
-        const uint64_t oh = (uint64_t)item * H + (uint64_t)g * GS + hi2;
-        if (n_chunks == 1) {
-            out[oh * D + d] = O / L;
+        if (!ml_base) {
+            o_base[hh * o_stride + d] = O / L;
         } else {
-            ws[(oh * n_chunks + chunk) * D + d] = O;
+            o_base[hh * o_stride + d] = O;
             if (d == 0) {
-                float *ml = ws + (uint64_t)n_items * H * n_chunks * D;
-                ml[(oh * n_chunks + chunk) * 2] = M;
-                ml[(oh * n_chunks + chunk) * 2 + 1] = L;
+                ml_base[hh * ml_stride] = M;
+                ml_base[hh * ml_stride + 1] = L;
             }
         }
+    }
+    __syncthreads();  // the LDS above is free for the workgroup's next unit
+}
+
+
+// ---------------------------------------------------------------------------------
+// Decode attention split by work, for launches with few units (one layer of a decode step
+// in model order): the (unit, tile) pairs of every item, unit-major, are shared out evenly
+// to the P workgroups, so ragged contexts leave no partial rounds of workgroups.  Each
+// workgroup works through its range unit by unit: a unit wholly inside the range is
+// written out directly; a unit cut by a range boundary leaves a partial in the
+// workgroup's slot 0 (its first unit) or 1 (its last), merged by k_attn_stream_merge.
+// Each workgroup computes the units' prefix sums itself from pos (n_items <= 2048).
+// Workspace: partials [P][2][8][D], their (max, sum) [P][2][8][2], then the prefix sums
+// [n_items + 1] (u64, written by workgroup 0 for the merge).
+// ---------------------------------------------------------------------------------
+constexpr uint32_t STREAM_MAX_ITEMS = 2048;
+
+// Unit-tiles of every item before item i (cum[i]) and in total (cum[n_items]).  Items with
+// a position past max_pos or a table too short count no tiles (and are reported).
+__device__ __forceinline__ void stream_prefix(uint64_t *cum, const uint32_t *__restrict__ pos,
+                                              const uint32_t *__restrict__ table_at,
+                                              uint64_t n_table, uint32_t n_items,
+                                              uint32_t max_pos, uint32_t per_unit_heads,
+                                              uint32_t B, int *err) {
+    __shared__ uint64_t part[256];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t per = (n_items + 255) / 256;  // <= 8
+    uint64_t loc[8], sum = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < 8; k++) {
+        const uint32_t i = tid * per + k;
+        uint64_t v = 0;
+        if (k < per && i < n_items) {
+            const uint32_t pl = pos[i];
+            if (pl > max_pos) {
+                if (blockIdx.x == 0) flag(err, ERR_POS);
+            } else if ((uint64_t)table_at[i] + (pl + B) / B > n_table) {
+                if (blockIdx.x == 0) flag(err, ERR_TABLE);
+            } else {
+                v = (uint64_t)((pl + 16) / 16) * per_unit_heads;
+            }
+        }
+        loc[k] = v;
+        sum += v;
+    }
+    part[tid] = sum;
+    __syncthreads();
+    for (uint32_t off = 1; off < 256; off <<= 1) {
+        const uint64_t v = tid >= off ? part[tid - off] : 0;
+        __syncthreads();
+        part[tid] += v;
+        __syncthreads();
+    }
+    uint64_t base = tid ? part[tid - 1] : 0;
+#pragma unroll
+    for (uint32_t k = 0; k < 8; k++) {
+        const uint32_t i = tid * per + k;
+        if (k < per && i < n_items) cum[i] = base;
+        base += loc[k];
+    }
+    if (tid == 0) cum[n_items] = part[255];
+    __syncthreads();
+}
+
+// The item whose range [cum[i], cum[i+1]) holds x (x < cum[n_items]).
+__device__ __forceinline__ uint32_t stream_item(const uint64_t *cum, uint32_t n_items, uint64_t x) {
+    uint32_t lo = 0, hi = n_items;  // cum[lo] <= x < cum[hi]
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) / 2;
+        if (cum[mid] <= x) lo = mid; else hi = mid;
+    }
+    return lo;
+}
+
+#define QV_STREAM_PARAMS                                                                        \
+    const uint8_t *__restrict__ pool, uint64_t pool_blocks, const float *__restrict__ q,        \
+        const uint32_t *__restrict__ blocks, uint64_t n_table,                                  \
+        const uint32_t *__restrict__ table_at, const uint32_t *__restrict__ pos,                \
+        uint32_t n_items, uint32_t H, uint32_t max_pos, float *__restrict__ out,                \
+        float *__restrict__ ws, uint32_t hc_n, Geo geo, int *err
+
+// A value every lane holds alike, moved to scalar registers.
+__device__ __forceinline__ uint32_t uni(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ uint64_t uni(uint64_t v) {
+    return (uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32)) << 32 |
+           __builtin_amdgcn_readfirstlane((uint32_t)v);
+}
+
+template <int D, bool Q8, bool NT, bool PK>
+__device__ __forceinline__ void attn_stream_body(QV_STREAM_PARAMS) {
+    __shared__ uint64_t cum[STREAM_MAX_ITEMS + 1];
+    const uint32_t G = (uint32_t)geo.G, B = (uint32_t)geo.B;
+    const uint32_t GS = H / G;
+    const uint32_t upi = G * hc_n;  // units per item
+    stream_prefix(cum, pos, table_at, n_table, n_items, max_pos, upi, B, err);
+    const uint64_t T = uni(cum[n_items]);
+    const uint32_t P = gridDim.x, w = blockIdx.x;
+    const uint64_t s0 = (uint64_t)w * T / P, s1 = (uint64_t)(w + 1) * T / P;
+    float *ml = ws + (uint64_t)P * 2 * 8 * D;
+    if (w == 0) {  // the prefix sums, for the merge
+        uint64_t *wc = (uint64_t *)(ml + (uint64_t)P * 2 * 8 * 2);
+        for (uint32_t i = threadIdx.x; i <= n_items; i += 256) wc[i] = cum[i];
+    }
+    bool first = true;
+    for (uint64_t x = s0; x < s1;) {
+        const uint32_t item = uni(stream_item(cum, n_items, x));
+        const uint64_t c0 = uni(cum[item]);
+        const uint64_t per_unit = (uni(cum[item + 1]) - c0) / upi;  // tiles of the item
+        const uint64_t rel = x - c0;
+        const uint32_t ul = (uint32_t)(rel / per_unit);  // unit within the item
+        const uint32_t g = ul / hc_n, hc = ul % hc_n;
+        const uint32_t t0 = (uint32_t)(rel - (uint64_t)ul * per_unit);
+        const uint64_t unit_end = c0 + (uint64_t)(ul + 1) * per_unit;
+        const uint64_t seg_end = unit_end < s1 ? unit_end : s1;
+        const uint32_t t1 = t0 + (uint32_t)(seg_end - x);
+        const uint32_t n = uni(pos[item]) + 1, tab = uni(table_at[item]);
+        const uint64_t oh0 = (uint64_t)item * H + (uint64_t)g * GS + hc * 8;
+        if (t0 == 0 && seg_end == unit_end) {
+            attn_unit<D, Q8, NT, PK>(pool, pool_blocks, q, blocks, H, geo, err, item, g, hc, n,
+                                     tab, t0, t1, out + oh0 * D, D, nullptr, 0);
+        } else {
+            const uint64_t slot = 2ull * w + (first ? 0u : 1u);
+            attn_unit<D, Q8, NT, PK>(pool, pool_blocks, q, blocks, H, geo, err, item, g, hc, n,
+                                     tab, t0, t1, ws + slot * 8 * D, D, ml + slot * 8 * 2, 2);
+        }
+        first = false;
+        x = seg_end;
+    }
+}
+
+template <int D, bool Q8, bool NT, bool PK>
+__global__ __launch_bounds__(256) void k_attn_stream(QV_STREAM_PARAMS) {
+    attn_stream_body<D, Q8, NT, PK>(pool, pool_blocks, q, blocks, n_table, table_at, pos, n_items,
+                                    H, max_pos, out, ws, hc_n, geo, err);
+}
+template <int D, bool Q8, bool NT, bool PK, int W>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W)))
+void k_attn_stream_w(QV_STREAM_PARAMS) {
+    attn_stream_body<D, Q8, NT, PK>(pool, pool_blocks, q, blocks, n_table, table_at, pos, n_items,
+                                    H, max_pos, out, ws, hc_n, geo, err);
+}
+
+// Merge for k_attn_stream: block = one (item, query head), D threads.  The unit's
+// range [a, b) of the work order lies in workgroups w0 .. w1; with w0 == w1 it was
+// written out whole.  Workgroup w's partial of it is in slot 1 when the unit starts
+// inside w's range after its first unit, else in slot 0; workgroups between them with
+// an empty range (more workgroups than tiles) hold none.  The same bookkeeping is
+// restated in tests/test_attention_split.py and checked there on random shapes.
+__global__ __launch_bounds__(256) void k_attn_stream_merge(const float *__restrict__ ws,
+                                                           uint32_t n_items, uint32_t H,
+                                                           uint32_t G, uint32_t hc_n,
+                                                           uint32_t P, uint32_t D,
+                                                           float *__restrict__ out) {
+    const uint32_t oh = blockIdx.x;
+    const uint32_t item = oh / H, h = oh % H;
+    if (item >= n_items) return;
+    const float *ml = ws + (uint64_t)P * 2 * 8 * D;
+    const uint64_t *cum = (const uint64_t *)(ml + (uint64_t)P * 2 * 8 * 2);
+    const uint64_t T = cum[n_items];
+    const uint32_t upi = G * hc_n, GS = H / G;
+    const uint64_t per_unit = (cum[item + 1] - cum[item]) / upi;
+    if (per_unit == 0 || T == 0) return;
+    const uint32_t g = h / GS, hin = h % GS, hc = hin / 8, hh = hin % 8;
+    const uint64_t a = cum[item] + (uint64_t)(g * hc_n + hc) * per_unit, b = a + per_unit;
+    // workgroup holding position x: the largest w with floor(w T / P) <= x
+    auto owner = [&](uint64_t x) { return (uint32_t)(((x + 1) * P + T - 1) / T - 1); };
+    const uint32_t w0 = owner(a), w1 = owner(b - 1);
+    if (w0 == w1) return;
+    const uint64_t start0 = (uint64_t)w0 * T / P;
+    // workgroups with an empty range (more workgroups than tiles) hold no partial
+    auto empty = [&](uint32_t w) { return (uint64_t)w * T / P == (uint64_t)(w + 1) * T / P; };
+    float M = -INFINITY;
+    for (uint32_t w = w0; w <= w1; w++) {
+        if (empty(w)) continue;
+        const uint64_t slot = 2ull * w + ((w == w0 && a != start0) ? 1u : 0u);
+        M = fmaxf(M, ml[(slot * 8 + hh) * 2]);
+    }
+    const float Ms = M == -INFINITY ? 0.0f : M;
+    for (uint32_t d = threadIdx.x; d < D; d += blockDim.x) {
+        float L = 0.0f, O = 0.0f;
+        for (uint32_t w = w0; w <= w1; w++) {
+            if (empty(w)) continue;
+            const uint64_t slot = 2ull * w + ((w == w0 && a != start0) ? 1u : 0u);
+            const float mc = ml[(slot * 8 + hh) * 2];
+            const float f = mc == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mc - Ms);
+            L = fmaf(ml[(slot * 8 + hh) * 2 + 1], f, L);
+            O = fmaf(ws[(slot * 8 + hh) * D + d], f, O);
+        }
+        out[(uint64_t)oh * D + d] = O / L;
     }
 }
 
@@ -1212,12 +1435,25 @@ int plan_attention(const Geometry &g, uint32_t n_items, uint32_t heads, uint32_t
     const uint64_t units = (uint64_t)n_items * g.G * p->hc;
     const uint64_t max_tiles = ((uint64_t)max_pos + 1 + 15) / 16;
     // workgroups to aim for: 8 per CU keeps all 256 CUs busy
-    // Split the context into chunks only when the launch is too small to fill the chip
-    // with one workgroup per unit (below 2 per CU); then aim for about 6 per CU.
-    // Measured per layer (one launch per layer): the 512 units of 128 x 8k (4 KV heads)
-    // and of cfg3's 64 x 2048 q8_0 (8 KV heads) run best unsplit; cfg2's 256 ragged units
-    // best near 1536 chunks.
+    // Launches too small to fill the chip with one workgroup per unit (below 2 per CU) are
+    // split.  By work (k_attn_stream, the default): every workgroup gets an equal share
+    // of the (unit, tile) pairs, whatever the contexts; 768 workgroups (3 per CU, one
+    // round).  Measured per layer of cfg2 (256 ragged units): 4.21 TB/s, against 3.77 for
+    // the best context-chunk split and 3.98 / 3.48 with 512 / 1024 workgroups.  Launches of
+    // 512 units and more (a layer of 128 x 8k, or of cfg3) run best unsplit: 6.0 and 4.8
+    // TB/s, against 5.7 and 3.3-4.3 split by work.
     const uint64_t full = (uint64_t)tune("QVKV_ATTN_FULL", 512);
+    if (tune("QVKV_ATTN_STREAM", 1) != 0 && units < full && n_items <= STREAM_MAX_ITEMS) {
+        const uint64_t work = units * max_tiles;  // bound: the actual work is known on the device
+        uint64_t wgs = (uint64_t)tune("QVKV_ATTN_STREAM_WG", 768);
+        if (wgs > (work + 3) / 4) wgs = (work + 3) / 4;  // at least a tile per wave
+        if (wgs < 1) wgs = 1;
+        p->kind = 2;
+        p->n_chunks = (uint32_t)wgs;
+        p->ws_bytes = wgs * 2 * 8 * (g.D + 2) * 4 + ((uint64_t)n_items + 1) * 8;
+        return QVKV_OK;
+    }
+    // Else (QVKV_ATTN_STREAM=0) into context chunks, aiming at about 6 workgroups per CU.
     const uint64_t target = (uint64_t)tune("QVKV_ATTN_TARGET", 1536);
     uint64_t nch = units >= full ? 1 : (target + units - 1) / units;
     const uint64_t cap = (max_tiles + 3) / 4;  // at least one tile per wave
@@ -1251,8 +1487,44 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
                                max_pos, out, geo, err);
         return hipGetLastError();
     }
-    const uint64_t grid = (uint64_t)n_items * g.G * p.hc * p.n_chunks;
     float *wsf = (float *)ws;
+    const bool q8 = g.dtype == QVKV_Q8_0;
+    const bool w4 = tune(q8 ? "QVKV_ATTN_WAVES4_Q8" : "QVKV_ATTN_WAVES4_F16", q8 ? 1 : 0) != 0;
+    // q8_0 with <= 4 query heads per KV head: two groups' probabilities per A operand
+    const bool pk = q8 && heads / (uint32_t)g.G <= 4 && tune("QVKV_ATTN_PACK", 1) != 0;
+    if (p.kind == 2) {
+        const unsigned P = p.n_chunks;
+#define QV_AS(DD, QQ, PK)                                                                       \
+    hipLaunchKernelGGL((k_attn_stream<DD, QQ, true, PK>), dim3(P), dim3(256), 0, s, pp,          \
+                       pool_blocks, q, blocks, n_table, table_at, pos, n_items, heads, max_pos,  \
+                       out, wsf, p.hc, geo, err)
+#define QV_AS_W4(DD, QQ, PK)                                                                    \
+    hipLaunchKernelGGL((k_attn_stream_w<DD, QQ, true, PK, 4>), dim3(P), dim3(256), 0, s, pp,     \
+                       pool_blocks, q, blocks, n_table, table_at, pos, n_items, heads, max_pos,  \
+                       out, wsf, p.hc, geo, err)
+        if (g.D == 64) {
+            if (!q8) QV_AS(64, false, false);
+            else if (pk) QV_AS(64, true, true);
+            else QV_AS(64, true, false);
+        } else if (g.D == 128) {
+            if (!q8) { if (w4) QV_AS_W4(128, false, false); else QV_AS(128, false, false); }
+            else if (pk) { if (w4) QV_AS_W4(128, true, true); else QV_AS(128, true, true); }
+            else { if (w4) QV_AS_W4(128, true, false); else QV_AS(128, true, false); }
+        } else {
+            if (!q8) QV_AS(256, false, false);
+            else if (pk) QV_AS(256, true, true);
+            else QV_AS(256, true, false);
+        }
+#undef QV_AS_W4
+#undef QV_AS
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(k_attn_stream_merge, dim3(n_items * heads), dim3(g.D), 0, s,
+                           (const float *)ws, n_items, heads, (uint32_t)g.G, p.hc, P,
+                           (uint32_t)g.D, out);
+        return hipGetLastError();
+    }
+    const uint64_t grid = (uint64_t)n_items * g.G * p.hc * p.n_chunks;
     // K/V tiles are streamed with non-temporal loads (read once).
     // Occupancy: `mode` 0 is the compiler's register choice (3 waves/SIMD at d=128), 4
     // holds the kernel to 4 waves per SIMD (125 VGPRs, no spill).  Measured (cfg5 f16,
@@ -1268,10 +1540,6 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
     hipLaunchKernelGGL((k_attn_mfma_w<DD, QQ, true, PK, 4>), dim3((unsigned)grid), dim3(256),   \
                        0, s, pp, pool_blocks, q, blocks, n_table, table_at, pos, n_items,       \
                        heads, max_pos, out, wsf, p.hc, p.n_chunks, p.tpc, geo, err)
-    const bool q8 = g.dtype == QVKV_Q8_0;
-    const bool w4 = tune(q8 ? "QVKV_ATTN_WAVES4_Q8" : "QVKV_ATTN_WAVES4_F16", q8 ? 1 : 0) != 0;
-    // q8_0 with <= 4 query heads per KV head: two groups' probabilities per A operand
-    const bool pk = q8 && heads / (uint32_t)g.G <= 4 && tune("QVKV_ATTN_PACK", 1) != 0;
     if (g.D == 64) {
         if (!q8) QV_ATTN(64, false, false);
         else if (pk) QV_ATTN(64, true, true);

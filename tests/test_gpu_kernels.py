@@ -282,8 +282,12 @@ def test_attention_ignores_nan_in_unwritten_slots(hip, dtype):
     assert e[0] <= MAX_ABS and e[1] <= REL_L2, e
 
 
-def test_attention_split_context_8k(hip):
-    """One long item alone: the launch splits the context and merges the partials."""
+@pytest.mark.parametrize("split", ["work", "chunks"])
+def test_attention_split_context_8k(hip, split, monkeypatch):
+    """One long item alone: the launch splits the context (by work, the default, or into
+    context chunks) and merges the partials."""
+    if split == "chunks":
+        monkeypatch.setenv("QVKV_ATTN_STREAM", "0")
     r = rng(7)
     L = layout(F16, 4, 128)
     lens = [8192]
@@ -299,6 +303,33 @@ def test_attention_split_context_8k(hip):
     want = sim.attention(q, 32, blocks, table_at, pos)
     max_abs, rel = attn_errors(got, want)
     print(f"  8k split: max_abs={max_abs:.2e} rel_l2={rel:.2e}", flush=True)
+    assert max_abs <= MAX_ABS and rel <= REL_L2
+
+
+@pytest.mark.parametrize("dtype", [F16, Q8_0])
+@pytest.mark.parametrize("split", ["work", "chunks"])
+def test_attention_split_ragged_batch(hip, dtype, split, monkeypatch):
+    """A small ragged batch (one layer of a decode step in model order: 24 items of 1 to
+    3000 positions, 8 KV heads, so 192 units): split by work, units are cut across
+    workgroup ranges at arbitrary tiles and merged; both split forms against the oracle."""
+    if split == "chunks":
+        monkeypatch.setenv("QVKV_ATTN_STREAM", "0")
+    r = rng(71 + (dtype == Q8_0))
+    L = layout(dtype, 8, 128)
+    lens = [int(x) for x in r.integers(1, 3000, 24)]
+    lens[0], lens[1] = 1, 16
+    N = sum((n + 15) // 16 for n in lens) + 4
+    pool = new_pool(L, N)
+    blocks, table_at, sim = fill_items(hip, L, pool, N, lens, r)
+    q = normal(r, (len(lens), 32, 128))
+    pos = np.array(lens, np.uint32) - 1
+    out = torch.full((len(lens) * 32 * 128,), float("nan"), dtype=torch.float32, device="cuda")
+    hip.attention(L, pool, N, cf32(q), cu32(blocks), cu32(table_at), cu32(pos), 32,
+                  int(pos.max()), out)
+    hip.check()
+    got = out.cpu().numpy().reshape(len(lens), 32, 128)
+    max_abs, rel = attn_errors(got, sim.attention(q, 32, blocks, table_at, pos))
+    print(f"  ragged {dtype} {split}: max_abs={max_abs:.2e} rel_l2={rel:.2e}", flush=True)
     assert max_abs <= MAX_ABS and rel <= REL_L2
 
 

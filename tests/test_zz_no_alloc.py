@@ -65,9 +65,10 @@ def test_noalloc_attention_equals_the_allocating_form(hip, dtype):
 def test_noalloc_attention_refuses_a_launch_past_its_scratch(hip, monkeypatch):
     from qubivex_amd import KvLayout, ShapeError, _lib
 
-    # a tiny launch over a long context with a forced split target: partials of 8 heads x
-    # 1024 chunks x 258 floats per item need more than the scratch array holds
-    monkeypatch.setenv("QVKV_ATTN_TARGET", "100000")
+    # a tiny launch over a long context split by work over as many workgroups as it has
+    # 4-tile shares (8192 here): 2 partial slots x 8 heads x 258 floats per workgroup need
+    # more than the scratch array holds
+    monkeypatch.setenv("QVKV_ATTN_STREAM_WG", "100000")
     L = KvLayout("f16", 1, 256, 16)
     q = torch.zeros((8, 8, 256), device="cuda")
     out = torch.zeros_like(q)
