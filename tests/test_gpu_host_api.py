@@ -367,3 +367,47 @@ def test_copy_on_write_over_layers_in_one_launch(hip):
             assert torch.equal(ck[:, :P], rk) and torch.equal(cv[:, :P], rv), (l, i)
             assert torch.equal(ck[:, P:], heads(kk[own])) and torch.equal(cv[:, P:], heads(kv[own])), (l, i)
     pool.close()
+
+
+def test_empty_batches_are_no_ops(hip):
+    """Every entry point takes an empty batch (no rows, items, segments or pairs) and
+    touches nothing: the pool's bytes are unchanged and the error flags stay clear."""
+    import ctypes
+
+    import torch
+
+    from qubivex_amd import KvLayout, _lib
+
+    L = KvLayout("f16", 2, 64, 16)
+    N = 4
+    pool = torch.full((N * L.block_bytes,), 7, dtype=torch.uint8, device="cuda")
+    lib, lay, dev = _lib.lib, ctypes.byref(L.c), hip.handle
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    p = ctypes.c_void_p(pool.data_ptr())
+    some = torch.zeros(64, dtype=torch.float32, device="cuda")
+    sp = ctypes.c_void_p(some.data_ptr())
+    calls = [
+        lambda: lib.qvkv_append_async(dev, lay, p, N, sp, sp, sp, 0, st),
+        lambda: lib.qvkv_gather_async(dev, lay, p, N, sp, 0, sp, sp, sp, 0, 0, _lib.F32, 0, sp, sp, st),
+        lambda: lib.qvkv_attention_async(dev, lay, p, N, sp, sp, 0, sp, sp, 0, 4, 0, sp, st),
+        lambda: lib.qvkv_attention_noalloc_async(dev, lay, p, N, sp, sp, 0, sp, sp, 0, 4, 0, sp, st),
+        lambda: lib.qvkv_prefill_attention_async(dev, lay, p, N, sp, 0, sp, 0, sp, sp, sp, sp, 0, 4,
+                                                 0, 0, sp, st),
+        lambda: lib.qvkv_block_copy_async(dev, lay, p, N, sp, sp, 0, st),
+    ]
+    for call in calls:
+        _lib.check(call())
+    buf = hip.alloc(N * L.block_bytes)
+    hip.write(buf, 0, bytes([7]) * (N * L.block_bytes))
+    hip.append_host(L, buf, np.zeros((0, L.kv_out), np.float32), np.zeros((0, L.kv_out), np.float32),
+                    np.zeros(0, np.uint32))
+    hip.block_copy_host(L, buf, [], [])
+    empty = np.zeros(0, np.uint32)
+    out = hip.decode_attention(L, buf, np.zeros((0, 4, 64), np.float32), 4, empty, empty, empty,
+                               np.zeros(0, np.float32), empty, np.zeros((0, L.kv_out), np.float32),
+                               np.zeros((0, L.kv_out), np.float32))
+    assert out.shape == (0, 4, 64)
+    hip.check()
+    assert hip.read(buf, 0, N * L.block_bytes) == bytes([7]) * (N * L.block_bytes)
+    assert int((pool != 7).sum()) == 0
+    buf.close()

@@ -434,3 +434,18 @@ def test_plan_over_layers_equals_per_layer_plans_in_one_batch():
     with pytest.raises(OutOfDeviceMemory):
         b.plan_append_layers(kids, [B * 60] * 3, 0, NL)
     assert ([b.tables(kids, l)[0].tolist() for l in range(NL)], b.stats()["free"]) == before
+
+
+def test_zero_counts_and_empty_plans_change_nothing():
+    """Plans over no sequences, or with zero new positions, take no block and issue no
+    copy; a fork of zero positions shares nothing."""
+    p = host_pool(16, 2)
+    s = p.create()
+    assert p.plan_append([], [], 0).size == 0
+    assert p.plan_append([s], [0], 1).size == 0
+    assert p.plan_append_layers([s], [0], 0, 2).size == 0
+    assert p.stats()["free"] == 16 and p.take_batches() == []
+    p.plan_append([s], [B + 3], 0)
+    kid = p.fork(s, 0)
+    assert p.length(kid, 0) == 0 and p.stats()["shared_blocks"] == 0
+    assert p.compact(mode="fill") == 0 and p.compact() == 0  # live blocks are 0 and 1 already
