@@ -443,9 +443,11 @@ __global__ __launch_bounds__(256) void k_gather(const uint8_t *__restrict__ pool
                                                 const uint64_t *__restrict__ out_at,
                                                 uint32_t n_items, uint32_t tiles_max,
                                                 uint64_t out_positions, void *out_k,
-                                                void *out_v, Geo geo, int *err) {
-    const uint32_t item = blockIdx.x / tiles_max;
-    const uint32_t tile = blockIdx.x - item * tiles_max;
+                                                void *out_v, uint32_t parts, Geo geo, int *err) {
+    // parts workgroups share one tile (each one batch of loads and stores of it)
+    const uint32_t part = blockIdx.x % parts, bt = blockIdx.x / parts;
+    const uint32_t item = bt / tiles_max;
+    const uint32_t tile = bt - item * tiles_max;
     if (item >= n_items) return;
     const uint32_t len = lens[item];
     const uint32_t p0 = tile * 16u;
@@ -474,7 +476,7 @@ __global__ __launch_bounds__(256) void k_gather(const uint8_t *__restrict__ pool
     if (DT == QVKV_F16 && OUT == QVKV_F16) {
         // A byte copy of the tile's rows: 8 loads in flight per thread, then 8 stores.
         constexpr int U = 8;
-        for (uint32_t b0 = 0; b0 < 2u * per_kv; b0 += 256u * U) {
+        for (uint32_t b0 = part * 256u * U; b0 < 2u * per_kv; b0 += parts * 256u * U) {
             u4v x[U];
             uint16_t *dst[U];
 #pragma unroll
@@ -507,7 +509,7 @@ __global__ __launch_bounds__(256) void k_gather(const uint8_t *__restrict__ pool
         const uint32_t c4 = D >> 2;
         const uint32_t per4 = G * 16u * c4;
         constexpr int U = 8;
-        for (uint32_t b0 = 0; b0 < 2u * per4; b0 += 256u * U) {
+        for (uint32_t b0 = part * 256u * U; b0 < 2u * per4; b0 += parts * 256u * U) {
             u2v x[U];
             float *dst[U];
 #pragma unroll
@@ -538,7 +540,7 @@ __global__ __launch_bounds__(256) void k_gather(const uint8_t *__restrict__ pool
         }
         return;
     }
-    for (uint32_t idx = threadIdx.x; idx < 2u * per_kv; idx += 256u) {
+    for (uint32_t idx = part * 256u + threadIdx.x; idx < 2u * per_kv; idx += parts * 256u) {
         const bool isv = idx >= per_kv;
         uint32_t r = isv ? idx - per_kv : idx;
         const uint32_t e = (r % c8) * 8u;
@@ -1378,10 +1380,16 @@ hipError_t launch_gather(const Geometry &g, const void *pool, uint64_t pool_bloc
     const uint64_t grid = (uint64_t)tiles * n_items;
     if (grid > 0x7fffffffull) return hipErrorInvalidValue;
     const uint8_t *p = (const uint8_t *)pool;
+    // f16 tiles of many heads: several workgroups per tile, each one batch of 8 loads in
+    // flight per thread (the f16 -> f16 copy moves 8 values per load, f16 -> f32 4)
+    const uint64_t per_batch = 256ull * 8 * (out_dtype == QVKV_F16 ? 8 : 4);
+    const uint64_t vals = 2ull * g.G * 16 * g.D;
+    uint32_t parts = tune("QVKV_GATHER_SPLIT", 1) ? (uint32_t)((vals + per_batch - 1) / per_batch) : 1u;
+    if (g.dtype != QVKV_F16 || grid * parts > 0x7fffffffull) parts = 1;
 #define QV_GATHER(DT, OT)                                                                      \
-    hipLaunchKernelGGL((k_gather<DT, OT>), dim3((unsigned)grid), dim3(256), 0, s, p,           \
+    hipLaunchKernelGGL((k_gather<DT, OT>), dim3((unsigned)(grid * parts)), dim3(256), 0, s, p,  \
                        pool_blocks, blocks, n_table, table_at, lens, out_at, n_items, tiles,   \
-                       out_positions, out_k, out_v, geo, err)
+                       out_positions, out_k, out_v, parts, geo, err)
 #define QV_GATHER_Q8(DD)                                                                       \
     hipLaunchKernelGGL((k_gather_q8<DD>), dim3((unsigned)grid), dim3(256), 0, s, p,            \
                        pool_blocks, blocks, n_table, table_at, lens, out_at, n_items, tiles,   \
