@@ -24,7 +24,10 @@
  *    Kernels never touch memory outside the pool for such input.
  *  - Threads: any thread may call (the trait is Send + Sync).  The library keeps an error
  *    flag and an attention workspace per stream, so callers on different streams never
- *    see each other's errors or overwrite each other's partial results.
+ *    see each other's errors or overwrite each other's partial results.  The first launch
+ *    on a stream sets its state up (a small device allocation), and an attention launch
+ *    may grow the stream's workspace: before capturing a stream into a HIP graph, run the
+ *    launches once uncaptured (or use qvkv_attention_noalloc_async).
  *  - A pool position is `slot = block * layout.block + offset` (the reference's
  *    `sync_to`, crates/qubivex-compute/src/discrete.rs:301-304).  Item t of a batch is
  *    one (sequence, layer) pair: its blocks are blocks[table_at[t] ..], in position order

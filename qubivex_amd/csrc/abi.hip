@@ -85,7 +85,10 @@ struct qvkv_dev {
     uint64_t stage_bytes = 0;
     hipEvent_t order_ev = nullptr;  // orders pool copies after a caller's stream
     hipEvent_t t0 = nullptr, t1 = nullptr;  // GPU time of a synchronous call
-    std::mutex mu;  // serialises host-memory entry points, stream states, workspace growth
+    // host_mu: the host-memory entry points, one at a time (the staging buffer and the
+    // device stream's state are theirs); mu: the stream states and workspace growth (held
+    // briefly).  Order: host_mu before mu.
+    std::mutex host_mu, mu;
     std::atomic<uint64_t> used{0}, peak{0}, refused{0};
     std::atomic<uint64_t> uploads{0}, upload_bytes{0}, downloads{0}, download_bytes{0};
     std::atomic<uint64_t> submissions{0}, wait_ns{0}, timed{0}, gpu_ns{0}, last_gpu_ns{0};
@@ -495,7 +498,7 @@ int qvkv_write(qvkv_dev *dev, qvkv_buf *buf, size_t offset, const void *host, si
     if (offset > buf->len || len > buf->len - offset)
         return fail(QVKV_E_DEVICE, "hip device error: write of %zu bytes at %zu past a %zu-byte buffer",
                     len, offset, buf->len);
-    std::lock_guard<std::mutex> lk(dev->mu);
+    std::lock_guard<std::mutex> lk(dev->host_mu);
     if (int rc = set_device(dev)) return rc;
     hipError_t e = hipMemcpyAsync((char *)buf->ptr + offset, host, len, hipMemcpyHostToDevice,
                                   dev->stream);
@@ -512,7 +515,7 @@ int qvkv_read(qvkv_dev *dev, const qvkv_buf *buf, size_t offset, void *host, siz
     if (offset > buf->len || len > buf->len - offset)
         return fail(QVKV_E_DEVICE, "hip device error: read of %zu bytes at %zu past a %zu-byte buffer",
                     len, offset, buf->len);
-    std::lock_guard<std::mutex> lk(dev->mu);
+    std::lock_guard<std::mutex> lk(dev->host_mu);
     if (int rc = set_device(dev)) return rc;
     if (int rc = download(dev, host, (const char *)buf->ptr + offset, len)) return rc;
     hipError_t e = hipStreamSynchronize(dev->stream);
@@ -593,7 +596,10 @@ int qvkv_attention_async(qvkv_dev *dev, const qvkv_layout *layout, const void *p
         return fail(QVKV_E_SHAPE, "shape mismatch in attention: null pointer");
     if (int rc = set_device(dev)) return rc;
     // The stream's workspace is grown and handed to the launch under the device lock, so
-    // no other thread frees it in between; launches on one stream use it in turn.
+    // no other thread frees it in between; launches on one stream use it in turn.  The
+    // device's own stream is also the host-memory entry points': take their lock too.
+    std::unique_lock<std::mutex> host_lk(dev->host_mu, std::defer_lock);
+    if ((hipStream_t)stream == dev->stream) host_lk.lock();
     std::lock_guard<std::mutex> lk(dev->mu);
     StreamState *st;
     if (int rc = state_locked(dev, (hipStream_t)stream, &st)) return rc;
@@ -699,7 +705,7 @@ int qvkv_append(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *pool, const 
         if (slots[r] / g.B >= held)
             return fail(QVKV_E_SHAPE, "shape mismatch in append: slot %u is in a block past the pool's %llu",
                         slots[r], (unsigned long long)held);
-    std::lock_guard<std::mutex> lk(dev->mu);
+    std::lock_guard<std::mutex> lk(dev->host_mu);
     if (int rc = set_device(dev)) return rc;
     Stager st;
     const uint64_t rowb = g.kv_out * 4;
@@ -743,7 +749,7 @@ int qvkv_gather(qvkv_dev *dev, const qvkv_layout *layout, const qvkv_buf *pool,
         if (out_at[t] + lens[t] > out_positions)
             return fail(QVKV_E_SHAPE, "shape mismatch in gather: item %u past out_positions", t);
     }
-    std::lock_guard<std::mutex> lk(dev->mu);
+    std::lock_guard<std::mutex> lk(dev->host_mu);
     if (int rc = set_device(dev)) return rc;
     const uint64_t esz = out_dtype == QVKV_F16 ? 2 : 4;
     const uint64_t ob = out_positions * g.kv_out * esz;
@@ -883,7 +889,7 @@ int qvkv_decode_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *po
         memcpy(&sk[(uint64_t)r * g.kv_out], sync + (uint64_t)r * 2 * g.kv_out, g.kv_out * 4);
         memcpy(&sv[(uint64_t)r * g.kv_out], sync + ((uint64_t)r * 2 + 1) * g.kv_out, g.kv_out * 4);
     }
-    std::lock_guard<std::mutex> lk(dev->mu);
+    std::lock_guard<std::mutex> lk(dev->host_mu);
     if (int rc = set_device(dev)) return rc;
     if (int rc = ensure_attention(dev, dev->own, p)) return rc;
     const uint64_t rowb = g.kv_out * 4, qb = (uint64_t)s * heads * g.D * 4;
@@ -1008,7 +1014,7 @@ int qvkv_prelude_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *p
         memcpy(&sk[(uint64_t)r * g.kv_out], sync + (uint64_t)r * 2 * g.kv_out, g.kv_out * 4);
         memcpy(&sv[(uint64_t)r * g.kv_out], sync + ((uint64_t)r * 2 + 1) * g.kv_out, g.kv_out * 4);
     }
-    std::lock_guard<std::mutex> lk(dev->mu);
+    std::lock_guard<std::mutex> lk(dev->host_mu);
     if (int rc = set_device(dev)) return rc;
     if (int rc = ensure_attention(dev, dev->own, plan)) return rc;
     const uint64_t q_out = (uint64_t)heads * g.D, rowb = g.kv_out * 4, qb = s * q_out * 4;
@@ -1094,7 +1100,7 @@ int qvkv::block_copy_after(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *p
             return fail(QVKV_E_SHAPE, "shape mismatch in block copy: a block past the pool's %llu",
                         (unsigned long long)held);
     if (n == 0) return QVKV_OK;
-    std::lock_guard<std::mutex> lk(dev->mu);
+    std::lock_guard<std::mutex> lk(dev->host_mu);
     if (int rc = set_device(dev)) return rc;
     Stager st;
     uint64_t so = st.add(src, n * 4ull), dd = st.add(dst, n * 4ull);
