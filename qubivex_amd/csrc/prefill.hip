@@ -287,19 +287,51 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
     const bool vwave = w < (uint32_t)VW;
     const uint32_t vq = lane & 7u, vpiece = (lane >> 3) + 8u * w;   // V lanes
     const uint32_t kt = threadIdx.x - 64u * VW;                      // K lanes
-    // Block bases of a tile's two 16-position halves (uniform across the workgroup: each
-    // half lies inside one block since B is a multiple of 16); positions past n_wg read
-    // as zero.
-    auto half_base = [&](uint32_t ph) -> const uint8_t * {
-        if (ph >= n_wg) return nullptr;
-        // a scalar load (constant address space): it counts on lgkmcnt, so it never waits
-        // behind the vmcnt of tiles still streaming into LDS
-        const uint32_t blk = ((const __attribute__((address_space(4))) uint32_t *)blocks)[tab + ph / B];
-        if (blk >= pool_blocks) {
-            if (threadIdx.x == 0) flag(err, ERR_BLOCK);
-            return nullptr;
+    // Block bases of 16-position tile halves (each half lies inside one block since B is a
+    // multiple of 16); positions past n_wg read as zero.  The register-staged form takes
+    // both halves of every tile; in the DMA form each wave moves the chunks of one half
+    // (waves 0-1: positions 0-15 of a tile, waves 2-3: 16-31) and resolves only that one.
+    // Tiles are resolved strictly in order, one tile ahead of their use: the (block, row)
+    // split of the next half advances by counters (no division by B), and the table
+    // entries are scalar loads (constant address space: they count on lgkmcnt, never
+    // behind the vmcnt of tiles streaming into LDS) that land while a tile's math runs.
+    constexpr int NH = DMA ? 1 : 2;          // halves a wave resolves per tile
+    const uint32_t my_half = DMA ? [&]() { return __builtin_amdgcn_readfirstlane(w >> 1); }() : 0u;
+    const uint8_t *const kv_g = pool + (uint64_t)g * B * D * 2u;   // this KV head's rows
+    const uint64_t bbytes = geo.bb;
+    // every uint32 id is in range when the pool has 2^32 blocks or more
+    const bool id_check = pool_blocks <= 0xffffffffull;
+    const uint32_t pool_ids = (uint32_t)(id_check ? pool_blocks : 0ull);
+    uint32_t at_bi = 0, at_row = 0;         // block index / row of the next half to resolve
+    auto step16 = [&]() {
+        at_row += 16u;
+        if (at_row == B) {
+            at_row = 0u;
+            at_bi++;
         }
-        return pool + (uint64_t)blk * geo.bb + ((uint64_t)g * B + ph % B) * D * 2u;
+    };
+    if (my_half) step16();
+    uint32_t nx_blk[NH], nx_row[NH];
+    bool nx_in[NH];
+#pragma unroll
+    for (int k = 0; k < NH; k++) nx_blk[k] = nx_row[k] = 0u, nx_in[k] = false;
+    auto resolve = [&](uint32_t t) {        // the half (halves) of tile t, after tile t - 1
+#pragma unroll
+        for (int k = 0; k < NH; k++) {
+            nx_in[k] = t * TP + 16u * (NH == 1 ? my_half : (uint32_t)k) < n_wg;
+            nx_row[k] = at_row;
+            if (nx_in[k])
+                nx_blk[k] = ((const __attribute__((address_space(4))) uint32_t *)blocks)[tab + at_bi];
+            step16();
+            if (NH == 1) step16();          // past the other half
+        }
+    };
+    bool bad_id = false;                    // flagged once, after the tile loop
+    auto resolved = [&](int k) -> const uint8_t * {  // a base of the last resolved tile
+        const bool bad = nx_in[k] && id_check && nx_blk[k] >= pool_ids;
+        bad_id |= bad;
+        const uint8_t *b = kv_g + (uint64_t)nx_blk[k] * bbytes + nx_row[k] * (uint32_t)(D * 2);
+        return nx_in[k] && !bad ? b : nullptr;
     };
     // Row r (0..31) of the tile from the bases of its two 16-position halves; positions
     // past n_wg (r >= valid) and bad blocks read as zero.
@@ -309,9 +341,10 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
         if (b == nullptr || r >= valid) return u4v{0u, 0u, 0u, 0u};
         return *(const u4v *)(b + off);
     };
-    auto load = [&](uint32_t t) {
+    auto load = [&](uint32_t t) {  // t = 0, 1, 2, ... in order
         const uint32_t p0 = t * TP;
-        const uint8_t *b0 = half_base(p0), *b1 = half_base(p0 + 16u);
+        const uint8_t *b0 = resolved(0), *b1 = resolved(1);
+        if (t + 1 < ntiles) resolve(t + 1);
         const uint32_t valid = n_wg - p0 < (uint32_t)TP ? n_wg - p0 : (uint32_t)TP;
         const bool full = valid == (uint32_t)TP && b0 != nullptr && b1 != nullptr;  // uniform
         if (vwave) {
@@ -458,6 +491,7 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
         }
     };
 
+    resolve(0);
     if constexpr (!DMA) {
         load(0);
         store(0);
@@ -496,40 +530,47 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
         // pool offsets of the K and V parts of a block, as values (a per-lane choice
         // between two kernel-argument fields would otherwise load through a vector address)
         const uint32_t koff = (uint32_t)geo.k_off, voff = (uint32_t)geo.v_off;
-        // Per chunk u of this thread, fixed for every tile: its pool offset inside a block,
-        // and for its wave (a wave's 64 chunks are 4 (d = 128) or 8 (d = 64) consecutive LDS
-        // rows of one K or V tile, inside one 16-position half) the half, whether it is V,
-        // and the LDS offset of the wave's first chunk.  The load then takes a scalar block
-        // base plus a 32-bit lane offset.
+        // Chunk u of this thread: wave w moves group 4 (w & 1) + u of its half's 8 groups of
+        // 64 chunks (4 LDS rows each): groups 0-3 the K rows holding the half's positions
+        // (LDS rows {0-3, 4-7, 16-19, 20-23} + 8 half), 4-7 its V rows (16 half + 4 (g - 4)
+        // ..).  Fixed for every tile: the chunk's pool offset inside a block, and for the
+        // wave whether it is V and the LDS offset of its first chunk.  The load then takes
+        // the half's scalar block base plus a 32-bit lane offset.
+        static_assert(CPT == 4 && CPR == 16, "the DMA form is laid out for d = 128");
+        auto chunk_u = [&](int u) -> uint32_t {  // chunk index: K 0..CH-1, then V
+            const uint32_t gi = 4u * (w & 1u) + (uint32_t)u, hf = w >> 1;
+            const uint32_t r0 = gi < 4u ? 4u * (gi & 1u) + 16u * (gi >> 1) + 8u * hf
+                                        : 16u * hf + 4u * (gi - 4u);
+            return (gi < 4u ? 0u : (uint32_t)CH) + r0 * CPR + lane;
+        };
         // (in a lambda: the host pass of a kernel body must not see the device builtins)
-        uint32_t c_off[CPT], c_lds[CPT], c_up[CPT], c_v[CPT];
+        uint32_t c_off[CPT], c_lds[CPT], c_v[CPT];
         [&]() {
 #pragma unroll
             for (int u = 0; u < CPT; u++) {
-                const uint32_t c = threadIdx.x + 256u * u;
+                const uint32_t c = chunk_u(u);
                 uint32_t pos, piece;
                 bool isv;
                 chunk(c, pos, piece, isv);
                 c_off[u] = (isv ? voff : koff) + ((pos & 15u) * D + piece * 8) * 2u;
                 const uint32_t cc = isv ? c - CH : c;
                 c_lds[u] = __builtin_amdgcn_readfirstlane((cc - lane) * 8);
-                c_up[u] = __builtin_amdgcn_readfirstlane(pos & 16u);
                 c_v[u] = __builtin_amdgcn_readfirstlane(isv ? 1u : 0u);
             }
         }();
-        auto issue = [&](uint32_t t, DmaSlot<D> &sl) {
-            const uint32_t p0 = t * TP;
-            const uint8_t *b0 = half_base(p0), *b1 = half_base(p0 + 16u);
-            const uint32_t valid = n_wg - p0 < (uint32_t)TP ? n_wg - p0 : (uint32_t)TP;
-            const bool full = valid == (uint32_t)TP && b0 != nullptr && b1 != nullptr;  // uniform
-            if (full) {
+        auto issue = [&](uint32_t t, DmaSlot<D> &sl) {  // t = 0, 1, 2, ... in order
+            const uint8_t *hb = resolved(0);
+            if (t + 1 < ntiles) resolve(t + 1);
+            const uint32_t p0 = t * TP + 16u * my_half;   // the wave's half
+            const uint32_t valid = n_wg > p0 ? min(n_wg - p0, 16u) : 0u;
+            if (valid == 16u && hb != nullptr) {  // uniform
                 // Cached loads (aux 0): the n_cb workgroups of a (segment, KV head) read the
                 // same tiles and share them through the XCD's L2.
 #pragma unroll
                 for (int u = 0; u < CPT; u++) {
                     // (operands named first: with them inline, hipcc's host pass dropped the
                     // kernel's launch stub without a diagnostic)
-                    const uint8_t *src = (c_up[u] ? b1 : b0) + c_off[u];
+                    const uint8_t *src = hb + c_off[u];
                     _Float16 *lds_dst = (c_v[u] ? sl.v : sl.k) + c_lds[u];
                     __builtin_amdgcn_global_load_lds(src, lds_dst, 16, 0, 0);
                 }
@@ -537,14 +578,15 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
                 // past n_wg or a bad block: through registers, zeros where invalid
 #pragma unroll
                 for (int u = 0; u < CPT; u++) {
-                    const uint32_t c = threadIdx.x + 256u * u;
+                    const uint32_t c = chunk_u(u);
                     uint32_t pos, piece;
                     bool isv;
                     chunk(c, pos, piece, isv);
                     const uint32_t off = (isv ? voff : koff) + ((pos & 15u) * D + piece * 8) * 2u;
                     _Float16 *dst = isv ? sl.v : sl.k;
                     const uint32_t cc = isv ? c - CH : c;
-                    const u4v x = fetch(b0, b1, valid, pos, off);
+                    const u4v x = hb != nullptr && (pos & 15u) < valid ? *(const u4v *)(hb + off)
+                                                                       : u4v{0u, 0u, 0u, 0u};
                     *(u4v *)(dst + cc * 8) = x;
                 }
             }
@@ -607,6 +649,7 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
             if (t + 2 < ntiles) step(t + 2, s2, s1);
         }
     }
+    if (bad_id && lane == 0) flag(err, ERR_BLOCK);  // any wave: each resolves its own half
     if (!wave_live) return;
     // ---- row totals; lane (col, grp) holds O rows 4 grp + i at d = 16 j + col
     l += __shfl_xor(l, 16);
