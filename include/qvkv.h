@@ -97,6 +97,9 @@ int qvkv_last_oom(uint64_t *requested, uint64_t *used, uint64_t *capacity);
 /* Opens HIP device `device` with its own stream (constructor of the backend;
  * DiscreteDevice::name/describe: crates/qubivex-compute/src/discrete.rs:437-441). */
 int qvkv_open(int device, qvkv_dev **out);
+/* Waits for the device and releases it.  Buffers still allocated on it stay valid to
+ * free with qvkv_free (and pools to destroy) afterwards, in any order; the device's last
+ * resources go with the last of them. */
 void qvkv_close(qvkv_dev *dev);
 int qvkv_describe(const qvkv_dev *dev, char *buf, size_t len);
 /* DiscreteDevice::usage (discrete.rs:461) */

@@ -96,7 +96,17 @@ struct qvkv_dev {
     uint8_t *scratch = nullptr;  // this device's copy of `scratch` (allocation-free entry)
     int *scratch_err = nullptr;  // its error flag (the first 256 bytes)
     char name[256] = {0};
+    // The caller's handle plus one per live buffer: a buffer may be freed after
+    // qvkv_close (in any teardown order), and the struct goes with the last of them.
+    std::atomic<int> refs{1};
+    std::atomic<bool> closed{false};
 };
+
+namespace {
+void release(qvkv_dev *dev) {
+    if (dev->refs.fetch_sub(1) == 1) delete dev;
+}
+}  // namespace
 
 struct qvkv_buf {
     qvkv_dev *dev;
@@ -417,7 +427,9 @@ void qvkv_close(qvkv_dev *dev) {
     if (dev->t0) (void)hipEventDestroy(dev->t0);
     if (dev->t1) (void)hipEventDestroy(dev->t1);
     if (dev->stream) (void)hipStreamDestroy(dev->stream);
-    delete dev;
+    dev->stream = nullptr;
+    dev->closed.store(true);
+    release(dev);
 }
 
 int qvkv_describe(const qvkv_dev *dev, char *buf, size_t len) {
@@ -476,17 +488,21 @@ int qvkv_alloc(qvkv_dev *dev, size_t len, qvkv_buf **out) {
     if (int rc = set_device(dev)) return rc;
     void *p = nullptr;
     if (int rc = dev_malloc(dev, &p, len)) return rc;
+    dev->refs.fetch_add(1);
     *out = new qvkv_buf{dev, p, len};
     return QVKV_OK;
 }
 
 void qvkv_free(qvkv_buf *buf) {
     if (!buf) return;
-    (void)hipSetDevice(buf->dev->device);
-    // In-flight work on the device's stream may still read the buffer.
-    (void)hipStreamSynchronize(buf->dev->stream);
-    dev_free(buf->dev, buf->ptr, buf->len);
+    qvkv_dev *dev = buf->dev;
+    (void)hipSetDevice(dev->device);
+    // In-flight work on the device's stream may still read the buffer (a closed device
+    // was synchronized by qvkv_close).
+    if (!dev->closed.load()) (void)hipStreamSynchronize(dev->stream);
+    dev_free(dev, buf->ptr, buf->len);
     delete buf;
+    release(dev);
 }
 
 void *qvkv_buf_ptr(const qvkv_buf *buf) { return buf ? buf->ptr : nullptr; }

@@ -150,6 +150,12 @@ __global__ __launch_bounds__(256) void k_prefill_mfma(QV_PREFILL_PARAMS) {
 // are exact f16 x f16 in f32 accumulators as in decode.
 // ---------------------------------------------------------------------------------
 
+// a compile-time flag passed to a generic lambda
+template <bool V>
+struct Flag {
+    static constexpr bool value = V;
+};
+
 template <int D>
 struct PrefillLds {
     static constexpr int TP = 32;          // positions per tile
@@ -238,8 +244,13 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
     const uint32_t col = lane & 15u, grp = lane >> 4;
     const uint32_t rw0 = r0 + w * 16u;                      // the wave's first row
     const bool wave_live = rw0 < nrows;
-    const uint32_t n_wave = wave_live ? p0s + min(nt - 1, (rw0 + 15u) / GS) + 1 : 0u;
-    const uint32_t n_wave_min = wave_live ? p0s + rw0 / GS + 1 : 0u;  // first row's limit
+    // (uniform per wave: scalar, so the per-tile tests against them are scalar branches)
+    const uint32_t n_wave = [&]() {
+        return __builtin_amdgcn_readfirstlane(wave_live ? p0s + min(nt - 1, (rw0 + 15u) / GS) + 1 : 0u);
+    }();
+    const uint32_t n_wave_min = [&]() {  // the first row's limit
+        return __builtin_amdgcn_readfirstlane(wave_live ? p0s + rw0 / GS + 1 : 0u);
+    }();
     const uint32_t row = rw0 + col;
     const bool rvalid = row < nrows;
     const uint32_t tj = rvalid ? row / GS : 0u, hh = rvalid ? row % GS : 0u;
@@ -299,9 +310,9 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
     const uint32_t my_half = DMA ? [&]() { return __builtin_amdgcn_readfirstlane(w >> 1); }() : 0u;
     const uint8_t *const kv_g = pool + (uint64_t)g * B * D * 2u;   // this KV head's rows
     const uint64_t bbytes = geo.bb;
-    // every uint32 id is in range when the pool has 2^32 blocks or more
-    const bool id_check = pool_blocks <= 0xffffffffull;
-    const uint32_t pool_ids = (uint32_t)(id_check ? pool_blocks : 0ull);
+    // ids at or past pool_ids are bad (the clamp only matters for id 0xffffffff in a pool of
+    // 2^32 blocks or more, which no device holds: a block is at least 2 KiB)
+    const uint32_t pool_ids = pool_blocks > 0xffffffffull ? 0xffffffffu : (uint32_t)pool_blocks;
     uint32_t at_bi = 0, at_row = 0;         // block index / row of the next half to resolve
     auto step16 = [&]() {
         at_row += 16u;
@@ -315,10 +326,12 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
     bool nx_in[NH];
 #pragma unroll
     for (int k = 0; k < NH; k++) nx_blk[k] = nx_row[k] = 0u, nx_in[k] = false;
-    auto resolve = [&](uint32_t t) {        // the half (halves) of tile t, after tile t - 1
+    // the half (halves) of tile t, after tile t - 1; in_range: t is known to be below
+    // the last tile
+    auto resolve = [&](uint32_t t, bool in_range = false) {
 #pragma unroll
         for (int k = 0; k < NH; k++) {
-            nx_in[k] = t * TP + 16u * (NH == 1 ? my_half : (uint32_t)k) < n_wg;
+            nx_in[k] = in_range || t * TP + 16u * (NH == 1 ? my_half : (uint32_t)k) < n_wg;
             nx_row[k] = at_row;
             if (nx_in[k])
                 nx_blk[k] = ((const __attribute__((address_space(4))) uint32_t *)blocks)[tab + at_bi];
@@ -328,7 +341,7 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
     };
     bool bad_id = false;                    // flagged once, after the tile loop
     auto resolved = [&](int k) -> const uint8_t * {  // a base of the last resolved tile
-        const bool bad = nx_in[k] && id_check && nx_blk[k] >= pool_ids;
+        const bool bad = nx_in[k] && nx_blk[k] >= pool_ids;
         bad_id |= bad;
         const uint8_t *b = kv_g + (uint64_t)nx_blk[k] * bbytes + nx_row[k] * (uint32_t)(D * 2);
         return nx_in[k] && !bad ? b : nullptr;
@@ -558,11 +571,14 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
                 c_v[u] = __builtin_amdgcn_readfirstlane(isv ? 1u : 0u);
             }
         }();
-        auto issue = [&](uint32_t t, DmaSlot<D> &sl) {  // t = 0, 1, 2, ... in order
+        // t = 0, 1, 2, ... in order; steady: t + 2 is below the last tile, so tile t is whole
+        // and both halves of t + 1 start before n_wg
+        auto issue = [&](auto steady, uint32_t t, DmaSlot<D> &sl) {
+            constexpr bool STEADY = decltype(steady)::value;
             const uint8_t *hb = resolved(0);
-            if (t + 1 < ntiles) resolve(t + 1);
+            if (STEADY || t + 1 < ntiles) resolve(t + 1, STEADY);
             const uint32_t p0 = t * TP + 16u * my_half;   // the wave's half
-            const uint32_t valid = n_wg > p0 ? min(n_wg - p0, 16u) : 0u;
+            const uint32_t valid = STEADY ? 16u : n_wg > p0 ? min(n_wg - p0, 16u) : 0u;
             if (valid == 16u && hb != nullptr) {  // uniform
                 // Cached loads (aux 0): the n_cb workgroups of a (segment, KV head) read the
                 // same tiles and share them through the XCD's L2.
@@ -630,23 +646,36 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
                 __builtin_amdgcn_s_waitcnt(0x0f70);                         // vmcnt(0)
             }
         };
-        auto step = [&](uint32_t t, DmaSlot<D> &cur, DmaSlot<D> &nxt) {
+        // steady: t + 4 is below the last tile (no range checks)
+        auto step = [&](auto steady, uint32_t t, DmaSlot<D> &cur, DmaSlot<D> &nxt) {
+            constexpr bool STEADY = decltype(steady)::value;
             // Tile t landed everywhere and every wave is past tile t - 1.  A bare barrier:
             // __syncthreads' fence would also wait for the tiles still in flight.
-            wait_tile(t);
+            if constexpr (STEADY) __builtin_amdgcn_s_waitcnt(0x0f74);  // vmcnt(4)
+            else wait_tile(t);
             __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): register-path LDS stores
             asm volatile("" ::: "memory");       // no LDS access moves across the barrier
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
-            if (t + 2 < ntiles) issue(t + 2, nxt);  // into tile t - 1's slot
+            if (STEADY || t + 2 < ntiles) issue(steady, t + 2, nxt);  // into tile t - 1's slot
             tile(t * TP, kread(cur), vread(cur));
         };
-        issue(0, s0);
-        if (ntiles > 1) issue(1, s1);
-        for (uint32_t t = 0; t < ntiles; t += 3) {
-            step(t, s0, s2);
-            if (t + 1 < ntiles) step(t + 1, s1, s0);
-            if (t + 2 < ntiles) step(t + 2, s2, s1);
+        const Flag<false> any;
+        const Flag<true> steady;
+        issue(any, 0, s0);
+        if (ntiles > 1) issue(any, 1, s1);
+        uint32_t t = 0;
+        // steady steps t .. t + 2 issue tiles up to t + 4 and resolve up to t + 5, which must
+        // not be the last tile (its second half may start past n_wg)
+        for (; t + 7 <= ntiles; t += 3) {
+            step(steady, t, s0, s2);
+            step(steady, t + 1, s1, s0);
+            step(steady, t + 2, s2, s1);
+        }
+        for (; t < ntiles; t += 3) {
+            step(any, t, s0, s2);
+            if (t + 1 < ntiles) step(any, t + 1, s1, s0);
+            if (t + 2 < ntiles) step(any, t + 2, s2, s1);
         }
     }
     if (bad_id && lane == 0) flag(err, ERR_BLOCK);  // any wave: each resolves its own half

@@ -411,3 +411,23 @@ def test_empty_batches_are_no_ops(hip):
     assert hip.read(buf, 0, N * L.block_bytes) == bytes([7]) * (N * L.block_bytes)
     assert int((pool != 7).sum()) == 0
     buf.close()
+
+
+def test_buffers_and_pools_outlive_a_closed_device(hip):
+    """qvkv_close before the last buffer and pool are freed (the order a garbage collector
+    may pick at teardown): the buffer and the pool are still freed cleanly afterwards (the
+    device's struct lives until the last of them)."""
+    from qubivex_amd import HipDevice, KvLayout, KvPool
+
+    dev = HipDevice(0)
+    buf = dev.alloc(1 << 20)
+    dev.write(buf, 0, b"\x01" * 64)
+    pool = KvPool(dev, KvLayout("f16", 2, 64, 16), 64, 2)
+    dev.close()  # the device first
+    buf.close()
+    pool.close()
+    # the other handle on the same GPU still works
+    b2 = hip.alloc(4096)
+    hip.write(b2, 0, b"\x02" * 16)
+    assert hip.read(b2, 0, 16) == b"\x02" * 16
+    b2.close()

@@ -83,6 +83,46 @@ def test_prefill_within_tolerance(hip, dtype, H, G, D, segs):
     assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)
 
 
+@pytest.mark.parametrize("dtype,D", [(F16, 128), (F16, 64), (Q8_0, 128)])
+def test_prefill_reads_no_table_entry_past_a_segment(hip, dtype, D):
+    """Each segment's table is followed by an id far past the pool.  The segments end 1-16
+    positions into a last tile whose count is a multiple of 3 (so the streaming loop's
+    three-tile steps end just before it, and the tile's second half starts past the
+    context): the kernel must resolve no table entry for that half, so no error is
+    latched, and the results match the oracle."""
+    print(f"prefill table tail {dtype} D={D}", flush=True)
+    r = rng(77 + D)
+    H = G = 8   # one query row per token: a 64-token segment is one workgroup
+    L = layout(dtype, G, D)
+    segs = [(261, 64), (360, 64), (944, 64), (1025, 40)]
+    lens = [n for n, _ in segs]
+    n_tok = np.array([m for _, m in segs], np.uint32)
+    N = sum((n + 15) // 16 for n in lens) + 5
+    pool = new_pool(L, N, fill=9)
+    blocks, table_at, sim = fill_items(hip, L, pool, N, lens, r)
+    padded, padded_at = [], []
+    for i, n in enumerate(lens):
+        padded_at.append(len(padded))
+        padded.extend(blocks[table_at[i]:table_at[i] + (n + 15) // 16])
+        padded.append(0xFFFFFFFF)
+    padded = np.array(padded, np.uint32)
+    padded_at = np.array(padded_at, np.uint32)
+    T = int(n_tok.sum())
+    q_at = np.concatenate([[0], np.cumsum(n_tok)[:-1]]).astype(np.uint32)
+    pos0 = (np.array(lens, np.uint32) - n_tok).astype(np.uint32)
+    q = normal(r, (T, H, D))
+    out = torch.full((T * H * D,), float("nan"), dtype=torch.float32, device="cuda")
+    hip.prefill_attention(L, pool, N, cf32(q), cu32(padded), cu32(padded_at), cu32(pos0),
+                          cu32(q_at), cu32(n_tok), H, int(max(lens)) - 1, int(n_tok.max()), out)
+    hip.check()
+    got = out.cpu().numpy().reshape(T, H, D)
+    ta, pos, rows = expand(table_at, lens, n_tok, q_at)
+    want = sim.attention(q[rows], H, blocks, ta, pos)
+    max_abs, rel = attn_errors(got[rows], want)
+    print(f"  max_abs={max_abs:.2e} rel_l2={rel:.2e}", flush=True)
+    assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)
+
+
 @pytest.mark.parametrize("exact_p", [True, False])
 def test_prefill_equals_decode_kernel_per_token(hip, exact_p, monkeypatch):
     """The prefill kernel and the decode kernel (one item per token) agree to float
