@@ -770,8 +770,12 @@ void k_prefill_q8(QV_PREFILL_PARAMS) {
     const uint32_t col = lane & 15u, grp = lane >> 4;
     const uint32_t rw0 = r0 + w * 16u;
     const bool wave_live = rw0 < nrows;
-    const uint32_t n_wave = wave_live ? p0s + min(nt - 1, (rw0 + 15u) / GS) + 1 : 0u;
-    const uint32_t n_wave_min = wave_live ? p0s + rw0 / GS + 1 : 0u;
+    const uint32_t n_wave = [&]() {  // scalar: the per-tile tests are scalar branches
+        return __builtin_amdgcn_readfirstlane(wave_live ? p0s + min(nt - 1, (rw0 + 15u) / GS) + 1 : 0u);
+    }();
+    const uint32_t n_wave_min = [&]() {
+        return __builtin_amdgcn_readfirstlane(wave_live ? p0s + rw0 / GS + 1 : 0u);
+    }();
     const uint32_t row = rw0 + col;
     const bool rvalid = row < nrows;
     const uint32_t tj = rvalid ? row / GS : 0u, hh = rvalid ? row % GS : 0u;
@@ -829,26 +833,46 @@ void k_prefill_q8(QV_PREFILL_PARAMS) {
     u4v xv;
     u2v xvs;
     uint32_t xks;
-    // The block of each 16-position half of a tile, resolved on the scalar unit (a
-    // constant-address-space load of the table entry): the block base and the first row
-    // of the half (g * B + its offset in the block), or null past n_wg / for a bad id.
+    // The block of each 16-position half of a tile, resolved on the scalar unit: the block
+    // base and the first row of the half (g * B + its offset in the block), or null past
+    // n_wg / for a bad id.  Tiles are resolved in order, one tile ahead of their use: the
+    // (block, row) split advances by counters (B is a multiple of 16) and the table
+    // entries are constant-address-space loads that land during a tile's math.
     struct Half {
         const uint8_t *base;
         uint32_t row0;
     };
-    auto half_of = [&](uint32_t ph) -> Half {
-        if (ph >= n_wg) return Half{nullptr, 0u};
-        const uint32_t bi = geo.fd_b.div(ph);
-        const uint32_t blk = ((const __attribute__((address_space(4))) uint32_t *)blocks)[tab + bi];
-        if (blk >= pool_blocks) {
-            if (threadIdx.x == 0) flag(err, ERR_BLOCK);
-            return Half{nullptr, 0u};
+    // ids at or past pool_ids are bad (the clamp only matters for id 0xffffffff in a pool of
+    // 2^32 blocks or more, which no device holds)
+    const uint32_t pool_ids = pool_blocks > 0xffffffffull ? 0xffffffffu : (uint32_t)pool_blocks;
+    uint32_t at_bi = 0, at_row = 0;         // block index / row of the next half to resolve
+    uint32_t nx_blk[2] = {0u, 0u}, nx_row[2] = {0u, 0u};
+    bool nx_in[2] = {false, false};
+    auto resolve = [&](uint32_t t) {        // the halves of tile t, after those of t - 1
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            nx_in[k] = t * TP + 16u * k < n_wg;
+            nx_row[k] = at_row;
+            if (nx_in[k])
+                nx_blk[k] = ((const __attribute__((address_space(4))) uint32_t *)blocks)[tab + at_bi];
+            at_row += 16u;
+            if (at_row == B) {
+                at_row = 0u;
+                at_bi++;
+            }
         }
-        return Half{pool + (uint64_t)blk * geo.bb, g * B + (ph - bi * B)};
     };
-    auto load = [&](uint32_t t) {
+    bool bad_id = false;                    // flagged once, after the tile loop
+    auto resolved = [&](int k) -> Half {    // a half of the last resolved tile
+        const bool bad = nx_in[k] && nx_blk[k] >= pool_ids;
+        bad_id |= bad;
+        return Half{nx_in[k] && !bad ? pool + (uint64_t)nx_blk[k] * geo.bb : nullptr,
+                    g * B + nx_row[k]};
+    };
+    auto load = [&](uint32_t t) {  // t = 0, 1, 2, ... in order
         const uint32_t p0 = t * TP;
-        const Half h0 = half_of(p0), h1 = half_of(p0 + 16u);
+        const Half h0 = resolved(0), h1 = resolved(1);
+        if (t + 1 < ntiles) resolve(t + 1);
         xk[0] = u2v{0u, 0u};
         xk[1] = u2v{0u, 0u};
         xv = u4v{0u, 0u, 0u, 0u};
@@ -1024,6 +1048,7 @@ void k_prefill_q8(QV_PREFILL_PARAMS) {
         if (t + 1 < ntiles) store(nxt);
         __syncthreads();
     };
+    resolve(0);
     load(0);
     store(sb0);
     __syncthreads();
@@ -1031,6 +1056,7 @@ void k_prefill_q8(QV_PREFILL_PARAMS) {
         step(t, sb0, sb1);
         if (t + 1 < ntiles) step(t + 1, sb1, sb0);
     }
+    if (bad_id && threadIdx.x == 0) flag(err, ERR_BLOCK);
     if (!wave_live) return;
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
