@@ -280,6 +280,40 @@ def run_decode(name, args, dev, legs, steps, warmup, cpu):
         log(f"[bench] {name} decode in model order ({NL} x append+attention over {S} items): "
             f"{lwall:.3f} ms/step ({S / (lwall / 1e3):.0f} tok/s); attention {la_ms:.3f} ms = "
             f"{res['layers_attn_gbs']:.0f} GB/s")
+        # The same step captured once into a HIP graph and replayed: the device time of the
+        # model-order step without this script's per-call launch cost (Python and ctypes
+        # issue each call slower than the GPU runs it here).  The replayed outputs must
+        # equal the eager step's bit for bit.
+        gs = torch.cuda.Stream()
+        gs.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(gs):
+            layer_step()  # the stream's first launches set up its flag and workspace
+        gs.synchronize()
+        dev.check(gs)
+        eager_out = out.clone()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=gs):
+            layer_step()
+        torch.cuda.synchronize()
+        for _ in range(max(warmup, 1)):
+            graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        dev.check(gs)
+        if not torch.equal(out, eager_out):
+            raise SystemExit("graph replay of the model-order step differs from the eager step")
+        g_ms = e0.elapsed_time(e1) / steps
+        res.update(layers_graph_ms_per_step=g_ms, layers_graph_tokens_per_s=S / (g_ms / 1e3),
+                   layers_graph_gbs=attn_bytes / (g_ms / 1e3) / 1e9)
+        log(f"[bench] {name} model order as one HIP graph: {g_ms:.3f} ms/step "
+            f"({S / (g_ms / 1e3):.0f} tok/s; attention bytes / step time = "
+            f"{res['layers_graph_gbs']:.0f} GB/s, appends included)")
+        del graph, eager_out
 
     if "gather" in legs:
         # Gather up to 8 layers' items (all positions) into contiguous [G][n][d] per item.
@@ -683,10 +717,12 @@ def roofline_of(config, res, info):
 
 def summary(res, info):
     keep = ("ms_per_step", "tokens_per_s", "attn_ms", "attn_gbs", "layers_ms_per_step",
-            "layers_tokens_per_s", "layers_attn_gbs", "gather_gbs", "copy_gbs", "append_gbs",
-            "prefill_tflops", "prelude_gbs")
+            "layers_tokens_per_s", "layers_attn_gbs", "layers_graph_ms_per_step",
+            "layers_graph_tokens_per_s", "layers_graph_gbs", "gather_gbs", "copy_gbs",
+            "append_gbs", "prefill_tflops", "prelude_gbs")
     out = {k: round(res[k], 4) for k in keep if k in res}
-    for k in ("attn_gbs", "layers_attn_gbs", "gather_gbs", "copy_gbs", "append_gbs"):
+    for k in ("attn_gbs", "layers_attn_gbs", "layers_graph_gbs", "gather_gbs", "copy_gbs",
+              "append_gbs"):
         if k in res:
             out[k.replace("_gbs", "_frac")] = round(res[k] / PEAK_HBM_GBS, 4)
     out["workload"] = workload_text(info)
@@ -771,6 +807,12 @@ def main():
             "ms_per_step": round(res.get("layers_ms_per_step", 0.0), 4),
             "tokens_per_s": round(res.get("layers_tokens_per_s", 0.0), 1),
             "attention_frac": round(res.get("layers_attn_gbs", 0.0) / PEAK_HBM_GBS, 4),
+            "graph_ms_per_step": round(res.get("layers_graph_ms_per_step", 0.0), 4),
+            "graph_tokens_per_s": round(res.get("layers_graph_tokens_per_s", 0.0), 1),
+            "graph_frac": round(res.get("layers_graph_gbs", 0.0) / PEAK_HBM_GBS, 4),
+            "note": "ms_per_step and attention_frac: each call issued from Python (the GPU "
+                    "waits on the launches at small batches); graph_*: the same step "
+                    "replayed as one HIP graph, appends included in the time",
         }
         line["fraction_of_roofline"] = {
             "attention": round(res["attn_gbs"] / PEAK_HBM_GBS, 4),

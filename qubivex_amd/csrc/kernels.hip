@@ -1003,10 +1003,21 @@ __device__ __forceinline__ void attn_unit(const uint8_t *__restrict__ pool, uint
 // written out directly; a unit cut by a range boundary leaves a partial in the
 // workgroup's slot 0 (its first unit) or 1 (its last), merged by k_attn_stream_merge.
 // Each workgroup computes the units' prefix sums itself from pos (n_items <= 2048).
-// Workspace: partials [P][2][8][D], their (max, sum) [P][2][8][2], then the prefix sums
-// [n_items + 1] (u64, written by workgroup 0 for the merge).
+// Workspace: partials [P][2][8][D], their (max, sum) [P][2][8][2], the prefix sums
+// [n_items + 1] (u64), then at the next 16-byte boundary one record per unit for the
+// merge (StreamRec; the sums and the records are written by workgroup 0).
 // ---------------------------------------------------------------------------------
 constexpr uint32_t STREAM_MAX_ITEMS = 2048;
+
+// A unit's place in the split for the merge: its range of the work order lies in
+// workgroups w0 .. w1 (w0 == w1: written out whole, nothing to merge), and w0 holds its
+// partial in slot s0 (1 when the unit starts inside w0's range after w0's first unit).
+struct StreamRec {
+    uint32_t w0, w1, s0, pad;
+};
+__host__ __device__ constexpr uint64_t stream_rec_at(uint64_t P, uint64_t D, uint64_t n_items) {
+    return (P * 2 * 8 * (D + 2) * 4 + (n_items + 1) * 8 + 15) / 16 * 16;  // bytes into ws
+}
 
 // Unit-tiles of every item before item i (cum[i]) and in total (cum[n_items]).  Items with
 // a position past max_pos or a table too short count no tiles (and are reported).
@@ -1090,9 +1101,24 @@ __device__ __forceinline__ void attn_stream_body(QV_STREAM_PARAMS) {
     const uint32_t P = gridDim.x, w = blockIdx.x;
     const uint64_t s0 = (uint64_t)w * T / P, s1 = (uint64_t)(w + 1) * T / P;
     float *ml = ws + (uint64_t)P * 2 * 8 * D;
-    if (w == 0) {  // the prefix sums, for the merge
+    if (w == 0) {  // the prefix sums and the units' records, for the merge
         uint64_t *wc = (uint64_t *)(ml + (uint64_t)P * 2 * 8 * 2);
         for (uint32_t i = threadIdx.x; i <= n_items; i += 256) wc[i] = cum[i];
+        StreamRec *rec = (StreamRec *)((uint8_t *)ws + stream_rec_at(P, D, n_items));
+        for (uint32_t u = threadIdx.x; u < n_items * upi; u += 256) {
+            const uint32_t item = u / upi, ul = u % upi;
+            const uint64_t per_unit = (cum[item + 1] - cum[item]) / upi;
+            StreamRec r{0u, 0u, 0u, 0u};
+            if (per_unit != 0) {
+                const uint64_t a = cum[item] + (uint64_t)ul * per_unit, b = a + per_unit;
+                // workgroup holding position x: the largest v with floor(v T / P) <= x
+                auto owner = [&](uint64_t x) { return (uint32_t)(((x + 1) * P + T - 1) / T - 1); };
+                r.w0 = owner(a);
+                r.w1 = owner(b - 1);
+                r.s0 = a != (uint64_t)r.w0 * T / P ? 1u : 0u;
+            }
+            rec[u] = r;
+        }
     }
     bool first = true;
     for (uint64_t x = s0; x < s1;) {
@@ -1134,11 +1160,11 @@ void k_attn_stream_w(QV_STREAM_PARAMS) {
 }
 
 // Merge for k_attn_stream: block = one (item, query head), D threads.  The unit's
-// range [a, b) of the work order lies in workgroups w0 .. w1; with w0 == w1 it was
-// written out whole.  Workgroup w's partial of it is in slot 1 when the unit starts
-// inside w's range after its first unit, else in slot 0; workgroups between them with
-// an empty range (more workgroups than tiles) hold none.  The same bookkeeping is
-// restated in tests/test_attention_split.py and checked there on random shapes.
+// range [a, b) of the work order lies in workgroups w0 .. w1 (its StreamRec); with
+// w0 == w1 it was written out whole.  Workgroup w's partial of it is in slot 1 when the
+// unit starts inside w's range after its first unit, else in slot 0; workgroups between
+// them with an empty range (more workgroups than tiles) hold none.  The same bookkeeping
+// is restated in tests/test_attention_split.py and checked there on random shapes.
 __global__ __launch_bounds__(256) void k_attn_stream_merge(const float *__restrict__ ws,
                                                            uint32_t n_items, uint32_t H,
                                                            uint32_t G, uint32_t hc_n,
@@ -1149,23 +1175,22 @@ __global__ __launch_bounds__(256) void k_attn_stream_merge(const float *__restri
     if (item >= n_items) return;
     const float *ml = ws + (uint64_t)P * 2 * 8 * D;
     const uint64_t *cum = (const uint64_t *)(ml + (uint64_t)P * 2 * 8 * 2);
-    const uint64_t T = cum[n_items];
-    const uint32_t upi = G * hc_n, GS = H / G;
-    const uint64_t per_unit = (cum[item + 1] - cum[item]) / upi;
-    if (per_unit == 0 || T == 0) return;
+    const StreamRec *recs = (const StreamRec *)((const uint8_t *)ws + stream_rec_at(P, D, n_items));
+    const uint32_t GS = H / G;
     const uint32_t g = h / GS, hin = h % GS, hc = hin / 8, hh = hin % 8;
-    const uint64_t a = cum[item] + (uint64_t)(g * hc_n + hc) * per_unit, b = a + per_unit;
-    // workgroup holding position x: the largest w with floor(w T / P) <= x
-    auto owner = [&](uint64_t x) { return (uint32_t)(((x + 1) * P + T - 1) / T - 1); };
-    const uint32_t w0 = owner(a), w1 = owner(b - 1);
+    const StreamRec r = recs[(uint64_t)item * G * hc_n + g * hc_n + hc];
+    const uint32_t w0 = r.w0, w1 = r.w1;
     if (w0 == w1) return;
-    const uint64_t start0 = (uint64_t)w0 * T / P;
-    // workgroups with an empty range (more workgroups than tiles) hold no partial
-    auto empty = [&](uint32_t w) { return (uint64_t)w * T / P == (uint64_t)(w + 1) * T / P; };
+    // Workgroups with an empty range (only when there are fewer tiles than workgroups)
+    // hold no partial.
+    const uint64_t T = cum[n_items];
+    auto empty = [&](uint32_t w) {
+        return T < P && (uint64_t)w * T / P == (uint64_t)(w + 1) * T / P;
+    };
     float M = -INFINITY;
     for (uint32_t w = w0; w <= w1; w++) {
         if (empty(w)) continue;
-        const uint64_t slot = 2ull * w + ((w == w0 && a != start0) ? 1u : 0u);
+        const uint64_t slot = 2ull * w + (w == w0 ? r.s0 : 0u);
         M = fmaxf(M, ml[(slot * 8 + hh) * 2]);
     }
     const float Ms = M == -INFINITY ? 0.0f : M;
@@ -1173,7 +1198,7 @@ __global__ __launch_bounds__(256) void k_attn_stream_merge(const float *__restri
         float L = 0.0f, O = 0.0f;
         for (uint32_t w = w0; w <= w1; w++) {
             if (empty(w)) continue;
-            const uint64_t slot = 2ull * w + ((w == w0 && a != start0) ? 1u : 0u);
+            const uint64_t slot = 2ull * w + (w == w0 ? r.s0 : 0u);
             const float mc = ml[(slot * 8 + hh) * 2];
             const float f = mc == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mc - Ms);
             L = fmaf(ml[(slot * 8 + hh) * 2 + 1], f, L);
@@ -1458,7 +1483,8 @@ int plan_attention(const Geometry &g, uint32_t n_items, uint32_t heads, uint32_t
         if (wgs < 1) wgs = 1;
         p->kind = 2;
         p->n_chunks = (uint32_t)wgs;
-        p->ws_bytes = wgs * 2 * 8 * (g.D + 2) * 4 + ((uint64_t)n_items + 1) * 8;
+        p->ws_bytes = stream_rec_at(wgs, g.D, n_items) +
+                      (uint64_t)n_items * g.G * p->hc * sizeof(StreamRec);
         return QVKV_OK;
     }
     // Else (QVKV_ATTN_STREAM=0) into context chunks, aiming at about 6 workgroups per CU.

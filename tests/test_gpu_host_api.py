@@ -431,3 +431,71 @@ def test_buffers_and_pools_outlive_a_closed_device(hip):
     hip.write(b2, 0, b"\x02" * 16)
     assert hip.read(b2, 0, 16) == b"\x02" * 16
     b2.close()
+
+
+def test_graph_replays_of_append_and_attention_match_eager(hip):
+    """After one eager step on a stream (which sets up its error flag and workspace), a
+    decode step in model order (per layer: append one row per sequence, then attention
+    over the layer's items, through the split-by-work path with its merge) is captured into
+    a HIP graph on that stream.  Every replay, with eager work and synchronizations between
+    replays, gives the eager step's outputs bit for bit."""
+    import torch
+
+    from qubivex_amd import KvLayout, KvPool
+
+    NL, G, D, H, B, S = 3, 8, 128, 32, 16, 8
+    L = KvLayout("f16", G, D, B)
+    r = np.random.default_rng(5)
+    lens = r.integers(100, 3000, size=S)
+    N = int(NL * (lens.sum() // B + 2 * S) + 64)
+    pool = KvPool(hip, L, N, NL)
+    mem = pool.memory
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    seqs = [pool.create() for _ in range(S)]
+
+    def t32(a):
+        return torch.from_numpy(np.ascontiguousarray(a, np.uint32).view(np.int32)).cuda()
+
+    slots = pool.plan_append_layers(seqs, [int(n) for n in lens], 0, NL)
+    k0 = torch.randn((slots.size, G * D), generator=gen, device="cuda")
+    hip.append(L, mem, N, k0, torch.randn_like(k0), t32(slots))
+    # the step's rows: one new position per sequence and layer (same slots every replay)
+    slots = pool.plan_append_layers(seqs, [1] * S, 0, NL)
+    d_slots = t32(slots)
+    kn = torch.randn((NL * S, G * D), generator=gen, device="cuda")
+    vn = torch.randn_like(kn)
+    q = torch.randn((NL * S, H * D), generator=gen, device="cuda")
+    out = torch.zeros((NL * S, H * D), device="cuda")
+    tabs = [pool.tables(seqs, l) for l in range(NL)]
+    d_tabs = [(t32(b), t32(ta), t32(p), int(p.max())) for b, ta, p in tabs]
+    torch.cuda.synchronize()
+
+    def step():
+        for l in range(NL):
+            rows = slice(l * S, (l + 1) * S)
+            hip.append(L, mem, N, kn[rows], vn[rows], d_slots[rows])
+            b, ta, p, mp = d_tabs[l]
+            hip.attention(L, mem, N, q[rows], b, ta, p, H, mp, out[rows])
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    s.synchronize()
+    hip.check(s)
+    ref = out.clone()
+    assert torch.isfinite(ref).all()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        step()
+    torch.cuda.synchronize()
+    for rep in range(4):
+        out.zero_()
+        junk = torch.randn((1 << 20,), generator=gen, device="cuda").sum()  # eager work
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        hip.check(s)
+        assert torch.equal(out, ref), rep
+        del junk
+    pool.close()
