@@ -313,6 +313,44 @@ def run_decode(name, args, dev, legs, steps, warmup, cpu):
         log(f"[bench] {name} model order as one HIP graph: {g_ms:.3f} ms/step "
             f"({S / (g_ms / 1e3):.0f} tok/s; attention bytes / step time = "
             f"{res['layers_graph_gbs']:.0f} GB/s, appends included)")
+        del graph
+
+        # The same step with each layer's append inside its attention launch
+        # (qvkv_append_attention_async, one launch per layer for f16 pools): the outputs
+        # must equal the eager step's bit for bit.
+        def fused_step():
+            for k_, v_, s_, q_, t_, p_, o_ in per_layer:
+                dev.append_attention(L, mem, n_blocks, q_, k_, v_, d_blocks, t_, p_, H,
+                                     max_pos, o_)
+
+        out.zero_()
+        with torch.cuda.stream(gs):
+            fused_step()
+        gs.synchronize()
+        dev.check(gs)
+        if not torch.equal(out, eager_out):
+            raise SystemExit("the fused append + attention step differs from the eager step")
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=gs):
+            fused_step()
+        torch.cuda.synchronize()
+        for _ in range(max(warmup, 1)):
+            graph.replay()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        dev.check(gs)
+        if not torch.equal(out, eager_out):
+            raise SystemExit("graph replay of the fused step differs from the eager step")
+        f_ms = e0.elapsed_time(e1) / steps
+        res.update(layers_fused_ms_per_step=f_ms, layers_fused_tokens_per_s=S / (f_ms / 1e3),
+                   layers_fused_gbs=attn_bytes / (f_ms / 1e3) / 1e9)
+        log(f"[bench] {name} model order, append fused into attention, one HIP graph: "
+            f"{f_ms:.3f} ms/step ({S / (f_ms / 1e3):.0f} tok/s; "
+            f"{res['layers_fused_gbs']:.0f} GB/s of attention bytes)")
         del graph, eager_out
 
     if "gather" in legs:
@@ -718,11 +756,12 @@ def roofline_of(config, res, info):
 def summary(res, info):
     keep = ("ms_per_step", "tokens_per_s", "attn_ms", "attn_gbs", "layers_ms_per_step",
             "layers_tokens_per_s", "layers_attn_gbs", "layers_graph_ms_per_step",
-            "layers_graph_tokens_per_s", "layers_graph_gbs", "gather_gbs", "copy_gbs",
+            "layers_graph_tokens_per_s", "layers_graph_gbs", "layers_fused_ms_per_step",
+            "layers_fused_tokens_per_s", "layers_fused_gbs", "gather_gbs", "copy_gbs",
             "append_gbs", "prefill_tflops", "prelude_gbs")
     out = {k: round(res[k], 4) for k in keep if k in res}
-    for k in ("attn_gbs", "layers_attn_gbs", "layers_graph_gbs", "gather_gbs", "copy_gbs",
-              "append_gbs"):
+    for k in ("attn_gbs", "layers_attn_gbs", "layers_graph_gbs", "layers_fused_gbs",
+              "gather_gbs", "copy_gbs", "append_gbs"):
         if k in res:
             out[k.replace("_gbs", "_frac")] = round(res[k] / PEAK_HBM_GBS, 4)
     out["workload"] = workload_text(info)
@@ -810,9 +849,14 @@ def main():
             "graph_ms_per_step": round(res.get("layers_graph_ms_per_step", 0.0), 4),
             "graph_tokens_per_s": round(res.get("layers_graph_tokens_per_s", 0.0), 1),
             "graph_frac": round(res.get("layers_graph_gbs", 0.0) / PEAK_HBM_GBS, 4),
+            "fused_graph_ms_per_step": round(res.get("layers_fused_ms_per_step", 0.0), 4),
+            "fused_graph_tokens_per_s": round(res.get("layers_fused_tokens_per_s", 0.0), 1),
+            "fused_graph_frac": round(res.get("layers_fused_gbs", 0.0) / PEAK_HBM_GBS, 4),
             "note": "ms_per_step and attention_frac: each call issued from Python (the GPU "
                     "waits on the launches at small batches); graph_*: the same step "
-                    "replayed as one HIP graph, appends included in the time",
+                    "replayed as one HIP graph, appends included in the time; fused_*: "
+                    "each layer's append inside its attention launch "
+                    "(qvkv_append_attention_async), as one HIP graph",
         }
         line["fraction_of_roofline"] = {
             "attention": round(res["attn_gbs"] / PEAK_HBM_GBS, 4),

@@ -174,6 +174,23 @@ int qvkv_attention_async(qvkv_dev *dev, const qvkv_layout *layout, const void *p
                          uint32_t n_items, uint32_t heads, uint32_t max_pos, float *out,
                          void *stream);
 
+/* Decode attention with the step's append: each item's new key and value rows k_new[t],
+ * v_new[t] ([n_items][kv_out] f32, narrowed as qvkv_append_async narrows them) are stored
+ * at position pos[t] of its table (the slot of that position, which the caller's
+ * planning made writable), then attention runs over positions 0..pos[t] as in
+ * qvkv_attention_async.  The reference's DeviceMoeAttention submission after its sync
+ * rows: "the new token's key and value are stored at pos[t], and attention reads
+ * positions 0..=pos[t]" (crates/qubivex-compute/src/discrete.rs:257-307).  f16 pools at
+ * d = 64, 128, 256 run it as one launch (the attention takes position pos[t] from the new
+ * rows and stores them); other layouts run the append and the attention in turn, on the
+ * stream.  The same results, bit for bit, as qvkv_append_async at those slots followed
+ * by qvkv_attention_async. */
+int qvkv_append_attention_async(qvkv_dev *dev, const qvkv_layout *layout, void *pool,
+                                uint64_t pool_blocks, const float *q, const float *k_new,
+                                const float *v_new, const uint32_t *blocks, uint64_t n_table,
+                                const uint32_t *table_at, const uint32_t *pos, uint32_t n_items,
+                                uint32_t heads, uint32_t max_pos, float *out, void *stream);
+
 /* qvkv_attention_async without any allocation: no counterpart in the reference.  For
  * callers that cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc).  Same arguments and results.  A launch that

@@ -120,6 +120,8 @@ SIGNATURES = {
                                     _u32, _vp, _vp]),
     "qvkv_attention_noalloc_async": (_i32, [_vp, _LP, _vp, _u64, _vp, _vp, _u64, _vp, _vp, _u32,
                                             _u32, _u32, _vp, _vp]),
+    "qvkv_append_attention_async": (_i32, [_vp, _LP, _vp, _u64, _vp, _vp, _vp, _vp, _u64, _vp,
+                                           _vp, _u32, _u32, _u32, _vp, _vp]),
     "qvkv_prefill_attention_async": (_i32, [_vp, _LP, _vp, _u64, _vp, _u64, _vp, _u64, _vp, _vp,
                                             _vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp]),
     "qvkv_block_copy_async": (_i32, [_vp, _LP, _vp, _u64, _vp, _vp, _u32, _vp]),

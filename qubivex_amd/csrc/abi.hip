@@ -626,6 +626,54 @@ int qvkv_attention_async(qvkv_dev *dev, const qvkv_layout *layout, const void *p
                     "attention launch");
 }
 
+int qvkv_append_attention_async(qvkv_dev *dev, const qvkv_layout *layout, void *pool,
+                                uint64_t pool_blocks, const float *q, const float *k_new,
+                                const float *v_new, const uint32_t *blocks, uint64_t n_table,
+                                const uint32_t *table_at, const uint32_t *pos, uint32_t n_items,
+                                uint32_t heads, uint32_t max_pos, float *out, void *stream) {
+    if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    Geometry g;
+    if (int rc = geometry(layout, &g)) return rc;
+    qvkv::AttnPlan p;
+    const char *why = "";
+    if (int rc = qvkv::plan_attention(g, n_items, heads, max_pos, &p, &why))
+        return fail(rc, "shape mismatch in attention: %s", why);
+    if (n_items == 0) return QVKV_OK;
+    if (!pool || !q || !k_new || !v_new || !blocks || !table_at || !pos || !out)
+        return fail(QVKV_E_SHAPE, "shape mismatch in attention: null pointer");
+    if (int rc = set_device(dev)) return rc;
+    std::unique_lock<std::mutex> host_lk(dev->host_mu, std::defer_lock);
+    if ((hipStream_t)stream == dev->stream) host_lk.lock();
+    std::lock_guard<std::mutex> lk(dev->mu);
+    StreamState *st;
+    if (int rc = state_locked(dev, (hipStream_t)stream, &st)) return rc;
+    const bool fused = qvkv::fused_append_attention(g);
+    // unfused: the items' slots after the attention workspace, then append + attention
+    const uint64_t slots_at = (p.ws_bytes + 255) / 256 * 256;
+    qvkv::AttnPlan pw = p;
+    if (!fused) pw.ws_bytes = slots_at + (uint64_t)n_items * 4;
+    if (int rc = ensure_attention(dev, st, pw)) return rc;
+    if (fused) {
+        qvkv::NewRows nr;
+        nr.k = k_new;
+        nr.v = v_new;
+        return launched(dev, qvkv::launch_attention(g, p, pool, pool_blocks, q, blocks, n_table,
+                                                    table_at, pos, n_items, heads, max_pos, out,
+                                                    st->ws, st->d_err, st->stream, nr),
+                        "append + attention launch");
+    }
+    uint32_t *slots = (uint32_t *)((uint8_t *)st->ws + slots_at);
+    hipError_t e = qvkv::launch_slots_at(g, blocks, n_table, table_at, pos, n_items, max_pos,
+                                         slots, st->d_err, st->stream);
+    if (e == hipSuccess)
+        e = qvkv::launch_append(g, pool, pool_blocks, k_new, v_new, slots, n_items, st->d_err,
+                                st->stream);
+    if (e == hipSuccess)
+        e = qvkv::launch_attention(g, p, pool, pool_blocks, q, blocks, n_table, table_at, pos,
+                                   n_items, heads, max_pos, out, st->ws, st->d_err, st->stream);
+    return launched(dev, e, "append + attention launch");
+}
+
 int qvkv_attention_noalloc_async(qvkv_dev *dev, const qvkv_layout *layout, const void *pool,
                                  uint64_t pool_blocks, const float *q, const uint32_t *blocks,
                                  uint64_t n_table, const uint32_t *table_at, const uint32_t *pos,

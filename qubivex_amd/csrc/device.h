@@ -274,6 +274,49 @@ struct Tile {
     bool ok;
 };
 
+// Fused append + attention, f16 pools: the tile that holds the appended position (rel =
+// its index in the tile) takes that position's key and value from the new rows kn / vn
+// (this KV head's d values, f32) instead of what the pool held there, rounded to f16 as the
+// append stores them (RNE); with `store`, the lanes also write them to the pool rows krow /
+// vrow, which is the append itself.  Lane (c, qg) holds key d = 32 i + 8 qg .. +7 of
+// position c and value d = c D/16 .. +D/16-1 of positions 4 qg .. 4 qg + 3.
+template <int D>
+__device__ __forceinline__ void patch_new_row(Tile<D, false> &t, uint32_t rel,
+                                              const float *__restrict__ kn,
+                                              const float *__restrict__ vn, uint8_t *krow,
+                                              uint8_t *vrow, uint32_t c, uint32_t qg,
+                                              bool store) {
+    if (c == rel) {
+#pragma unroll
+        for (int i = 0; i < D / 32; i++) {
+            const float4 a = *(const float4 *)(kn + 32 * i + 8 * qg);
+            const float4 b = *(const float4 *)(kn + 32 * i + 8 * qg + 4);
+            const u4v w = {pack_h2(a.x, a.y), pack_h2(a.z, a.w), pack_h2(b.x, b.y),
+                           pack_h2(b.z, b.w)};
+            t.k[4 * i] = w.x;
+            t.k[4 * i + 1] = w.y;
+            t.k[4 * i + 2] = w.z;
+            t.k[4 * i + 3] = w.w;
+            if (store) *(u4v *)(krow + (32 * i + 8 * qg) * 2) = w;
+        }
+    }
+    const uint32_t vi = rel - 4 * qg;  // the value row of this lane that holds it, if any
+    if (vi < 4) {
+        constexpr int VW = D / 32;     // words of this lane's D/16 values
+        uint32_t w[VW];
+#pragma unroll
+        for (int e = 0; e < VW; e++) w[e] = pack_h2(vn[c * (D / 16) + 2 * e], vn[c * (D / 16) + 2 * e + 1]);
+#pragma unroll
+        for (int r = 0; r < 4; r++)  // selects: a register array is not indexed by vi
+#pragma unroll
+            for (int e = 0; e < VW; e++) t.v[r][e] = (uint32_t)r == vi ? w[e] : t.v[r][e];
+        if (store) {
+#pragma unroll
+            for (int e = 0; e < VW; e++) *(uint32_t *)(vrow + c * (D / 16) * 2 + 4 * e) = w[e];
+        }
+    }
+}
+
 // Tile tt (positions 16tt..16tt+15) of block blk (the table entry of position 16tt).
 template <int D, bool Q8, bool NT>
 __device__ __forceinline__ void load_tile_of(Tile<D, Q8> &t, uint32_t tt, uint32_t blk,

@@ -83,10 +83,22 @@ hipError_t launch_prefill(const Geometry &g, const void *pool, uint64_t pool_blo
                           const uint32_t *n_tok, uint32_t n_seg, uint32_t heads,
                           uint32_t max_pos, uint32_t max_tok, uint64_t q_rows, float *out,
                           int *err, hipStream_t s, bool f16_values = true);
+// New key and value rows of a fused append + attention (n_items rows of kv_out floats
+// each, stored at each item's position pos[i] and attended there); null in a plain
+// attention launch.  The fused form runs for f16 pools at d = 64, 128, 256.
+struct NewRows {
+    const float *k = nullptr, *v = nullptr;
+};
+bool fused_append_attention(const Geometry &g);
 hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *pool,
                             uint64_t pool_blocks, const float *q, const uint32_t *blocks,
                             uint64_t n_table, const uint32_t *table_at, const uint32_t *pos,
                             uint32_t n_items, uint32_t heads, uint32_t max_pos, float *out,
-                            void *ws, int *err, hipStream_t s);
+                            void *ws, int *err, hipStream_t s, NewRows nr = NewRows{});
+// Each item's pool slot of position pos[i] (block * B + offset), for the append of the
+// unfused form; an item past max_pos or its table gets slot 0xffffffff (flagged).
+hipError_t launch_slots_at(const Geometry &g, const uint32_t *blocks, uint64_t n_table,
+                           const uint32_t *table_at, const uint32_t *pos, uint32_t n_items,
+                           uint32_t max_pos, uint32_t *slots, int *err, hipStream_t s);
 
 }  // namespace qvkv

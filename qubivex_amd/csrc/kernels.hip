@@ -786,35 +786,43 @@ __global__ __launch_bounds__(256) void k_block_copy(uint8_t *__restrict__ pool,
         const uint32_t *__restrict__ table_at, const uint32_t *__restrict__ pos,                \
         uint32_t n_items, uint32_t H, uint32_t max_pos, float *__restrict__ out,                \
         float *__restrict__ ws, uint32_t hc_n, uint32_t n_chunks, uint32_t tpc, Geo geo,        \
-        int *err
+        int *err, NewRows nr
 #define QV_ATTN_ARGS                                                                            \
     pool, pool_blocks, q, blocks, n_table, table_at, pos, n_items, H, max_pos, out, ws, hc_n,   \
-        n_chunks, tpc, geo, err
+        n_chunks, tpc, geo, err, nr
 
-template <int D, bool Q8, bool NT, bool PK>
+template <int D, bool Q8, bool NT, bool PK, bool NR>
 __device__ __forceinline__ void attn_body(QV_ATTN_PARAMS);
-template <int D, bool Q8, bool NT, bool PK>
+template <int D, bool Q8, bool NT, bool PK, bool NR>
 __device__ __forceinline__ void attn_unit(const uint8_t *__restrict__ pool, uint64_t pool_blocks,
                                           const float *__restrict__ q,
                                           const uint32_t *__restrict__ blocks, uint32_t H,
                                           const Geo &geo, int *err, uint32_t item, uint32_t g,
                                           uint32_t hc, uint32_t n, uint32_t tab, uint32_t t_begin,
                                           uint32_t t_end, float *o_base, uint64_t o_stride,
-                                          float *ml_base, uint64_t ml_stride);
+                                          float *ml_base, uint64_t ml_stride, NewRows nr);
 
 template <int D, bool Q8, bool NT, bool PK>
 __global__ __launch_bounds__(256) void k_attn_mfma(QV_ATTN_PARAMS) {
-    attn_body<D, Q8, NT, PK>(QV_ATTN_ARGS);
+    attn_body<D, Q8, NT, PK, false>(QV_ATTN_ARGS);
+}
+// The fused append + attention form (f16; new rows in nr): a separate build, so the plain
+// kernel keeps its registers, held to the plain kernel's occupancy (3 waves/SIMD; 1 at
+// d = 256).
+template <int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 3)))
+void k_attn_mfma_nr(QV_ATTN_PARAMS) {
+    attn_body<D, false, true, false, true>(QV_ATTN_ARGS);
 }
 
 // The same kernel held to the registers of W waves per SIMD (512 / W per lane).
 template <int D, bool Q8, bool NT, bool PK, int W>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W)))
 void k_attn_mfma_w(QV_ATTN_PARAMS) {
-    attn_body<D, Q8, NT, PK>(QV_ATTN_ARGS);
+    attn_body<D, Q8, NT, PK, false>(QV_ATTN_ARGS);
 }
 
-template <int D, bool Q8, bool NT, bool PK>
+template <int D, bool Q8, bool NT, bool PK, bool NR>
 __device__ __forceinline__ void attn_body(QV_ATTN_PARAMS) {
     const uint32_t G = (uint32_t)geo.G, B = (uint32_t)geo.B;
     const uint32_t GS = H / G;
@@ -852,14 +860,14 @@ __device__ __forceinline__ void attn_body(QV_ATTN_PARAMS) {
 
     const uint64_t oh0 = (uint64_t)item * H + (uint64_t)g * GS + hc * 8;
     if (n_chunks == 1) {
-        attn_unit<D, Q8, NT, PK>(pool, pool_blocks, q, blocks, H, geo, err, item, g, hc, n, tab,
-                                 t_begin, t_end, out + oh0 * D, D, nullptr, 0);
+        attn_unit<D, Q8, NT, PK, NR>(pool, pool_blocks, q, blocks, H, geo, err, item, g, hc, n, tab,
+                                 t_begin, t_end, out + oh0 * D, D, nullptr, 0, nr);
     } else {
         float *ml = ws + (uint64_t)n_items * H * n_chunks * D;
-        attn_unit<D, Q8, NT, PK>(pool, pool_blocks, q, blocks, H, geo, err, item, g, hc, n, tab,
+        attn_unit<D, Q8, NT, PK, NR>(pool, pool_blocks, q, blocks, H, geo, err, item, g, hc, n, tab,
                                  t_begin, t_end, ws + (oh0 * n_chunks + chunk) * D,
                                  (uint64_t)n_chunks * D, ml + (oh0 * n_chunks + chunk) * 2,
-                                 (uint64_t)n_chunks * 2);
+                                 (uint64_t)n_chunks * 2, nr);
     }
 }
 
@@ -868,14 +876,14 @@ __device__ __forceinline__ void attn_body(QV_ATTN_PARAMS) {
 // the 4 waves.  Head hh's result goes to o_base[hh * o_stride + d]: the output (ml_base
 // null) or, for part of the context, the unnormalised partial with its max and sum at
 // ml_base[hh * ml_stride] (log2 domain).
-template <int D, bool Q8, bool NT, bool PK>
+template <int D, bool Q8, bool NT, bool PK, bool NR>
 __device__ __forceinline__ void attn_unit(const uint8_t *__restrict__ pool, uint64_t pool_blocks,
                                           const float *__restrict__ q,
                                           const uint32_t *__restrict__ blocks, uint32_t H,
                                           const Geo &geo, int *err, uint32_t item, uint32_t g,
                                           uint32_t hc, uint32_t n, uint32_t tab, uint32_t t_begin,
                                           uint32_t t_end, float *o_base, uint64_t o_stride,
-                                          float *ml_base, uint64_t ml_stride) {
+                                          float *ml_base, uint64_t ml_stride, NewRows nr) {
     constexpr int NJ = D / 16;  // MFMA steps over d
     __shared__ float sm[4][8], sl[4][8];
     __shared__ float so[4][8][D];
@@ -928,9 +936,26 @@ __device__ __forceinline__ void attn_unit(const uint8_t *__restrict__ pool, uint
             compute_tile<D, Q8, PK>(cur, st, qf, n, n, qg, hi_col, sigma);
         }
     } else {
-        for (uint32_t tt = t_begin + w; tt < t_end; tt += 4) {
+        // NR: the unit's last tile holds the appended position; its wave takes it after
+        // the loop (the same order), so the loop body is the plain kernel's
+        const uint32_t t_last = NR ? (n - 1) / 16 : t_end;
+        uint32_t tt = t_begin + w;
+        for (; tt < t_end && tt != t_last; tt += 4) {
             Tile<D, Q8> cur;
             load_tile<D, Q8, NT>(cur, tt, pool, pool_blocks, blocks, tab, g, c, qg, geo, err);
+            compute_tile<D, Q8, PK>(cur, st, qf, n, n, qg, hi_col, sigma);
+        }
+        if (NR && tt < t_end) {  // tt == t_last: position n - 1 comes from the new rows
+            Tile<D, Q8> cur;
+            load_tile<D, Q8, NT>(cur, tt, pool, pool_blocks, blocks, tab, g, c, qg, geo, err);
+            if (cur.ok) {  // (the block is valid) the first head chunk also stores the rows
+                const uint32_t blk = blocks[tab + (n - 1) / B];
+                uint8_t *row = (uint8_t *)pool + (uint64_t)blk * geo.bb +
+                               ((uint64_t)g * B + (n - 1) % B) * D * 2u;
+                const uint64_t at = (uint64_t)item * geo.kv_out + (uint64_t)g * D;
+                patch_new_row<D>(cur, (n - 1) & 15u, nr.k + at, nr.v + at, row + geo.k_off,
+                                 row + geo.v_off, c, qg, hc == 0);
+            }
             compute_tile<D, Q8, PK>(cur, st, qf, n, n, qg, hi_col, sigma);
         }
     }
@@ -1081,7 +1106,7 @@ __device__ __forceinline__ uint32_t stream_item(const uint64_t *cum, uint32_t n_
         const uint32_t *__restrict__ blocks, uint64_t n_table,                                  \
         const uint32_t *__restrict__ table_at, const uint32_t *__restrict__ pos,                \
         uint32_t n_items, uint32_t H, uint32_t max_pos, float *__restrict__ out,                \
-        float *__restrict__ ws, uint32_t hc_n, Geo geo, int *err
+        float *__restrict__ ws, uint32_t hc_n, Geo geo, int *err, NewRows nr
 
 // A value every lane holds alike, moved to scalar registers.
 __device__ __forceinline__ uint32_t uni(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
@@ -1090,7 +1115,7 @@ __device__ __forceinline__ uint64_t uni(uint64_t v) {
            __builtin_amdgcn_readfirstlane((uint32_t)v);
 }
 
-template <int D, bool Q8, bool NT, bool PK>
+template <int D, bool Q8, bool NT, bool PK, bool NR>
 __device__ __forceinline__ void attn_stream_body(QV_STREAM_PARAMS) {
     __shared__ uint64_t cum[STREAM_MAX_ITEMS + 1];
     const uint32_t G = (uint32_t)geo.G, B = (uint32_t)geo.B;
@@ -1135,12 +1160,13 @@ __device__ __forceinline__ void attn_stream_body(QV_STREAM_PARAMS) {
         const uint32_t n = uni(pos[item]) + 1, tab = uni(table_at[item]);
         const uint64_t oh0 = (uint64_t)item * H + (uint64_t)g * GS + hc * 8;
         if (t0 == 0 && seg_end == unit_end) {
-            attn_unit<D, Q8, NT, PK>(pool, pool_blocks, q, blocks, H, geo, err, item, g, hc, n,
-                                     tab, t0, t1, out + oh0 * D, D, nullptr, 0);
+            attn_unit<D, Q8, NT, PK, NR>(pool, pool_blocks, q, blocks, H, geo, err, item, g, hc, n,
+                                     tab, t0, t1, out + oh0 * D, D, nullptr, 0, nr);
         } else {
             const uint64_t slot = 2ull * w + (first ? 0u : 1u);
-            attn_unit<D, Q8, NT, PK>(pool, pool_blocks, q, blocks, H, geo, err, item, g, hc, n,
-                                     tab, t0, t1, ws + slot * 8 * D, D, ml + slot * 8 * 2, 2);
+            attn_unit<D, Q8, NT, PK, NR>(pool, pool_blocks, q, blocks, H, geo, err, item, g, hc, n,
+                                     tab, t0, t1, ws + slot * 8 * D, D, ml + slot * 8 * 2, 2,
+                                     nr);
         }
         first = false;
         x = seg_end;
@@ -1149,14 +1175,21 @@ __device__ __forceinline__ void attn_stream_body(QV_STREAM_PARAMS) {
 
 template <int D, bool Q8, bool NT, bool PK>
 __global__ __launch_bounds__(256) void k_attn_stream(QV_STREAM_PARAMS) {
-    attn_stream_body<D, Q8, NT, PK>(pool, pool_blocks, q, blocks, n_table, table_at, pos, n_items,
-                                    H, max_pos, out, ws, hc_n, geo, err);
+    attn_stream_body<D, Q8, NT, PK, false>(pool, pool_blocks, q, blocks, n_table, table_at, pos, n_items,
+                                    H, max_pos, out, ws, hc_n, geo, err, nr);
 }
 template <int D, bool Q8, bool NT, bool PK, int W>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W)))
 void k_attn_stream_w(QV_STREAM_PARAMS) {
-    attn_stream_body<D, Q8, NT, PK>(pool, pool_blocks, q, blocks, n_table, table_at, pos, n_items,
-                                    H, max_pos, out, ws, hc_n, geo, err);
+    attn_stream_body<D, Q8, NT, PK, false>(pool, pool_blocks, q, blocks, n_table, table_at, pos, n_items,
+                                    H, max_pos, out, ws, hc_n, geo, err, nr);
+}
+template <int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 3)))
+void k_attn_stream_nr(QV_STREAM_PARAMS) {
+    attn_stream_body<D, false, true, false, true>(pool, pool_blocks, q, blocks, n_table,
+                                                  table_at, pos, n_items, H, max_pos, out, ws,
+                                                  hc_n, geo, err, nr);
 }
 
 // Merge for k_attn_stream: block = one (item, query head), D threads.  The unit's
@@ -1502,11 +1535,40 @@ int plan_attention(const Geometry &g, uint32_t n_items, uint32_t heads, uint32_t
     return QVKV_OK;
 }
 
+bool fused_append_attention(const Geometry &g) {
+    return g.dtype == QVKV_F16 && (g.D == 64 || g.D == 128 || g.D == 256);
+}
+
+__global__ __launch_bounds__(256) void k_slots_at(const uint32_t *__restrict__ blocks,
+                                                  uint64_t n_table,
+                                                  const uint32_t *__restrict__ table_at,
+                                                  const uint32_t *__restrict__ pos,
+                                                  uint32_t n_items, uint32_t max_pos, uint32_t B,
+                                                  uint32_t *__restrict__ slots, int *err) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= n_items) return;
+    const uint32_t p = pos[i];
+    uint32_t slot = 0xffffffffu;
+    if (p > max_pos) flag(err, ERR_POS);
+    else if ((uint64_t)table_at[i] + p / B >= n_table) flag(err, ERR_TABLE);
+    else slot = blocks[table_at[i] + p / B] * B + p % B;
+    slots[i] = slot;
+}
+
+hipError_t launch_slots_at(const Geometry &g, const uint32_t *blocks, uint64_t n_table,
+                           const uint32_t *table_at, const uint32_t *pos, uint32_t n_items,
+                           uint32_t max_pos, uint32_t *slots, int *err, hipStream_t s) {
+    if (n_items == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_slots_at, dim3((n_items + 255) / 256), dim3(256), 0, s, blocks, n_table,
+                       table_at, pos, n_items, max_pos, (uint32_t)g.B, slots, err);
+    return hipGetLastError();
+}
+
 hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *pool,
                             uint64_t pool_blocks, const float *q, const uint32_t *blocks,
                             uint64_t n_table, const uint32_t *table_at, const uint32_t *pos,
                             uint32_t n_items, uint32_t heads, uint32_t max_pos, float *out,
-                            void *ws, int *err, hipStream_t s) {
+                            void *ws, int *err, hipStream_t s, NewRows nr) {
     if (n_items == 0) return hipSuccess;
     const Geo geo = to_geo(g);
     const uint8_t *pp = (const uint8_t *)pool;
@@ -1531,24 +1593,33 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
 #define QV_AS(DD, QQ, PK)                                                                       \
     hipLaunchKernelGGL((k_attn_stream<DD, QQ, true, PK>), dim3(P), dim3(256), 0, s, pp,          \
                        pool_blocks, q, blocks, n_table, table_at, pos, n_items, heads, max_pos,  \
-                       out, wsf, p.hc, geo, err)
+                       out, wsf, p.hc, geo, err, nr)
+#define QV_AS_NR(DD)                                                                            \
+    hipLaunchKernelGGL((k_attn_stream_nr<DD>), dim3(P), dim3(256), 0, s,                        \
+                       pp, pool_blocks, q, blocks, n_table, table_at, pos, n_items, heads,      \
+                       max_pos, out, wsf, p.hc, geo, err, nr)
 #define QV_AS_W4(DD, QQ, PK)                                                                    \
     hipLaunchKernelGGL((k_attn_stream_w<DD, QQ, true, PK, 4>), dim3(P), dim3(256), 0, s, pp,     \
                        pool_blocks, q, blocks, n_table, table_at, pos, n_items, heads, max_pos,  \
-                       out, wsf, p.hc, geo, err)
+                       out, wsf, p.hc, geo, err, nr)
         if (g.D == 64) {
-            if (!q8) QV_AS(64, false, false);
+            if (!q8) { if (nr.k) QV_AS_NR(64); else QV_AS(64, false, false); }
             else if (pk) QV_AS(64, true, true);
             else QV_AS(64, true, false);
         } else if (g.D == 128) {
-            if (!q8) { if (w4) QV_AS_W4(128, false, false); else QV_AS(128, false, false); }
+            if (!q8) {
+                if (nr.k) QV_AS_NR(128);
+                else if (w4) QV_AS_W4(128, false, false);
+                else QV_AS(128, false, false);
+            }
             else if (pk) { if (w4) QV_AS_W4(128, true, true); else QV_AS(128, true, true); }
             else { if (w4) QV_AS_W4(128, true, false); else QV_AS(128, true, false); }
         } else {
-            if (!q8) QV_AS(256, false, false);
+            if (!q8) { if (nr.k) QV_AS_NR(256); else QV_AS(256, false, false); }
             else if (pk) QV_AS(256, true, true);
             else QV_AS(256, true, false);
         }
+#undef QV_AS_NR
 #undef QV_AS_W4
 #undef QV_AS
         hipError_t e = hipGetLastError();
@@ -1569,24 +1640,33 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
 #define QV_ATTN(DD, QQ, PK)                                                                     \
     hipLaunchKernelGGL((k_attn_mfma<DD, QQ, true, PK>), dim3((unsigned)grid), dim3(256), 0, s,  \
                        pp, pool_blocks, q, blocks, n_table, table_at, pos, n_items, heads,      \
-                       max_pos, out, wsf, p.hc, p.n_chunks, p.tpc, geo, err)
+                       max_pos, out, wsf, p.hc, p.n_chunks, p.tpc, geo, err, nr)
 #define QV_ATTN_W4(DD, QQ, PK)                                                                  \
     hipLaunchKernelGGL((k_attn_mfma_w<DD, QQ, true, PK, 4>), dim3((unsigned)grid), dim3(256),   \
                        0, s, pp, pool_blocks, q, blocks, n_table, table_at, pos, n_items,       \
-                       heads, max_pos, out, wsf, p.hc, p.n_chunks, p.tpc, geo, err)
+                       heads, max_pos, out, wsf, p.hc, p.n_chunks, p.tpc, geo, err, nr)
+#define QV_ATTN_NR(DD)                                                                          \
+    hipLaunchKernelGGL((k_attn_mfma_nr<DD>), dim3((unsigned)grid),                              \
+                       dim3(256), 0, s, pp, pool_blocks, q, blocks, n_table, table_at, pos,     \
+                       n_items, heads, max_pos, out, wsf, p.hc, p.n_chunks, p.tpc, geo, err, nr)
     if (g.D == 64) {
-        if (!q8) QV_ATTN(64, false, false);
+        if (!q8) { if (nr.k) QV_ATTN_NR(64); else QV_ATTN(64, false, false); }
         else if (pk) QV_ATTN(64, true, true);
         else QV_ATTN(64, true, false);
     } else if (g.D == 128) {
-        if (!q8) { if (w4) QV_ATTN_W4(128, false, false); else QV_ATTN(128, false, false); }
+        if (!q8) {
+            if (nr.k) QV_ATTN_NR(128);
+            else if (w4) QV_ATTN_W4(128, false, false);
+            else QV_ATTN(128, false, false);
+        }
         else if (pk) { if (w4) QV_ATTN_W4(128, true, true); else QV_ATTN(128, true, true); }
         else { if (w4) QV_ATTN_W4(128, true, false); else QV_ATTN(128, true, false); }
     } else {
-        if (!q8) QV_ATTN(256, false, false);
+        if (!q8) { if (nr.k) QV_ATTN_NR(256); else QV_ATTN(256, false, false); }
         else if (pk) QV_ATTN(256, true, true);
         else QV_ATTN(256, true, false);
     }
+#undef QV_ATTN_NR
 #undef QV_ATTN_W4
 #undef QV_ATTN
     hipError_t e = hipGetLastError();

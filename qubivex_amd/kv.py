@@ -187,6 +187,16 @@ class HipDevice:
                                     _ptr(out_at), lens.numel(), max_len, od, out_positions,
                                     _ptr(out_k), _ptr(out_v), _stream(stream)))
 
+    def append_attention(self, layout: KvLayout, pool, pool_blocks, q, k_new, v_new, blocks,
+                         table_at, pos, heads, max_pos, out, stream=None):
+        """Stores each item's new key and value rows at its position pos[i], then attends over
+        0..pos[i] (the reference's DeviceMoeAttention submission; one launch for f16 pools)."""
+        check(lib.qvkv_append_attention_async(self.handle, ctypes.byref(layout.c), _ptr(pool),
+                                              pool_blocks, _ptr(q), _ptr(k_new), _ptr(v_new),
+                                              _ptr(blocks), blocks.numel(), _ptr(table_at),
+                                              _ptr(pos), pos.numel(), heads, max_pos, _ptr(out),
+                                              _stream(stream)))
+
     def attention(self, layout: KvLayout, pool, pool_blocks, q, blocks, table_at, pos, heads,
                   max_pos, out, stream=None):
         check(lib.qvkv_attention_async(self.handle, ctypes.byref(layout.c), _ptr(pool),
