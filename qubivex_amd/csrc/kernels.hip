@@ -117,9 +117,10 @@ __device__ __forceinline__ AppendItem append_item(uint32_t w, uint32_t total, ui
     return it;
 }
 
-// U chunks per thread per round, all loads issued before any store.
-template <int DT, int U, bool NT, int DD>
-__global__ __launch_bounds__(256) void k_append(uint8_t *__restrict__ pool, uint64_t pool_blocks,
+// U chunks per thread per round, all loads issued before any store.  (64-thread workgroups,
+// which help the block copy, measured slower here: 5.09-5.24 against 5.43-5.47 TB/s.)
+template <int DT, int U, bool NT, int DD, int T = 256>
+__global__ __launch_bounds__(T) void k_append(uint8_t *__restrict__ pool, uint64_t pool_blocks,
                                                 const float *__restrict__ k,
                                                 const float *__restrict__ v,
                                                 const uint32_t *__restrict__ slots, uint32_t n,
@@ -127,12 +128,12 @@ __global__ __launch_bounds__(256) void k_append(uint8_t *__restrict__ pool, uint
     const uint32_t cpr = geo.kv_out >> 3;  // 8-value chunks per K (or V) row
     const uint32_t total = (DD ? (n + 15u) / 16u * 16u : n) * 2u * cpr;
     const uint32_t D = DD ? (uint32_t)DD : (uint32_t)geo.D;
-    for (uint32_t b0 = blockIdx.x * 256u * U; b0 < total; b0 += gridDim.x * 256u * U) {
+    for (uint32_t b0 = blockIdx.x * (uint32_t)T * U; b0 < total; b0 += gridDim.x * (uint32_t)T * U) {
         AppendItem its[U];
         float4 xa[U], xb[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            its[u] = append_item<DD>(b0 + u * 256u + threadIdx.x, total, n, cpr, fd_row, pool,
+            its[u] = append_item<DD>(b0 + u * (uint32_t)T + threadIdx.x, total, n, cpr, fd_row, pool,
                                      pool_blocks, k, v, slots, geo, err);
             if (its[u].ok) {
                 xa[u] = load_f4<NT>(its[u].src);
@@ -742,15 +743,16 @@ __global__ __launch_bounds__(256) void k_gather_q8(const uint8_t *__restrict__ p
 }
 
 // ---------------------------------------------------------------------------------
-// Block copy: workgroup = U * 4 KiB of one (src, dst) pair, all loads before stores.
+// Block copy: workgroup = T threads x U x 16 bytes of one (src, dst) pair, all loads before
+// stores.
 // ---------------------------------------------------------------------------------
-template <int U>
-__global__ __launch_bounds__(256) void k_block_copy(uint8_t *__restrict__ pool,
-                                                    uint64_t pool_blocks,
-                                                    const uint32_t *__restrict__ src,
-                                                    const uint32_t *__restrict__ dst,
-                                                    uint32_t n, uint32_t wgs_per_block,
-                                                    uint64_t bb, int *err) {
+template <int U, int T = 256>
+__global__ __launch_bounds__(T) void k_block_copy(uint8_t *__restrict__ pool,
+                                                  uint64_t pool_blocks,
+                                                  const uint32_t *__restrict__ src,
+                                                  const uint32_t *__restrict__ dst,
+                                                  uint32_t n, uint32_t wgs_per_block,
+                                                  uint64_t bb, int *err) {
     const uint32_t pair = blockIdx.x / wgs_per_block;
     const uint32_t part = blockIdx.x - pair * wgs_per_block;
     if (pair >= n) return;
@@ -762,16 +764,16 @@ __global__ __launch_bounds__(256) void k_block_copy(uint8_t *__restrict__ pool,
     const u4v *from = (const u4v *)(pool + (uint64_t)s * bb);
     u4v *to = (u4v *)(pool + (uint64_t)d * bb);
     const uint64_t words = bb >> 4;
-    const uint64_t begin = (uint64_t)part * 256u * U;
+    const uint64_t begin = (uint64_t)part * T * U;
     u4v r[U];
 #pragma unroll
     for (int u = 0; u < U; u++) {
-        const uint64_t i = begin + threadIdx.x + u * 256u;
+        const uint64_t i = begin + threadIdx.x + u * T;
         if (i < words) r[u] = __builtin_nontemporal_load(from + i);
     }
 #pragma unroll
     for (int u = 0; u < U; u++) {
-        const uint64_t i = begin + threadIdx.x + u * 256u;
+        const uint64_t i = begin + threadIdx.x + u * T;
         if (i < words) __builtin_nontemporal_store(r[u], to + i);
     }
 }
@@ -1357,8 +1359,8 @@ int tune(const char *name, int def) {
 // A streaming kernel runs best with short-lived workgroups (one pass each): the hardware
 // dispatcher then keeps every CU full through the tail, where strided loops leave
 // stragglers.
-static unsigned grid_for(uint64_t threads, uint64_t per_cu) {
-    uint64_t wgs = (threads + 255) / 256;
+static unsigned grid_for(uint64_t threads, uint64_t per_cu, uint64_t wg = 256) {
+    uint64_t wgs = (threads + wg - 1) / wg;
     const uint64_t cap = 256ull * per_cu;
     return (unsigned)(wgs < 1 ? 1 : (wgs > cap ? cap : wgs));
 }
@@ -1468,16 +1470,33 @@ hipError_t launch_block_copy(const Geometry &g, void *pool, uint64_t pool_blocks
                              const uint32_t *src, const uint32_t *dst, uint32_t n, int *err,
                              hipStream_t s) {
     if (n == 0) return hipSuccess;
-    const int U = tune("QVKV_COPY_U", 4) >= 8 ? 8 : 4;
-    const uint32_t per = (uint32_t)((g.block_bytes / 16 + 256 * U - 1) / (256 * U));
+    // One wave per workgroup, 16 bytes per lane (1 KiB of a pair per workgroup): many short
+    // workgroups keep the most copies in flight.  Measured against 256 threads x 4 (16 KiB):
+    // 32 KiB blocks 6.34-6.39 vs 5.61-5.66 TB/s, cfg4 compaction (64 KiB blocks) 5.43-5.53
+    // vs 5.00-5.05; 2 or 4 per lane, 128 or 256 threads, and 8 per lane were slower.
+    const int ut = tune("QVKV_COPY_U", 1);
+    const int U = ut >= 8 ? 8 : ut >= 4 ? 4 : ut >= 2 ? 2 : 1;
+    const int tt = tune("QVKV_COPY_T", 64);
+    const int T = tt >= 256 ? 256 : tt >= 128 ? 128 : 64;
+    const uint32_t per = (uint32_t)((g.block_bytes / 16 + (uint64_t)T * U - 1) / ((uint64_t)T * U));
     const uint64_t grid = (uint64_t)per * n;
     if (grid > 0x7fffffffull) return hipErrorInvalidValue;
-    if (U == 8)
-        hipLaunchKernelGGL(k_block_copy<8>, dim3((unsigned)grid), dim3(256), 0, s, (uint8_t *)pool,
-                           pool_blocks, src, dst, n, per, g.block_bytes, err);
-    else
-        hipLaunchKernelGGL(k_block_copy<4>, dim3((unsigned)grid), dim3(256), 0, s, (uint8_t *)pool,
-                           pool_blocks, src, dst, n, per, g.block_bytes, err);
+#define QV_BC(UU, TT)                                                                           \
+    hipLaunchKernelGGL((k_block_copy<UU, TT>), dim3((unsigned)grid), dim3(TT), 0, s,             \
+                       (uint8_t *)pool, pool_blocks, src, dst, n, per, g.block_bytes, err)
+    if (T == 256) {
+        if (U == 8) QV_BC(8, 256);
+        else if (U == 4) QV_BC(4, 256);
+        else if (U == 2) QV_BC(2, 256);
+        else QV_BC(1, 256);
+    } else if (T == 128) {
+        QV_BC(1, 128);
+    } else {
+        if (U >= 4) QV_BC(4, 64);
+        else if (U == 2) QV_BC(2, 64);
+        else QV_BC(1, 64);
+    }
+#undef QV_BC
     return hipGetLastError();
 }
 
