@@ -182,8 +182,10 @@ def test_gather_bit_exact(hip, dtype, G, D):
             assert np.array_equal(hk, oracle.f16_bits(wk).reshape(G, n, D)), f"item {t} f16 keys"
 
 
-def test_block_copy_bytes(hip):
-    L = layout(F16, 8, 128)
+@pytest.mark.parametrize("dtype,G,D", [(F16, 8, 128), (Q8_0, 3, 160), (Q8_0, 2, 64), (F16, 1, 200)])
+def test_block_copy_bytes(hip, dtype, G, D):
+    """Blocks of 64 KiB and of sizes that are not a multiple of one workgroup's 1 KiB."""
+    L = layout(dtype, G, D)
     N = 64
     pool = new_pool(L, N, fill=11)
     before = pool.cpu().numpy().reshape(N, -1).copy()
