@@ -434,8 +434,9 @@ __device__ __forceinline__ void store_f8(float *dst, const float *y) {
     __builtin_nontemporal_store(f4v{y[4], y[5], y[6], y[7]}, (f4v *)(dst + 4));
 }
 
-template <int DT, int OUT>
-__global__ __launch_bounds__(256) void k_gather(const uint8_t *__restrict__ pool,
+// T threads per workgroup; UF: loads in flight per thread in the f16 -> f16 copy.
+template <int DT, int OUT, int T = 256, int UF = 8>
+__global__ __launch_bounds__(T) void k_gather(const uint8_t *__restrict__ pool,
                                                 uint64_t pool_blocks,
                                                 const uint32_t *__restrict__ blocks,
                                                 uint64_t n_table,
@@ -475,15 +476,15 @@ __global__ __launch_bounds__(256) void k_gather(const uint8_t *__restrict__ pool
     const uint32_t c8 = D >> 3;                 // 8-value chunks per row
     const uint32_t per_kv = G * 16u * c8;       // chunks per tile for K (or V)
     if (DT == QVKV_F16 && OUT == QVKV_F16) {
-        // A byte copy of the tile's rows: 8 loads in flight per thread, then 8 stores.
-        constexpr int U = 8;
-        for (uint32_t b0 = part * 256u * U; b0 < 2u * per_kv; b0 += parts * 256u * U) {
+        // A byte copy of the tile's rows: UF loads in flight per thread, then UF stores.
+        constexpr int U = UF;
+        for (uint32_t b0 = part * (uint32_t)T * U; b0 < 2u * per_kv; b0 += parts * (uint32_t)T * U) {
             u4v x[U];
             uint16_t *dst[U];
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 dst[u] = nullptr;
-                const uint32_t idx = b0 + u * 256u + threadIdx.x;
+                const uint32_t idx = b0 + u * (uint32_t)T + threadIdx.x;
                 if (idx >= 2u * per_kv) continue;
                 const bool isv = idx >= per_kv;
                 uint32_t r = isv ? idx - per_kv : idx;
@@ -1458,6 +1459,22 @@ hipError_t launch_gather(const Geometry &g, const void *pool, uint64_t pool_bloc
     if (g.dtype == QVKV_Q8_0 && q8fast && g.D == 64) QV_GATHER_Q8(64);
     else if (g.dtype == QVKV_Q8_0 && q8fast && g.D == 128) QV_GATHER_Q8(128);
     else if (g.dtype == QVKV_Q8_0 && q8fast && g.D == 256) QV_GATHER_Q8(256);
+    else if (g.dtype == QVKV_F16 && out_dtype == QVKV_F16 && tune("QVKV_GATHER_T", 64) == 64) {
+        // f16 -> f16: one-wave workgroups of 4 loads per lane (4 KiB of a tile each), as for
+        // the block copy.  Measured (4 runs each): cfg2 6.25-6.59 against 5.77-6.30 TB/s
+        // for 256 threads x 8, cfg5 5.96-6.41 against 5.74-6.39; 1, 2 or 8 per lane slower.
+        const int uf = tune("QVKV_GATHER_UF", 4);
+        const uint32_t UFv = uf >= 8 ? 8 : uf >= 4 ? 4 : uf >= 2 ? 2 : 1;
+        const uint32_t parts64 = (uint32_t)((vals + 64ull * UFv * 8 - 1) / (64ull * UFv * 8));
+#define QV_G64(UU)                                                                              \
+    hipLaunchKernelGGL((k_gather<QVKV_F16, QVKV_F16, 64, UU>), dim3((unsigned)(grid * parts64)),  \
+                       dim3(64), 0, s, p, pool_blocks, blocks, n_table, table_at, lens, out_at,  \
+                       n_items, tiles, out_positions, out_k, out_v, parts64, geo, err)
+        if (grid * parts64 > 0x7fffffffull) return hipErrorInvalidValue;
+        if (UFv == 8) QV_G64(8); else if (UFv == 4) QV_G64(4); else if (UFv == 2) QV_G64(2);
+        else QV_G64(1);
+#undef QV_G64
+    }
     else if (g.dtype == QVKV_F16 && out_dtype == QVKV_F16) QV_GATHER(QVKV_F16, QVKV_F16);
     else if (g.dtype == QVKV_F16) QV_GATHER(QVKV_F16, QVKV_F32);
     else QV_GATHER(QVKV_Q8_0, QVKV_F32);
