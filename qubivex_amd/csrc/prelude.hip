@@ -376,6 +376,130 @@ __global__ __launch_bounds__(256) void k_prelude_r(float *__restrict__ q, float 
     prelude_heads<D, FULL, HB>(x, bias, h0, nh, part, t, lane, a);
 }
 
+// Full-row norm (QkNorm::Full), rows up to 4096 values.  Lane l owns elements 64 j + l of a
+// row as in the reference's reduction; a row's j are spread over WPR waves of a workgroup
+// (16 each), so its loads are spread too (16 values per lane per wave instead of up to 64
+// in one), and a workgroup holds 4 / WPR rows.  The sum of squares stays lane l's fused
+// multiply-add chain over j in order: with WPR > 1 each wave continues the running sum the
+// wave before left in LDS.  The RoPE pairs of a head lie in one wave (a head is d/64
+// consecutive j).  rows: q rows (part 0, row = token), or k and v rows (row 2 t + 0 / 1).
+template <int D, int WPR>
+__global__ __launch_bounds__(256) void k_prelude_full(float *__restrict__ q, float *__restrict__ k,
+                                                      float *__restrict__ v, uint32_t s,
+                                                      uint32_t heads, uint32_t kvh, bool kv_rows,
+                                                      PreludeArgs a) {
+    constexpr uint32_t JW = 16;            // elements per lane per wave
+    constexpr uint32_t JD = D / 64;        // elements per lane per head
+    constexpr uint32_t RPW = 4 / WPR;      // rows per workgroup
+    __shared__ float run[RPW][64];
+    __shared__ float scale_of_row[RPW];
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t rw = w / WPR, wr = w % WPR;  // the wave's row in the workgroup, its part of it
+    const uint32_t row = blockIdx.x * RPW + rw;
+    const bool live = row < (kv_rows ? 2 * s : s);
+    const uint32_t t = kv_rows ? row / 2 : row;
+    const uint32_t part = kv_rows ? 1u + (row & 1u) : 0u;
+    const uint32_t nh = part == 0 ? heads : kvh;
+    const uint32_t J = nh * JD;            // elements per lane in the row (at most 64)
+    const uint32_t j0 = wr * JW;
+    const uint32_t nj = live && J > j0 ? (J - j0 < JW ? J - j0 : JW) : 0u;
+    float *x = (part == 0 ? q : part == 1 ? k : v) + (uint64_t)t * nh * D;
+    const float *bias = part == 0 ? a.q_bias : part == 1 ? a.k_bias : a.v_bias;
+    float z[JW];
+#pragma unroll
+    for (uint32_t u = 0; u < JW; u++)
+        z[u] = u < nj ? __builtin_nontemporal_load(&x[64 * (j0 + u) + lane]) : 0.0f;
+#pragma unroll
+    for (uint32_t u = 0; u < JW; u++) {
+        float y = z[u];
+        if (bias && u < nj) y = y + bias[64 * (j0 + u) + lane];
+        if (a.has_clip) y = y < -a.clip ? -a.clip : (y > a.clip ? a.clip : y);
+        z[u] = y;
+    }
+    // (every wave of a workgroup takes the barriers: the norm's presence is per launch for
+    // q rows; k and v rows alternate, and only the k rows' waves use the chain)
+    const float *wn = part == 0 ? a.q_norm : part == 1 ? a.k_norm : nullptr;
+    const bool norm_any = kv_rows ? a.k_norm != nullptr : a.q_norm != nullptr;
+    if (norm_any) {
+        float acc = 0.0f;
+        if constexpr (WPR == 1) {
+#pragma unroll
+            for (uint32_t u = 0; u < JW; u++)
+                if (u < nj) acc = fmaf(z[u], z[u], acc);
+        } else {
+            for (uint32_t step = 0; step < WPR; step++) {
+                if (wr == step) {
+                    acc = step == 0 ? 0.0f : run[rw][lane];
+#pragma unroll
+                    for (uint32_t u = 0; u < JW; u++)
+                        if (u < nj) acc = fmaf(z[u], z[u], acc);
+                    run[rw][lane] = acc;
+                }
+                __syncthreads();
+            }
+            acc = run[rw][lane];
+        }
+        float rs = 0.0f;
+        if constexpr (WPR == 1) {
+            rs = rms_scale_of(lane_tree_x(acc), (float)(nh * D), a.eps);
+        } else {
+            if (wr == 0) {
+                const float r = rms_scale_of(lane_tree_x(acc), (float)(nh * D), a.eps);
+                if (lane == 0) scale_of_row[rw] = r;
+            }
+            __syncthreads();
+            rs = scale_of_row[rw];
+        }
+        if (wn != nullptr) {
+#pragma unroll
+            for (uint32_t u = 0; u < JW; u++)
+                if (u < nj) z[u] = (z[u] * rs) * wn[64 * (j0 + u) + lane];
+        }
+    }
+    if (part != 2 && nj != 0) {
+        const float *cs = a.rope + (uint64_t)t * D;
+        if constexpr (D == 64) {
+            const uint32_t i = lane & 31u;
+            const float c = cs[i], sn = cs[32 + i];
+            const bool first = lane < 32;
+#pragma unroll
+            for (uint32_t u = 0; u < JW; u++) {
+                // v_permlane32_swap of z with itself: lanes l and l ^ 32 both get
+                // (x[l mod 32], x[l mod 32 + 32]) = (x1, x2) of their pair
+                const uint32_t zu = __builtin_bit_cast(uint32_t, z[u]);
+                const auto pr = __builtin_amdgcn_permlane32_swap(zu, zu, false, false);
+                const uint32_t u1 = pr[0], u2 = pr[1];
+                const float x1 = __builtin_bit_cast(float, u1);
+                const float x2 = __builtin_bit_cast(float, u2);
+                const float p1 = x1 * c, p2 = x2 * sn, p3 = x2 * c, p4 = x1 * sn;
+                z[u] = first ? p1 - p2 : p3 + p4;
+            }
+        } else {
+            constexpr uint32_t JH = JD / 2;  // pairs (jj, jj + JH) of a head
+            float c[JH], sn[JH];
+#pragma unroll
+            for (uint32_t jj = 0; jj < JH; jj++) {
+                c[jj] = cs[64 * jj + lane];
+                sn[jj] = cs[D / 2 + 64 * jj + lane];
+            }
+#pragma unroll
+            for (uint32_t h = 0; h < JW / JD; h++)
+#pragma unroll
+                for (uint32_t jj = 0; jj < JH; jj++) {
+                    const float x1 = z[h * JD + jj], x2 = z[h * JD + jj + JH];
+                    const float p1 = x1 * c[jj], p2 = x2 * sn[jj], p3 = x2 * c[jj],
+                                p4 = x1 * sn[jj];
+                    z[h * JD + jj] = p1 - p2;
+                    z[h * JD + jj + JH] = p3 + p4;
+                }
+        }
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < JW; u++)
+        if (u < nj) __builtin_nontemporal_store(z[u], &x[64 * (j0 + u) + lane]);
+}
+
 hipError_t launch_prelude(float *q, float *k, float *v, uint32_t s, uint32_t heads,
                           uint32_t kvh, uint32_t d, const PreludeArgs &a, hipStream_t st) {
     if (s == 0) return hipSuccess;
@@ -386,6 +510,34 @@ hipError_t launch_prelude(float *q, float *k, float *v, uint32_t s, uint32_t hea
         // +2 % at 32 query heads; 5 % slower at d = 256, equal at d = 64)
         const bool wide = !full && a.norm == QVKV_NORM_PER_HEAD && d == 128 &&
                           tune("QVKV_PRELUDE_WIDE", 1) != 0;
+        if (full && tune("QVKV_PRELUDE_FULL_WG", 1) != 0) {
+            // q rows, then k and v rows: waves per row by the row's length (16 values per
+            // lane per wave)
+            for (int kv = 0; kv < 2; kv++) {
+                const uint32_t J = (kv ? kvh : heads) * (d / 64);
+                const int wpr = J > 32 ? 4 : J > 16 ? 2 : 1;
+                const uint64_t rows = (uint64_t)s * (kv ? 2 : 1);
+                const uint64_t grid = (rows * wpr + 3) / 4;
+                if (grid > 0x7fffffffull) return hipErrorInvalidValue;
+#define QV_PRE_FULL(DD, WW)                                                                     \
+    hipLaunchKernelGGL((k_prelude_full<DD, WW>), dim3((unsigned)grid), dim3(256), 0, st, q, k, v, \
+                       s, heads, kvh, kv != 0, a)
+#define QV_PRE_FULL_D(DD)                                                                       \
+    do {                                                                                        \
+        if (wpr == 4) QV_PRE_FULL(DD, 4);                                                       \
+        else if (wpr == 2) QV_PRE_FULL(DD, 2);                                                  \
+        else QV_PRE_FULL(DD, 1);                                                                \
+    } while (0)
+                if (d == 64) QV_PRE_FULL_D(64);
+                else if (d == 128) QV_PRE_FULL_D(128);
+                else QV_PRE_FULL_D(256);
+#undef QV_PRE_FULL_D
+#undef QV_PRE_FULL
+                hipError_t e = hipGetLastError();
+                if (e != hipSuccess) return e;
+            }
+            return hipSuccess;
+        }
         const uint32_t hb = (full ? 4096u : wide ? 2048u : 1024u) / d;
         const uint32_t uq = (heads + hb - 1) / hb, ukv = (kvh + hb - 1) / hb;
         const uint64_t waves = (uint64_t)s * (uq + 2 * ukv);

@@ -39,6 +39,9 @@ CASES = [
     (16, 2, 256, "full", None, True, 2.0),
     (64, 8, 64, "full", 3.0, False, 4.0),
     (40, 8, 128, "full", None, True, 1.0),
+    # full-row norms whose rows take 2 waves (17-32 values per lane) and k rows of one wave
+    (16, 16, 128, "full", 4.0, True, 2.0),
+    (24, 2, 64, "full", None, False, 1.0),
 ]
 
 
