@@ -438,7 +438,8 @@ def test_graph_replays_of_append_and_attention_match_eager(hip):
     decode step in model order (per layer: append one row per sequence, then attention
     over the layer's items, through the split-by-work path with its merge) is captured into
     a HIP graph on that stream.  Every replay, with eager work and synchronizations between
-    replays, gives the eager step's outputs bit for bit."""
+    replays, gives the eager step's outputs bit for bit; so does the same step through
+    qvkv_append_attention_async, captured as well."""
     import torch
 
     from qubivex_amd import KvLayout, KvPool
@@ -498,4 +499,24 @@ def test_graph_replays_of_append_and_attention_match_eager(hip):
         hip.check(s)
         assert torch.equal(out, ref), rep
         del junk
+
+    # the same step through the fused entry point (one launch per layer), captured too
+    def fused_step():
+        for l in range(NL):
+            rows = slice(l * S, (l + 1) * S)
+            b, ta, p, mp = d_tabs[l]
+            hip.append_attention(L, mem, N, q[rows], kn[rows], vn[rows], b, ta, p, H, mp,
+                                 out[rows])
+
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2, stream=s):
+        fused_step()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g2.replay()
+        torch.cuda.synchronize()
+        hip.check(s)
+        assert torch.equal(out, ref), ("fused", rep)
     pool.close()
