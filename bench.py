@@ -712,24 +712,34 @@ def run_cfg1(args, dev):
         d_b, d_t, d_p, d_s, d_l = c32(blocks), c32(tat), c32(pos), c32(sl), c32(pos + 1)
         out_at = torch.from_numpy((np.arange(NL, dtype=np.int64) * n)).cuda()
         # the device path of one decode step: append, gather and attention of every layer
+        # (odd steps: the append inside the attention launch, qvkv_append_attention_async)
         evs[step][0].record(stream)
-        dev.append(L, mem, N, kn, kn, d_s)
-        dev.gather(L, mem, N, d_b, d_t, d_l, out_at, n, ok, ov, "f16")
-        dev.attention(L, mem, N, q, d_b, d_t, d_p, H, int(pos.max()), out)
+        if step % 2 == 0:
+            dev.append(L, mem, N, kn, kn, d_s)
+            dev.gather(L, mem, N, d_b, d_t, d_l, out_at, n, ok, ov, "f16")
+            dev.attention(L, mem, N, q, d_b, d_t, d_p, H, int(pos.max()), out)
+        else:
+            dev.append_attention(L, mem, N, q, kn, kn, d_b, d_t, d_p, H, int(pos.max()), out)
+            dev.gather(L, mem, N, d_b, d_t, d_l, out_at, n, ok, ov, "f16")
         evs[step][1].record(stream)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3
-    gpu = float(np.mean([a.elapsed_time(b) for a, b in evs]))
+    gpu = float(np.mean([a.elapsed_time(b) for a, b in evs[0::2]]))
+    gpu_f = float(np.mean([a.elapsed_time(b) for a, b in evs[1::2]]))
     dev.check()
     pool.close()
     res = {"prefill_append_ms": prefill_ms, "decode_steps": T, "decode_total_ms": wall,
            "decode_step_us": wall / T * 1e3, "decode_step_device_us": gpu * 1e3,
+           "decode_step_fused_device_us": gpu_f * 1e3,
            "note": "latency-bound: per step 16 layers x (append 1 + gather + attention); "
-                   "decode_step_us includes the Python host planning, decode_step_device_us is "
-                   "the three launches from the first to the last (HIP events); no roofline claim"}
+                   "decode_step_us includes the Python host planning; decode_step_device_us is "
+                   "the three launches from the first to the last (HIP events, even steps), "
+                   "decode_step_fused_device_us the two launches with the append inside the "
+                   "attention (odd steps); no roofline claim"}
     log(f"[bench] cfg1: prefill-append {P} x {NL} layers {prefill_ms:.2f} ms; {T} decode steps "
         f"(append + gather + attention, all layers) {wall:.1f} ms = {wall / T * 1e3:.0f} us/step "
-        f"with host planning, {gpu * 1e3:.1f} us/step on the device")
+        f"with host planning, {gpu * 1e3:.1f} us/step on the device ({gpu_f * 1e3:.1f} with the "
+        f"append fused into the attention launch)")
     return res
 
 
