@@ -180,10 +180,10 @@ int qvkv_attention_async(qvkv_dev *dev, const qvkv_layout *layout, const void *p
  * planning made writable), then attention runs over positions 0..pos[t] as in
  * qvkv_attention_async.  The reference's DeviceMoeAttention submission after its sync
  * rows: "the new token's key and value are stored at pos[t], and attention reads
- * positions 0..=pos[t]" (crates/qubivex-compute/src/discrete.rs:257-307).  f16 pools at
- * d = 64, 128, 256 run it as one launch (the attention takes position pos[t] from the new
- * rows and stores them); other layouts run the append and the attention in turn, on the
- * stream.  The same results, bit for bit, as qvkv_append_async at those slots followed
+ * positions 0..=pos[t]" (crates/qubivex-compute/src/discrete.rs:257-307).  f16 and q8_0
+ * pools at d = 64, 128, 256 run it as one launch (the attention takes position pos[t] from
+ * the new rows, narrowed or quantised as the append would store them, and stores them);
+ * other layouts run the append and the attention in turn, on the stream.  The same results, bit for bit, as qvkv_append_async at those slots followed
  * by qvkv_attention_async. */
 int qvkv_append_attention_async(qvkv_dev *dev, const qvkv_layout *layout, void *pool,
                                 uint64_t pool_blocks, const float *q, const float *k_new,

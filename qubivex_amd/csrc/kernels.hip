@@ -282,6 +282,91 @@ __device__ __forceinline__ void q8_scale(float amax, float &d, float &inv) {
     inv = d > 0.0f ? 1.0f / d : 0.0f;
 }
 
+// Fused append + attention, q8_0 pools: the tile that holds the appended position (rel =
+// its index in the tile) takes that position's key and value rows quantised from the new
+// rows kn / vn (this KV head's d values, f32, here staged in LDS) exactly as k_append_q8
+// stores them (group maxima, q8_scale, quant_q8), instead of what the pool held there; with
+// krow set (the first head chunk), the lanes also store the row's bytes and scales (krow/ks:
+// K bytes and scales, vrow/vs: V bytes and scales), which is the append itself.  Lane
+// (c, qg) holds the K bytes of position c for logical d = 32 i + 8 qg + e (its stored run:
+// byte 8 i + e), the V bytes of positions 4 qg .. 4 qg + 3 for d = 32 g + 2 c + u (byte
+// 2 g + u), and the scales of positions 4 qg .. 4 qg + 3.  Every lane quantises the slices
+// it would hold (the groups' maxima over the lanes sharing a group: 4 for K, 16 for V); the
+// lanes holding position rel take them.  Runs once per unit, on its last tile.  The lane
+// swaps are DPP and permlane moves: with __shfl_xor (ds_bpermute) here, inside the tile
+// loop, the 4-waves-per-SIMD build returned wrong outputs (its 3-wave build did not).
+template <int D>
+__device__ __forceinline__ void q8_patch_new_row(Tile<D, true> &t, uint32_t rel,
+                                                 const float *kn, const float *vn,
+                                                 uint8_t *krow, uint8_t *ks, uint8_t *vrow,
+                                                 uint8_t *vs, uint32_t c, uint32_t qg) {
+    constexpr int NG = D / 32;
+    constexpr int VW = Tile<D, true>::VW;
+    const uint32_t ri = rel - 4 * qg;  // the tile row of this lane's V rows and scales
+    // K, group by group; every lane knows each group's scale after the lane swaps
+#pragma unroll
+    for (int i = 0; i < NG; i++) {
+        const float4 a = *(const float4 *)(kn + 32 * i + 8 * qg);
+        const float4 b = *(const float4 *)(kn + 32 * i + 8 * qg + 4);
+        const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        float amax = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(x[e]));
+        amax = max_xor16_32(amax);  // the 4 lane groups
+        float d, inv;
+        q8_scale(amax, d, inv);
+        const uint32_t w0 = pack_q4(quant_q8(x[0], inv), quant_q8(x[1], inv),
+                                    quant_q8(x[2], inv), quant_q8(x[3], inv));
+        const uint32_t w1 = pack_q4(quant_q8(x[4], inv), quant_q8(x[5], inv),
+                                    quant_q8(x[6], inv), quant_q8(x[7], inv));
+        if (c == rel) {
+            t.k[2 * i] = w0;
+            t.k[2 * i + 1] = w1;
+            if (krow) *(u2v *)(krow + qg * (D / 4) + 8 * i) = u2v{w0, w1};
+        }
+        const uint32_t sb = __builtin_bit_cast(uint16_t, (_Float16)d);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {  // selects: a register array indexed by ri would be
+            const int h = r * NG + i, wd = h >> 1, sh = 16 * (h & 1);  // moved to scratch
+            t.ks[wd] = (uint32_t)r == ri ? (t.ks[wd] & ~(0xffffu << sh)) | (sb << sh) : t.ks[wd];
+        }
+        if (krow && c == 0 && qg == 0) *(_Float16 *)(ks + 2 * i) = (_Float16)d;
+    }
+    // V: this lane's two values of each group
+    uint32_t vw[VW];
+#pragma unroll
+    for (int i = 0; i < VW; i++) vw[i] = 0u;
+#pragma unroll
+    for (int g = 0; g < NG; g++) {
+        const float x0 = vn[32 * g + 2 * c], x1 = vn[32 * g + 2 * c + 1];
+        float amax = fmaxf(fabsf(x0), fabsf(x1));
+        amax = fmaxf(amax, dpp_f<DPP_XOR1>(amax));  // the 16 lanes of the row
+        amax = fmaxf(amax, dpp_f<DPP_XOR2>(amax));
+        amax = fmaxf(amax, dpp_f<DPP_ROR4>(amax));
+        amax = fmaxf(amax, dpp_f<DPP_ROR8>(amax));
+        float d, inv;
+        q8_scale(amax, d, inv);
+        const uint32_t pair = ((uint32_t)quant_q8(x0, inv) & 0xffu) |
+                              (((uint32_t)quant_q8(x1, inv) & 0xffu) << 8);
+        vw[g >> 1] |= pair << (16 * (g & 1));  // stored bytes 2 g, 2 g + 1
+        const uint32_t sb = __builtin_bit_cast(uint16_t, (_Float16)d);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int h = r * NG + g, wd = h >> 1, sh = 16 * (h & 1);
+            t.vs[wd] = (uint32_t)r == ri ? (t.vs[wd] & ~(0xffffu << sh)) | (sb << sh) : t.vs[wd];
+        }
+        if (vrow && c == 0 && qg == 0) *(_Float16 *)(vs + 2 * g) = (_Float16)d;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int i = 0; i < VW; i++) t.v[r][i] = (uint32_t)r == ri ? vw[i] : t.v[r][i];
+    if (vrow && qg == 0) {
+#pragma unroll
+        for (int i = 0; i < VW; i++) *(uint32_t *)(vrow + c * (D / 16) + 4 * i) = vw[i];
+    }
+}
+
 template <int U, int MODE, int D>
 __global__ __launch_bounds__(256) void k_append_q8(uint8_t *__restrict__ pool,
                                                    uint64_t pool_blocks,
@@ -817,6 +902,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
 void k_attn_mfma_nr(QV_ATTN_PARAMS) {
     attn_body<D, false, true, false, true>(QV_ATTN_ARGS);
 }
+// q8_0: held to the plain q8_0 kernel's occupancy (4 waves/SIMD at d = 128)
+template <int D, bool PK>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 4 : 1)))
+void k_attn_mfma_q8nr(QV_ATTN_PARAMS) {
+    attn_body<D, true, true, PK, true>(QV_ATTN_ARGS);
+}
 
 // The same kernel held to the registers of W waves per SIMD (512 / W per lane).
 template <int D, bool Q8, bool NT, bool PK, int W>
@@ -904,6 +995,23 @@ __device__ __forceinline__ void attn_unit(const uint8_t *__restrict__ pool, uint
     const bool hvalid = hidx < GS;
     const uint32_t sigma = (c >> 2) & 1u;  // PK: which group of a pair this lane scales for
 
+    // q8_0 NR: the wave that will take the unit's last tile copies the new K and V rows
+    // (2 d floats) into LDS first, so they are there when it reaches that tile
+    __shared__ __attribute__((aligned(16))) float nrow[Q8 && NR ? 2 * D : 4];
+    if constexpr (Q8 && NR) {
+        const uint32_t t_last = (n - 1) / 16;
+        if (t_last >= t_begin && t_last < t_end && w == (t_last - t_begin) % 4u) {
+            const uint64_t at = (uint64_t)item * geo.kv_out + (uint64_t)g * D;
+#pragma unroll
+            for (int i = 0; i < (2 * D + 255) / 256; i++) {  // 64 lanes x 4 floats a load
+                const uint32_t e = 4u * (lane + 64u * i);
+                if (e < 2u * D)
+                    *(float4 *)(nrow + e) = *(const float4 *)(e < D ? nr.k + at + e
+                                                                    : nr.v + at + (e - D));
+            }
+        }
+    }
+
     // Query fragments (B operand of QK^T): column c, k-step j holds d = dset(qg, j).
     h4 qf[NJ];
     {
@@ -927,6 +1035,8 @@ __device__ __forceinline__ void attn_unit(const uint8_t *__restrict__ pool, uint
     if constexpr (Q8) {
         // The table entries of the wave's next 64 tiles are fetched one per lane ahead of
         // the tiles; a tile's block id is then a lane read into a scalar register.
+        // NR: the unit's last tile holds the appended position, patched from nrow
+        const uint32_t t_last = NR ? (n - 1) / 16 : t_end;
         uint32_t ids = 0;
         for (uint32_t tt = t_begin + w, k = 0; tt < t_end; tt += 4, k = (k + 1) & 63u) {
             if (k == 0) {
@@ -936,6 +1046,18 @@ __device__ __forceinline__ void attn_unit(const uint8_t *__restrict__ pool, uint
             Tile<D, Q8> cur;
             load_tile_of<D, Q8, NT>(cur, tt, __builtin_amdgcn_readlane(ids, k), pool, pool_blocks,
                                     g, c, qg, geo, err);
+            if (NR && tt == t_last && cur.ok) {  // (the block is valid)
+                // the first head chunk also stores the rows
+                uint8_t *base = hc == 0 ? (uint8_t *)pool + (uint64_t)blocks[tab + (n - 1) / B] * geo.bb
+                                        : nullptr;
+                const uint64_t rowidx = (uint64_t)g * B + (n - 1) % B;
+                q8_patch_new_row<D>(cur, (n - 1) & 15u, nrow, nrow + D,
+                                    base ? base + geo.k_off + rowidx * D : nullptr,
+                                    base ? base + geo.ks_off + rowidx * (D / 32) * 2u : nullptr,
+                                    base ? base + geo.v_off + rowidx * D : nullptr,
+                                    base ? base + geo.vs_off + rowidx * (D / 32) * 2u : nullptr,
+                                    c, qg);
+            }
             compute_tile<D, Q8, PK>(cur, st, qf, n, n, qg, hi_col, sigma);
         }
     } else {
@@ -1193,6 +1315,14 @@ void k_attn_stream_nr(QV_STREAM_PARAMS) {
     attn_stream_body<D, false, true, false, true>(pool, pool_blocks, q, blocks, n_table,
                                                   table_at, pos, n_items, H, max_pos, out, ws,
                                                   hc_n, geo, err, nr);
+}
+// (3 waves/SIMD at d = 128: at the plain stream kernel's 4 its registers spill)
+template <int D, bool PK>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 3 : 1)))
+void k_attn_stream_q8nr(QV_STREAM_PARAMS) {
+    attn_stream_body<D, true, true, PK, true>(pool, pool_blocks, q, blocks, n_table, table_at,
+                                              pos, n_items, H, max_pos, out, ws, hc_n, geo, err,
+                                              nr);
 }
 
 // Merge for k_attn_stream: block = one (item, query head), D threads.  The unit's
@@ -1572,7 +1702,8 @@ int plan_attention(const Geometry &g, uint32_t n_items, uint32_t heads, uint32_t
 }
 
 bool fused_append_attention(const Geometry &g) {
-    return g.dtype == QVKV_F16 && (g.D == 64 || g.D == 128 || g.D == 256);
+    return (g.dtype == QVKV_F16 || tune("QVKV_FUSED_Q8", 1) != 0) &&
+           (g.D == 64 || g.D == 128 || g.D == 256);
 }
 
 __global__ __launch_bounds__(256) void k_slots_at(const uint32_t *__restrict__ blocks,
@@ -1638,7 +1769,15 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
     hipLaunchKernelGGL((k_attn_stream_w<DD, QQ, true, PK, 4>), dim3(P), dim3(256), 0, s, pp,     \
                        pool_blocks, q, blocks, n_table, table_at, pos, n_items, heads, max_pos,  \
                        out, wsf, p.hc, geo, err, nr)
-        if (g.D == 64) {
+#define QV_AS_Q8NR(DD, PK)                                                                      \
+    hipLaunchKernelGGL((k_attn_stream_q8nr<DD, PK>), dim3(P), dim3(256), 0, s, pp, pool_blocks,  \
+                       q, blocks, n_table, table_at, pos, n_items, heads, max_pos, out, wsf,    \
+                       p.hc, geo, err, nr)
+        if (q8 && nr.k) {
+            if (g.D == 64) { if (pk) QV_AS_Q8NR(64, true); else QV_AS_Q8NR(64, false); }
+            else if (g.D == 128) { if (pk) QV_AS_Q8NR(128, true); else QV_AS_Q8NR(128, false); }
+            else { if (pk) QV_AS_Q8NR(256, true); else QV_AS_Q8NR(256, false); }
+        } else if (g.D == 64) {
             if (!q8) { if (nr.k) QV_AS_NR(64); else QV_AS(64, false, false); }
             else if (pk) QV_AS(64, true, true);
             else QV_AS(64, true, false);
@@ -1655,6 +1794,7 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
             else if (pk) QV_AS(256, true, true);
             else QV_AS(256, true, false);
         }
+#undef QV_AS_Q8NR
 #undef QV_AS_NR
 #undef QV_AS_W4
 #undef QV_AS
@@ -1685,7 +1825,15 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
     hipLaunchKernelGGL((k_attn_mfma_nr<DD>), dim3((unsigned)grid),                              \
                        dim3(256), 0, s, pp, pool_blocks, q, blocks, n_table, table_at, pos,     \
                        n_items, heads, max_pos, out, wsf, p.hc, p.n_chunks, p.tpc, geo, err, nr)
-    if (g.D == 64) {
+#define QV_ATTN_Q8NR(DD, PK)                                                                    \
+    hipLaunchKernelGGL((k_attn_mfma_q8nr<DD, PK>), dim3((unsigned)grid), dim3(256), 0, s, pp,    \
+                       pool_blocks, q, blocks, n_table, table_at, pos, n_items, heads, max_pos,  \
+                       out, wsf, p.hc, p.n_chunks, p.tpc, geo, err, nr)
+    if (q8 && nr.k) {
+        if (g.D == 64) { if (pk) QV_ATTN_Q8NR(64, true); else QV_ATTN_Q8NR(64, false); }
+        else if (g.D == 128) { if (pk) QV_ATTN_Q8NR(128, true); else QV_ATTN_Q8NR(128, false); }
+        else { if (pk) QV_ATTN_Q8NR(256, true); else QV_ATTN_Q8NR(256, false); }
+    } else if (g.D == 64) {
         if (!q8) { if (nr.k) QV_ATTN_NR(64); else QV_ATTN(64, false, false); }
         else if (pk) QV_ATTN(64, true, true);
         else QV_ATTN(64, true, false);
@@ -1702,6 +1850,7 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
         else if (pk) QV_ATTN(256, true, true);
         else QV_ATTN(256, true, false);
     }
+#undef QV_ATTN_Q8NR
 #undef QV_ATTN_NR
 #undef QV_ATTN_W4
 #undef QV_ATTN

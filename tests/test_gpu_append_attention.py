@@ -3,8 +3,9 @@ position, then attention over 0..pos -- the reference's DeviceMoeAttention submi
 its sync rows (crates/qubivex-compute/src/discrete.rs:257-307).  It must give, bit for bit,
 the outputs and the pool bytes of qvkv_append_async at the same slots followed by
 qvkv_attention_async (whose parity with the oracle the attention tests pin), on every
-launch form: one workgroup per unit, the split by work, the context-chunk split, and the
-unfused layouts (q8_0, head dims without an MFMA kernel)."""
+launch form (one workgroup per unit, the split by work, the context-chunk split), for f16
+and q8_0 pools (q8_0: the new rows quantised as the append stores them), and on the unfused
+paths (head dims without an MFMA kernel, or QVKV_FUSED_Q8=0)."""
 import numpy as np
 import pytest
 
@@ -19,7 +20,14 @@ CASES = [
     ("f16", 2, 32, 128, 32, [95, 96, 97, 500], {}),                        # 2 head chunks
     ("f16", 8, 16, 64, 16, [200, 47, 1], {}),
     ("f16", 4, 8, 256, 256, [600, 255, 256], {}),
-    ("q8_0", 8, 32, 128, 16, [300, 1000, 31], {}),                         # unfused
+    ("q8_0", 8, 32, 128, 16, [300, 1000, 31], {}),                         # split by work
+    ("q8_0", 4, 32, 128, 16, [2049, 15, 16, 31, 33] * 26, {}),             # one per unit
+    ("q8_0", 8, 32, 128, 16, [1000, 17, 64, 4095] * 32, {}),               # one per unit, packed
+    ("q8_0", 8, 32, 128, 16, [3000, 700, 129], {"QVKV_ATTN_STREAM": "0"}),  # context chunks
+    ("q8_0", 2, 32, 128, 32, [95, 96, 97, 500], {}),                       # 2 head chunks
+    ("q8_0", 8, 16, 64, 16, [200, 47, 1], {}),
+    ("q8_0", 4, 8, 256, 256, [600, 255, 256], {}),
+    ("q8_0", 8, 32, 128, 16, [300, 31], {"QVKV_FUSED_Q8": "0"}),           # unfused
     ("f16", 4, 8, 96, 16, [100, 33], {}),                                  # unfused (generic)
 ]
 
