@@ -35,10 +35,25 @@ CASES = [
 @pytest.mark.parametrize("dtype,G,H,D,B,lens,env", CASES)
 def test_append_attention_equals_append_then_attention(hip, dtype, G, H, D, B, lens, env,
                                                        monkeypatch):
+    run_case(hip, dtype, G, H, D, B, lens, env, monkeypatch)
+
+
+@pytest.mark.parametrize("dtype,lens,env", [
+    ("f16", [300, 17, 64], {}), ("f16", [2049, 15] * 130, {}),
+    ("q8_0", [300, 17, 64], {}), ("q8_0", [2049, 15] * 130, {}),
+])
+def test_append_attention_with_special_values_in_the_new_rows(hip, dtype, lens, env, monkeypatch):
+    """NaN, infinities, values past the f16 range, f32 subnormals and an all-zero q8_0 group
+    in the step's new rows: the fused launch narrows or quantises them exactly as the append
+    (compared bit for bit, NaN outputs included)."""
+    run_case(hip, dtype, 8, 32, 128, 16, lens, env, monkeypatch, special=True)
+
+
+def run_case(hip, dtype, G, H, D, B, lens, env, monkeypatch, special=False):
     from qubivex_amd import KvLayout, KvPool
 
-    print(f"append+attention {dtype} G={G} H={H} D={D} B={B} items={len(lens)} env={env}",
-          flush=True)
+    print(f"append+attention {dtype} G={G} H={H} D={D} B={B} items={len(lens)} env={env} "
+          f"special={special}", flush=True)
     for k, v in env.items():
         monkeypatch.setenv(k, v)
     L = KvLayout(dtype, G, D, B)
@@ -60,6 +75,14 @@ def test_append_attention_equals_append_then_attention(hip, dtype, G, H, D, B, l
     assert (pos == np.array(lens)).all()
     kn = torch.randn((S, G * D), generator=gen, device="cuda")
     vn = torch.randn_like(kn)
+    if special:
+        odd = torch.tensor([float("nan"), float("inf"), -float("inf"), 1e30, -1e30, 1e-40,
+                            65520.0, 6e-8], device="cuda")
+        kn[0, :8] = odd
+        vn[0, 8:16] = odd
+        kn[1 % S, 32:64] = 0.0  # an all-zero q8_0 group
+        vn[1 % S, 32:64] = 0.0
+        kn[2 % S, D:D + 8] = odd.flip(0)
     q = torch.randn((S, H * D), generator=gen, device="cuda")
     d_b, d_t, d_p = t32(blocks), t32(table_at), t32(pos)
     torch.cuda.synchronize()
@@ -80,8 +103,9 @@ def test_append_attention_equals_append_then_attention(hip, dtype, G, H, D, B, l
     hip.check()
     pool_b = hip.read(pool.buffer, 0, size)
 
-    assert torch.isfinite(out_a).all()
-    assert torch.equal(out_a, out_b)
+    if not special:
+        assert torch.isfinite(out_a).all()
+    assert torch.equal(out_a.view(torch.int32), out_b.view(torch.int32))
     assert pool_a == pool_b
     assert pool_a != before  # the rows were stored
     pool.close()
