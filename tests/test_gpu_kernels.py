@@ -221,6 +221,11 @@ ATTN_CASES = [
     (Q8_0, 12, 4, 128, [50, 513]),
     (Q8_0, 10, 2, 128, [300]),
     (Q8_0, 24, 2, 64, [95]),
+    # 512-767 units (one layer of a decode step): one workgroup per unit, unsplit
+    (F16, 32, 8, 128, [(37 * i) % 700 + 1 for i in range(80)]),
+    (F16, 16, 1, 128, [(53 * i) % 300 + 1 for i in range(300)]),  # two head chunks
+    (Q8_0, 32, 8, 128, [(41 * i) % 700 + 1 for i in range(80)]),
+    (Q8_0, 32, 4, 128, [(29 * i) % 500 + 1 for i in range(150)]),
 ]
 
 
