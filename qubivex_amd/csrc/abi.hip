@@ -103,8 +103,17 @@ struct qvkv_dev {
 };
 
 namespace {
+// The last reference (the caller's handle or a live buffer) also takes the device's stream
+// and events: a buffer freed while, or after, the device closes still synchronizes on a
+// valid (idle) stream.
 void release(qvkv_dev *dev) {
-    if (dev->refs.fetch_sub(1) == 1) delete dev;
+    if (dev->refs.fetch_sub(1) != 1) return;
+    (void)hipSetDevice(dev->device);
+    if (dev->order_ev) (void)hipEventDestroy(dev->order_ev);
+    if (dev->t0) (void)hipEventDestroy(dev->t0);
+    if (dev->t1) (void)hipEventDestroy(dev->t1);
+    if (dev->stream) (void)hipStreamDestroy(dev->stream);
+    delete dev;
 }
 }  // namespace
 
@@ -423,13 +432,10 @@ void qvkv_close(qvkv_dev *dev) {
     }
     dev->streams.clear();
     dev_free(dev, dev->stage, dev->stage_bytes);
-    if (dev->order_ev) (void)hipEventDestroy(dev->order_ev);
-    if (dev->t0) (void)hipEventDestroy(dev->t0);
-    if (dev->t1) (void)hipEventDestroy(dev->t1);
-    if (dev->stream) (void)hipStreamDestroy(dev->stream);
-    dev->stream = nullptr;
+    dev->stage = nullptr;
+    dev->stage_bytes = 0;
     dev->closed.store(true);
-    release(dev);
+    release(dev);  // the stream and events go with the last reference
 }
 
 int qvkv_describe(const qvkv_dev *dev, char *buf, size_t len) {
@@ -498,7 +504,7 @@ void qvkv_free(qvkv_buf *buf) {
     qvkv_dev *dev = buf->dev;
     (void)hipSetDevice(dev->device);
     // In-flight work on the device's stream may still read the buffer (a closed device
-    // was synchronized by qvkv_close).
+    // was synchronized by qvkv_close; its stream stays valid while this buffer holds it).
     if (!dev->closed.load()) (void)hipStreamSynchronize(dev->stream);
     dev_free(dev, buf->ptr, buf->len);
     delete buf;
