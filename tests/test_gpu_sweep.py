@@ -10,13 +10,17 @@ values, launch form), so that combinations no list names still meet the oracle:
   * prefill attention of a random segment per sequence within the same bounds, each token
     checked as the decode item the reference's host prefill runs
     (crates/qubivex-arch/src/lib.rs:1296-1320);
-  * the fused append + attention bit for bit against the append followed by attention.
+  * the fused append + attention bit for bit against the append followed by attention;
+  * append (f16 narrowing, q8_0 quantisation), gather and block copy bit for bit against
+    the oracle's f16 / q8_0 encoders (crates/qubivex-compute/src/math.rs:13-60,
+    formats.rs:21-99) and its simulated pool, rows scaled over 1e-6..300 with specials.
 Each case prints its parameters first, so a failure names them."""
 import numpy as np
 import pytest
 
-from helpers import F16, MAX_ABS, Q8_0, REL_L2, attn_errors, normal, rng
-from test_gpu_kernels import cf32, cu32, fill_items, layout, new_pool
+import oracle
+from helpers import F16, MAX_ABS, Q8_0, REL_L2, attn_errors, decode_pool, normal, rng
+from test_gpu_kernels import EDGE_F32, cf32, cu32, cu64, fill_items, is_nan16, layout, new_pool
 from test_gpu_prefill import expand
 
 pytestmark = pytest.mark.gpu
@@ -111,3 +115,78 @@ def test_random_shapes_fused_append_attention(hip, seed, monkeypatch):
 
     dtype, D, G, H, B, lens, form = draw(seed)
     run_case(hip, "f16" if dtype == F16 else "q8_0", G, H, D, B, lens, FORMS[form], monkeypatch)
+
+
+@pytest.mark.parametrize("seed", SEEDS[1::2])
+def test_random_shapes_store_gather_and_copy_bytes(hip, seed):
+    dtype, D, G, H, B, lens, _ = draw(seed)
+    print(f"bytes seed={seed} {dtype} D={D} G={G} B={B} items={len(lens)}", flush=True)
+    r = rng(seed + 1)
+    L = layout(dtype, G, D, B)
+
+    # append at random slots of a zeroed pool: every stored code against the oracle's encoder
+    N = int(r.integers(2, 40))
+    n = int(r.integers(1, min(N * B, 300) + 1))
+    slots = r.choice(N * B, n, replace=False).astype(np.uint32)
+    k = normal(r, (n, G * D), 0.01) * np.float32(r.choice([1e-6, 1e-3, 1.0, 300.0], (n, 1)))
+    v = normal(r, (n, G * D), 0.01)
+    m = min(EDGE_F32.size, G * D)
+    k[0, :m] = EDGE_F32[:m]
+    v[-1, :m] = -EDGE_F32[:m]
+    pool = new_pool(L, N)
+    hip.append(L, pool, N, cf32(k), cf32(v), cu32(slots))
+    hip.check()
+    dec = decode_pool(pool.cpu().numpy(), L, N)
+    b, o = slots // B, slots % B
+    for name, x in (("k", k), ("v", v)):
+        got = dec[name][b, :, o]                       # [n][G][D]
+        if dtype == F16:
+            want = oracle.f16_bits(x).reshape(n, G, D)
+            ok = (got == want) | (is_nan16(got) & is_nan16(want))
+            assert ok.all(), (name, np.argwhere(~ok)[:4])
+        else:
+            want = oracle.q8_0_quantize(x).reshape(n, G, D // 32, 34)
+            wscale = want[..., 0].astype(np.uint16) | (want[..., 1].astype(np.uint16) << 8)
+            gscale = dec[name + "s"][b, :, o]
+            assert ((gscale == wscale) | (is_nan16(gscale) & is_nan16(wscale))).all(), name + " scales"
+            assert (got == want[..., 2:].view(np.int8).reshape(n, G, D)).all(), name + " values"
+    written = np.zeros(N * B, bool)
+    written[slots] = True
+    keys = dec["k"].transpose(0, 2, 1, 3).reshape(N * B, G, D)
+    assert not keys[~written].any()
+
+    # gather of ragged items through shuffled tables, f32 (and f16 for f16 pools)
+    glens = [min(x, 700) for x in lens]
+    N = sum((x + B - 1) // B for x in glens) + 3
+    pool = new_pool(L, N, fill=seed)
+    blocks, table_at, sim = fill_items(hip, L, pool, N, glens, r)
+    out_at = np.concatenate([[0], np.cumsum(glens)[:-1]]).astype(np.uint64)
+    total = int(sum(glens))
+    for od in (["f32", "f16"] if dtype == F16 else ["f32"]):
+        tdt = torch.float32 if od == "f32" else torch.float16
+        ok_ = torch.full((total * L.kv_out,), 7, dtype=tdt, device="cuda")
+        ov_ = torch.full_like(ok_, 7)
+        hip.gather(L, pool, N, cu32(blocks), cu32(table_at), cu32(glens), cu64(out_at),
+                   max(glens), ok_, ov_, out_dtype=od)
+        hip.check()
+        gk, gv = ok_.cpu().numpy(), ov_.cpu().numpy()
+        for t, x in enumerate(glens):
+            wk, wv = sim.gather(blocks, table_at, t, x)
+            a, e = int(out_at[t]) * L.kv_out, (int(out_at[t]) + x) * L.kv_out
+            if od == "f32":
+                assert np.array_equal(gk[a:e].view(np.uint32), wk.reshape(-1).view(np.uint32)), t
+                assert np.array_equal(gv[a:e].view(np.uint32), wv.reshape(-1).view(np.uint32)), t
+            else:
+                assert np.array_equal(gk[a:e].view(np.uint16), oracle.f16_bits(wk)), t
+                assert np.array_equal(gv[a:e].view(np.uint16), oracle.f16_bits(wv)), t
+
+    # block copy between disjoint random block sets
+    before = pool.cpu().numpy().reshape(N, -1).copy()
+    ids = r.permutation(N)
+    c = int(r.integers(1, N // 2 + 1))
+    src, dst = ids[:c].astype(np.uint32), ids[c:2 * c].astype(np.uint32)
+    hip.block_copy(L, pool, N, cu32(src), cu32(dst))
+    hip.check()
+    want = before.copy()
+    want[dst] = before[src]
+    assert np.array_equal(pool.cpu().numpy().reshape(N, -1), want)
