@@ -68,6 +68,7 @@ struct AttnPlan {
     uint32_t n_chunks;  // context chunks per (item, kv head, head chunk); kind 2: workgroups
     uint32_t tpc;       // 16-position tiles per chunk
     uint64_t ws_bytes;  // workspace for partial results (0 when n_chunks == 1)
+    uint32_t ucost;     // kind 2: a unit's set-up cost in tiles (its share of the split)
 };
 int plan_attention(const Geometry &g, uint32_t n_items, uint32_t heads, uint32_t max_pos,
                    AttnPlan *p, const char **why);

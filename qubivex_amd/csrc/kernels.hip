@@ -1147,8 +1147,10 @@ __device__ __forceinline__ void attn_unit(const uint8_t *__restrict__ pool, uint
 
 // ---------------------------------------------------------------------------------
 // Decode attention split by work, for launches with few units (one layer of a decode step
-// in model order): the (unit, tile) pairs of every item, unit-major, are shared out evenly
-// to the P workgroups, so ragged contexts leave no partial rounds of workgroups.  Each
+// in model order): the slots of every item, unit-major, are shared out evenly to the P
+// workgroups, so ragged contexts leave no partial rounds of workgroups.  A unit holds
+// `ucost` set-up slots (no tiles: its fixed cost in tile-equivalents) and then one slot
+// per 16-position tile; a workgroup whose range holds only set-up slots of a unit skips it.  Each
 // workgroup works through its range unit by unit: a unit wholly inside the range is
 // written out directly; a unit cut by a range boundary leaves a partial in the
 // workgroup's slot 0 (its first unit) or 1 (its last), merged by k_attn_stream_merge.
@@ -1175,7 +1177,7 @@ __device__ __forceinline__ void stream_prefix(uint64_t *cum, const uint32_t *__r
                                               const uint32_t *__restrict__ table_at,
                                               uint64_t n_table, uint32_t n_items,
                                               uint32_t max_pos, uint32_t per_unit_heads,
-                                              uint32_t B, int *err) {
+                                              uint32_t B, uint32_t ucost, int *err) {
     __shared__ uint64_t part[256];
     const uint32_t tid = threadIdx.x;
     const uint32_t per = (n_items + 255) / 256;  // <= 8
@@ -1191,7 +1193,7 @@ __device__ __forceinline__ void stream_prefix(uint64_t *cum, const uint32_t *__r
             } else if ((uint64_t)table_at[i] + (pl + B) / B > n_table) {
                 if (blockIdx.x == 0) flag(err, ERR_TABLE);
             } else {
-                v = (uint64_t)((pl + 16) / 16) * per_unit_heads;
+                v = (uint64_t)((pl + 16) / 16 + ucost) * per_unit_heads;
             }
         }
         loc[k] = v;
@@ -1231,7 +1233,7 @@ __device__ __forceinline__ uint32_t stream_item(const uint64_t *cum, uint32_t n_
         const uint32_t *__restrict__ blocks, uint64_t n_table,                                  \
         const uint32_t *__restrict__ table_at, const uint32_t *__restrict__ pos,                \
         uint32_t n_items, uint32_t H, uint32_t max_pos, float *__restrict__ out,                \
-        float *__restrict__ ws, uint32_t hc_n, Geo geo, int *err, NewRows nr
+        float *__restrict__ ws, uint32_t hc_n, uint32_t ucost, Geo geo, int *err, NewRows nr
 
 // A value every lane holds alike, moved to scalar registers.
 __device__ __forceinline__ uint32_t uni(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
@@ -1246,7 +1248,7 @@ __device__ __forceinline__ void attn_stream_body(QV_STREAM_PARAMS) {
     const uint32_t G = (uint32_t)geo.G, B = (uint32_t)geo.B;
     const uint32_t GS = H / G;
     const uint32_t upi = G * hc_n;  // units per item
-    stream_prefix(cum, pos, table_at, n_table, n_items, max_pos, upi, B, err);
+    stream_prefix(cum, pos, table_at, n_table, n_items, max_pos, upi, B, ucost, err);
     const uint64_t T = uni(cum[n_items]);
     const uint32_t P = gridDim.x, w = blockIdx.x;
     const uint64_t s0 = (uint64_t)w * T / P, s1 = (uint64_t)(w + 1) * T / P;
@@ -1260,12 +1262,16 @@ __device__ __forceinline__ void attn_stream_body(QV_STREAM_PARAMS) {
             const uint64_t per_unit = (cum[item + 1] - cum[item]) / upi;
             StreamRec r{0u, 0u, 0u, 0u};
             if (per_unit != 0) {
-                const uint64_t a = cum[item] + (uint64_t)ul * per_unit, b = a + per_unit;
+                // the unit's slots [a0, b): ucost set-up slots, then its tiles [a, b)
+                const uint64_t a0 = cum[item] + (uint64_t)ul * per_unit, a = a0 + ucost;
+                const uint64_t b = a0 + per_unit;
                 // workgroup holding position x: the largest v with floor(v T / P) <= x
                 auto owner = [&](uint64_t x) { return (uint32_t)(((x + 1) * P + T - 1) / T - 1); };
                 r.w0 = owner(a);
                 r.w1 = owner(b - 1);
-                r.s0 = a != (uint64_t)r.w0 * T / P ? 1u : 0u;
+                // slot 1 when w0 took tiles of an earlier unit: its range starts before a0
+                // (the slot before a0 is the previous unit's last tile)
+                r.s0 = (uint64_t)r.w0 * T / P < a0 ? 1u : 0u;
             }
             rec[u] = r;
         }
@@ -1274,14 +1280,19 @@ __device__ __forceinline__ void attn_stream_body(QV_STREAM_PARAMS) {
     for (uint64_t x = s0; x < s1;) {
         const uint32_t item = uni(stream_item(cum, n_items, x));
         const uint64_t c0 = uni(cum[item]);
-        const uint64_t per_unit = (uni(cum[item + 1]) - c0) / upi;  // tiles of the item
+        const uint64_t per_unit = (uni(cum[item + 1]) - c0) / upi;  // slots of a unit
         const uint64_t rel = x - c0;
         const uint32_t ul = (uint32_t)(rel / per_unit);  // unit within the item
         const uint32_t g = ul / hc_n, hc = ul % hc_n;
-        const uint32_t t0 = (uint32_t)(rel - (uint64_t)ul * per_unit);
+        const uint64_t tiles_at = c0 + (uint64_t)ul * per_unit + ucost;  // its first tile
         const uint64_t unit_end = c0 + (uint64_t)(ul + 1) * per_unit;
         const uint64_t seg_end = unit_end < s1 ? unit_end : s1;
-        const uint32_t t1 = t0 + (uint32_t)(seg_end - x);
+        if (seg_end <= tiles_at) {  // only set-up slots of this unit: nothing to do
+            x = seg_end;
+            continue;
+        }
+        const uint32_t t0 = x > tiles_at ? (uint32_t)(x - tiles_at) : 0u;
+        const uint32_t t1 = (uint32_t)(seg_end - tiles_at);
         const uint32_t n = uni(pos[item]) + 1, tab = uni(table_at[item]);
         const uint64_t oh0 = (uint64_t)item * H + (uint64_t)g * GS + hc * 8;
         if (t0 == 0 && seg_end == unit_end) {
@@ -1301,28 +1312,28 @@ __device__ __forceinline__ void attn_stream_body(QV_STREAM_PARAMS) {
 template <int D, bool Q8, bool NT, bool PK>
 __global__ __launch_bounds__(256) void k_attn_stream(QV_STREAM_PARAMS) {
     attn_stream_body<D, Q8, NT, PK, false>(pool, pool_blocks, q, blocks, n_table, table_at, pos, n_items,
-                                    H, max_pos, out, ws, hc_n, geo, err, nr);
+                                    H, max_pos, out, ws, hc_n, ucost, geo, err, nr);
 }
 template <int D, bool Q8, bool NT, bool PK, int W>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W)))
 void k_attn_stream_w(QV_STREAM_PARAMS) {
     attn_stream_body<D, Q8, NT, PK, false>(pool, pool_blocks, q, blocks, n_table, table_at, pos, n_items,
-                                    H, max_pos, out, ws, hc_n, geo, err, nr);
+                                    H, max_pos, out, ws, hc_n, ucost, geo, err, nr);
 }
 template <int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 3)))
 void k_attn_stream_nr(QV_STREAM_PARAMS) {
     attn_stream_body<D, false, true, false, true>(pool, pool_blocks, q, blocks, n_table,
                                                   table_at, pos, n_items, H, max_pos, out, ws,
-                                                  hc_n, geo, err, nr);
+                                                  hc_n, ucost, geo, err, nr);
 }
 // (3 waves/SIMD at d = 128: at the plain stream kernel's 4 its registers spill)
 template <int D, bool PK>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 3 : 1)))
 void k_attn_stream_q8nr(QV_STREAM_PARAMS) {
     attn_stream_body<D, true, true, PK, true>(pool, pool_blocks, q, blocks, n_table, table_at,
-                                              pos, n_items, H, max_pos, out, ws, hc_n, geo, err,
-                                              nr);
+                                              pos, n_items, H, max_pos, out, ws, hc_n, ucost, geo,
+                                              err, nr);
 }
 
 // Merge for k_attn_stream: block = one (item, query head), D threads.  The unit's
@@ -1660,6 +1671,7 @@ int plan_attention(const Geometry &g, uint32_t n_items, uint32_t heads, uint32_t
     p->n_chunks = 1;
     p->tpc = 0;
     p->ws_bytes = 0;
+    p->ucost = 0;
     if (!mfma) {
         if ((uint64_t)n_items * heads > 0x7fffffffull) { *why = "batch too large"; return QVKV_E_SHAPE; }
         return QVKV_OK;
@@ -1682,6 +1694,11 @@ int plan_attention(const Geometry &g, uint32_t n_items, uint32_t heads, uint32_t
         if (wgs < 1) wgs = 1;
         p->kind = 2;
         p->n_chunks = (uint32_t)wgs;
+        // Each unit also costs set-up work (its query rows, table start, the workgroup's
+        // LDS merge and output) worth about 8 tiles: counting it in the shares evens out
+        // workgroups that start several short units (cfg2-like layer of 32 ragged items:
+        // 64.2 -> 60.1 us; contexts / 8: 31.7 -> 22.0 us; 4-24 within 2 % of 8).
+        p->ucost = (uint32_t)tune("QVKV_STREAM_UNIT_COST", 8);
         p->ws_bytes = stream_rec_at(wgs, g.D, n_items) +
                       (uint64_t)n_items * g.G * p->hc * sizeof(StreamRec);
         return QVKV_OK;
@@ -1760,19 +1777,19 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
 #define QV_AS(DD, QQ, PK)                                                                       \
     hipLaunchKernelGGL((k_attn_stream<DD, QQ, true, PK>), dim3(P), dim3(256), 0, s, pp,          \
                        pool_blocks, q, blocks, n_table, table_at, pos, n_items, heads, max_pos,  \
-                       out, wsf, p.hc, geo, err, nr)
+                       out, wsf, p.hc, p.ucost, geo, err, nr)
 #define QV_AS_NR(DD)                                                                            \
     hipLaunchKernelGGL((k_attn_stream_nr<DD>), dim3(P), dim3(256), 0, s,                        \
                        pp, pool_blocks, q, blocks, n_table, table_at, pos, n_items, heads,      \
-                       max_pos, out, wsf, p.hc, geo, err, nr)
+                       max_pos, out, wsf, p.hc, p.ucost, geo, err, nr)
 #define QV_AS_W4(DD, QQ, PK)                                                                    \
     hipLaunchKernelGGL((k_attn_stream_w<DD, QQ, true, PK, 4>), dim3(P), dim3(256), 0, s, pp,     \
                        pool_blocks, q, blocks, n_table, table_at, pos, n_items, heads, max_pos,  \
-                       out, wsf, p.hc, geo, err, nr)
+                       out, wsf, p.hc, p.ucost, geo, err, nr)
 #define QV_AS_Q8NR(DD, PK)                                                                      \
     hipLaunchKernelGGL((k_attn_stream_q8nr<DD, PK>), dim3(P), dim3(256), 0, s, pp, pool_blocks,  \
                        q, blocks, n_table, table_at, pos, n_items, heads, max_pos, out, wsf,    \
-                       p.hc, geo, err, nr)
+                       p.hc, p.ucost, geo, err, nr)
         if (q8 && nr.k) {
             if (g.D == 64) { if (pk) QV_AS_Q8NR(64, true); else QV_AS_Q8NR(64, false); }
             else if (g.D == 128) { if (pk) QV_AS_Q8NR(128, true); else QV_AS_Q8NR(128, false); }
