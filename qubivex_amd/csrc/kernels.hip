@@ -1356,30 +1356,51 @@ __global__ __launch_bounds__(256) void k_attn_stream_merge(const float *__restri
     const uint32_t GS = H / G;
     const uint32_t g = h / GS, hin = h % GS, hc = hin / 8, hh = hin % 8;
     const StreamRec r = recs[(uint64_t)item * G * hc_n + g * hc_n + hc];
+    const uint64_t T = cum[n_items];  // (loaded beside the record, not after it)
     const uint32_t w0 = r.w0, w1 = r.w1;
     if (w0 == w1) return;
     // Workgroups with an empty range (only when there are fewer tiles than workgroups)
     // hold no partial.
-    const uint64_t T = cum[n_items];
     auto empty = [&](uint32_t w) {
         return T < P && (uint64_t)w * T / P == (uint64_t)(w + 1) * T / P;
     };
+    // The unit's partials are read 4 workgroups at a time, every load of a group issued
+    // before any is used (one memory round trip per group instead of one per partial);
+    // they are combined in workgroup order.
+    auto slot_of = [&](uint32_t w) { return 2ull * w + (w == w0 ? r.s0 : 0u); };
     float M = -INFINITY;
-    for (uint32_t w = w0; w <= w1; w++) {
-        if (empty(w)) continue;
-        const uint64_t slot = 2ull * w + (w == w0 ? r.s0 : 0u);
-        M = fmaxf(M, ml[(slot * 8 + hh) * 2]);
+    for (uint32_t wb = w0; wb <= w1; wb += 4) {
+        float mc[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t w = wb + k;
+            mc[k] = w <= w1 && !empty(w) ? ml[(slot_of(w) * 8 + hh) * 2] : -INFINITY;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) M = fmaxf(M, mc[k]);
     }
     const float Ms = M == -INFINITY ? 0.0f : M;
     for (uint32_t d = threadIdx.x; d < D; d += blockDim.x) {
         float L = 0.0f, O = 0.0f;
-        for (uint32_t w = w0; w <= w1; w++) {
-            if (empty(w)) continue;
-            const uint64_t slot = 2ull * w + (w == w0 ? r.s0 : 0u);
-            const float mc = ml[(slot * 8 + hh) * 2];
-            const float f = mc == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mc - Ms);
-            L = fmaf(ml[(slot * 8 + hh) * 2 + 1], f, L);
-            O = fmaf(ws[(slot * 8 + hh) * D + d], f, O);
+        for (uint32_t wb = w0; wb <= w1; wb += 4) {
+            float mc[4], lc[4], oc[4];
+            bool live[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t w = wb + k;
+                live[k] = w <= w1 && !empty(w);
+                const uint64_t slot = live[k] ? slot_of(w) : 0u;
+                mc[k] = live[k] ? ml[(slot * 8 + hh) * 2] : -INFINITY;
+                lc[k] = live[k] ? ml[(slot * 8 + hh) * 2 + 1] : 0.0f;
+                oc[k] = live[k] ? ws[(slot * 8 + hh) * D + d] : 0.0f;
+            }
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                if (!live[k]) continue;
+                const float f = mc[k] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mc[k] - Ms);
+                L = fmaf(lc[k], f, L);
+                O = fmaf(oc[k], f, O);
+            }
         }
         out[(uint64_t)oh * D + d] = O / L;
     }
