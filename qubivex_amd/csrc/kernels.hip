@@ -879,9 +879,9 @@ __global__ __launch_bounds__(T) void k_block_copy(uint8_t *__restrict__ pool,
     pool, pool_blocks, q, blocks, n_table, table_at, pos, n_items, H, max_pos, out, ws, hc_n,   \
         n_chunks, tpc, geo, err, nr
 
-template <int D, bool Q8, bool NT, bool PK, bool NR>
+template <int D, bool Q8, bool NT, bool PK, bool NR, bool IDS = false>
 __device__ __forceinline__ void attn_body(QV_ATTN_PARAMS);
-template <int D, bool Q8, bool NT, bool PK, bool NR>
+template <int D, bool Q8, bool NT, bool PK, bool NR, bool IDS = false>
 __device__ __forceinline__ void attn_unit(const uint8_t *__restrict__ pool, uint64_t pool_blocks,
                                           const float *__restrict__ q,
                                           const uint32_t *__restrict__ blocks, uint32_t H,
@@ -900,7 +900,14 @@ __global__ __launch_bounds__(256) void k_attn_mfma(QV_ATTN_PARAMS) {
 template <int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 3)))
 void k_attn_mfma_nr(QV_ATTN_PARAMS) {
-    attn_body<D, false, true, false, true>(QV_ATTN_ARGS);
+    attn_body<D, false, true, false, true, true>(QV_ATTN_ARGS);
+}
+// f16 launches of one layer's items (below 2048 units): the tile loop fetches its table
+// entries ahead of the tiles (IDS; the batched launch is faster without).
+template <int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 3)))
+void k_attn_mfma_ids(QV_ATTN_PARAMS) {
+    attn_body<D, false, true, false, false, true>(QV_ATTN_ARGS);
 }
 // q8_0: held to the plain q8_0 kernel's occupancy (4 waves/SIMD at d = 128)
 template <int D, bool PK>
@@ -916,7 +923,7 @@ void k_attn_mfma_w(QV_ATTN_PARAMS) {
     attn_body<D, Q8, NT, PK, false>(QV_ATTN_ARGS);
 }
 
-template <int D, bool Q8, bool NT, bool PK, bool NR>
+template <int D, bool Q8, bool NT, bool PK, bool NR, bool IDS>
 __device__ __forceinline__ void attn_body(QV_ATTN_PARAMS) {
     const uint32_t G = (uint32_t)geo.G, B = (uint32_t)geo.B;
     const uint32_t GS = H / G;
@@ -954,11 +961,11 @@ __device__ __forceinline__ void attn_body(QV_ATTN_PARAMS) {
 
     const uint64_t oh0 = (uint64_t)item * H + (uint64_t)g * GS + hc * 8;
     if (n_chunks == 1) {
-        attn_unit<D, Q8, NT, PK, NR>(pool, pool_blocks, q, blocks, H, geo, err, item, g, hc, n, tab,
+        attn_unit<D, Q8, NT, PK, NR, IDS>(pool, pool_blocks, q, blocks, H, geo, err, item, g, hc, n, tab,
                                  t_begin, t_end, out + oh0 * D, D, nullptr, 0, nr);
     } else {
         float *ml = ws + (uint64_t)n_items * H * n_chunks * D;
-        attn_unit<D, Q8, NT, PK, NR>(pool, pool_blocks, q, blocks, H, geo, err, item, g, hc, n, tab,
+        attn_unit<D, Q8, NT, PK, NR, IDS>(pool, pool_blocks, q, blocks, H, geo, err, item, g, hc, n, tab,
                                  t_begin, t_end, ws + (oh0 * n_chunks + chunk) * D,
                                  (uint64_t)n_chunks * D, ml + (oh0 * n_chunks + chunk) * 2,
                                  (uint64_t)n_chunks * 2, nr);
@@ -970,7 +977,7 @@ __device__ __forceinline__ void attn_body(QV_ATTN_PARAMS) {
 // the 4 waves.  Head hh's result goes to o_base[hh * o_stride + d]: the output (ml_base
 // null) or, for part of the context, the unnormalised partial with its max and sum at
 // ml_base[hh * ml_stride] (log2 domain).
-template <int D, bool Q8, bool NT, bool PK, bool NR>
+template <int D, bool Q8, bool NT, bool PK, bool NR, bool IDS>
 __device__ __forceinline__ void attn_unit(const uint8_t *__restrict__ pool, uint64_t pool_blocks,
                                           const float *__restrict__ q,
                                           const uint32_t *__restrict__ blocks, uint32_t H,
@@ -1063,11 +1070,20 @@ __device__ __forceinline__ void attn_unit(const uint8_t *__restrict__ pool, uint
     } else {
         // NR: the unit's last tile holds the appended position; its wave takes it after
         // the loop (the same order), so the loop body is the plain kernel's
+        // IDS: the table entries of the wave's next 64 tiles are fetched one per lane ahead
+        // of the tiles (as in the q8_0 loop), so a tile's loads wait on no table load.
         const uint32_t t_last = NR ? (n - 1) / 16 : t_end;
         uint32_t tt = t_begin + w;
-        for (; tt < t_end && tt != t_last; tt += 4) {
+        uint32_t ids = 0;
+        for (uint32_t k = 0; tt < t_end && tt != t_last; tt += 4, k = (k + 1) & 63u) {
+            if (IDS && k == 0) {
+                const uint32_t tl = tt + 4u * lane;
+                ids = tl < t_end ? blocks[tab + tl * 16u / B] : 0u;
+            }
             Tile<D, Q8> cur;
-            load_tile<D, Q8, NT>(cur, tt, pool, pool_blocks, blocks, tab, g, c, qg, geo, err);
+            load_tile_of<D, Q8, NT>(cur, tt,
+                                    IDS ? __builtin_amdgcn_readlane(ids, k) : blocks[tab + tt * 16u / B],
+                                    pool, pool_blocks, g, c, qg, geo, err);
             compute_tile<D, Q8, PK>(cur, st, qf, n, n, qg, hi_col, sigma);
         }
         if (NR && tt < t_end) {  // tt == t_last: position n - 1 comes from the new rows
@@ -1844,6 +1860,10 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
         return hipGetLastError();
     }
     const uint64_t grid = (uint64_t)n_items * g.G * p.hc * p.n_chunks;
+    // f16, d = 128, launches of one layer's items (cfg5: 512 workgroups): the table entries
+    // fetched ahead of the tiles (per layer cfg5 16.7-17.2 -> 16.2 ms per step; the batched
+    // launch of every layer lost 2-4 % with it)
+    const bool per_layer = grid < (uint64_t)tune("QVKV_ATTN_IDS_BELOW", 2048);
     // K/V tiles are streamed with non-temporal loads (read once).
     // Occupancy: `mode` 0 is the compiler's register choice (3 waves/SIMD at d=128), 4
     // holds the kernel to 4 waves per SIMD (125 VGPRs, no spill).  Measured (cfg5 f16,
@@ -1863,6 +1883,10 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
     hipLaunchKernelGGL((k_attn_mfma_nr<DD>), dim3((unsigned)grid),                              \
                        dim3(256), 0, s, pp, pool_blocks, q, blocks, n_table, table_at, pos,     \
                        n_items, heads, max_pos, out, wsf, p.hc, p.n_chunks, p.tpc, geo, err, nr)
+#define QV_ATTN_IDS(DD)                                                                         \
+    hipLaunchKernelGGL((k_attn_mfma_ids<DD>), dim3((unsigned)grid), dim3(256), 0, s, pp,        \
+                       pool_blocks, q, blocks, n_table, table_at, pos, n_items, heads, max_pos,  \
+                       out, wsf, p.hc, p.n_chunks, p.tpc, geo, err, nr)
 #define QV_ATTN_Q8NR(DD, PK)                                                                    \
     hipLaunchKernelGGL((k_attn_mfma_q8nr<DD, PK>), dim3((unsigned)grid), dim3(256), 0, s, pp,    \
                        pool_blocks, q, blocks, n_table, table_at, pos, n_items, heads, max_pos,  \
@@ -1879,6 +1903,7 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
         if (!q8) {
             if (nr.k) QV_ATTN_NR(128);
             else if (w4) QV_ATTN_W4(128, false, false);
+            else if (per_layer) QV_ATTN_IDS(128);
             else QV_ATTN(128, false, false);
         }
         else if (pk) { if (w4) QV_ATTN_W4(128, true, true); else QV_ATTN(128, true, true); }
@@ -1889,6 +1914,7 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
         else QV_ATTN(256, true, false);
     }
 #undef QV_ATTN_Q8NR
+#undef QV_ATTN_IDS
 #undef QV_ATTN_NR
 #undef QV_ATTN_W4
 #undef QV_ATTN
