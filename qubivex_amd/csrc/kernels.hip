@@ -1806,7 +1806,12 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
     }
     float *wsf = (float *)ws;
     const bool q8 = g.dtype == QVKV_Q8_0;
-    const bool w4 = tune(q8 ? "QVKV_ATTN_WAVES4_Q8" : "QVKV_ATTN_WAVES4_F16", q8 ? 1 : 0) != 0;
+    // q8_0 at d = 128 always runs its 4-wave builds (k_attn_mfma_w / k_attn_stream_w, MFMA
+    // accumulators in VGPRs): the same source built for 3 waves/SIMD (accumulators in AGPRs)
+    // returned wrong outputs in the oracle tests (both the unsplit and the split-by-work
+    // form), so those builds are not launched.  f16 selects its 4-wave build by
+    // QVKV_ATTN_WAVES4_F16 (measured slower, oracle tests green).
+    const bool w4 = q8 || tune("QVKV_ATTN_WAVES4_F16", 0) != 0;
     // q8_0 with <= 4 query heads per KV head: two groups' probabilities per A operand
     const bool pk = q8 && heads / (uint32_t)g.G <= 4 && tune("QVKV_ATTN_PACK", 1) != 0;
     if (p.kind == 2) {
@@ -1841,8 +1846,8 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
                 else if (w4) QV_AS_W4(128, false, false);
                 else QV_AS(128, false, false);
             }
-            else if (pk) { if (w4) QV_AS_W4(128, true, true); else QV_AS(128, true, true); }
-            else { if (w4) QV_AS_W4(128, true, false); else QV_AS(128, true, false); }
+            else if (pk) QV_AS_W4(128, true, true);
+            else QV_AS_W4(128, true, false);
         } else {
             if (!q8) { if (nr.k) QV_AS_NR(256); else QV_AS(256, false, false); }
             else if (pk) QV_AS(256, true, true);
@@ -1906,8 +1911,8 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
             else if (per_layer) QV_ATTN_IDS(128);
             else QV_ATTN(128, false, false);
         }
-        else if (pk) { if (w4) QV_ATTN_W4(128, true, true); else QV_ATTN(128, true, true); }
-        else { if (w4) QV_ATTN_W4(128, true, false); else QV_ATTN(128, true, false); }
+        else if (pk) QV_ATTN_W4(128, true, true);
+        else QV_ATTN_W4(128, true, false);
     } else {
         if (!q8) { if (nr.k) QV_ATTN_NR(256); else QV_ATTN(256, false, false); }
         else if (pk) QV_ATTN(256, true, true);

@@ -250,6 +250,23 @@ def test_attention_within_tolerance(hip, dtype, H, G, D, lens):
     assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)
 
 
+# Launch switches a caller may set (QVKV_* environment variables read at each launch) and
+# a few shapes each, from ATTN_CASES: every selectable build must meet the same tolerance.
+SWITCH_CASES = [ATTN_CASES[i] for i in (0, 1, 8, 9)] + ATTN_CASES[-4:]
+
+
+@pytest.mark.parametrize("env", [{"QVKV_ATTN_WAVES4_F16": "1"}, {"QVKV_ATTN_PACK": "0"},
+                                 {"QVKV_ATTN_XCD": "0"}, {"QVKV_ATTN_IDS_BELOW": "0"},
+                                 {"QVKV_STREAM_UNIT_COST": "0"}, {"QVKV_ATTN_STREAM": "0"}],
+                         ids=lambda e: ",".join(f"{k}={v}" for k, v in e.items()))
+@pytest.mark.parametrize("dtype,H,G,D,lens", SWITCH_CASES)
+def test_attention_launch_switches_stay_within_tolerance(hip, dtype, H, G, D, lens, env,
+                                                         monkeypatch):
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    test_attention_within_tolerance(hip, dtype, H, G, D, lens)
+
+
 @pytest.mark.parametrize("dtype", [F16, Q8_0])
 def test_attention_ignores_nan_in_unwritten_slots(hip, dtype):
     """Slots past each item's last position hold 0xFF bytes: NaN f16 values and NaN q8_0
