@@ -1148,8 +1148,9 @@ hipError_t launch_prefill(const Geometry &g, const void *pool, uint64_t pool_blo
     if (!q8 && (g.D == 64 || g.D == 128) && tune("QVKV_PREFILL_V2", 1)) {
         const uint32_t n_qb = (uint32_t)(((uint64_t)max_tok * GS + 63) / 64);
         const unsigned grid2 = (unsigned)((uint64_t)n_seg * g.G * n_qb);
+        const unsigned pad = (unsigned)tune("QVKV_PREFILL_LDS_PAD", 0);
 #define QV_PF2(DD, DMA, PS)                                                                    \
-    hipLaunchKernelGGL((k_prefill_f16<DD, DMA, PS>), dim3(grid2), dim3(256), 0, s, pp,           \
+    hipLaunchKernelGGL((k_prefill_f16<DD, DMA, PS>), dim3(grid2), dim3(256), pad, s, pp,         \
                        pool_blocks, q, blocks, n_table, table_at, pos0, q_at, n_tok, n_seg,     \
                        heads, max_pos, max_tok, q_rows, n_qb, out, geo, err)
         // P as one f16 (the default) or as high part + residual (QVKV_PREFILL_EXACT_P=1)
