@@ -257,7 +257,8 @@ SWITCH_CASES = [ATTN_CASES[i] for i in (0, 1, 8, 9)] + ATTN_CASES[-4:]
 
 @pytest.mark.parametrize("env", [{"QVKV_ATTN_WAVES4_F16": "1"}, {"QVKV_ATTN_PACK": "0"},
                                  {"QVKV_ATTN_XCD": "0"}, {"QVKV_ATTN_IDS_BELOW": "0"},
-                                 {"QVKV_STREAM_UNIT_COST": "0"}, {"QVKV_ATTN_STREAM": "0"}],
+                                 {"QVKV_STREAM_UNIT_COST": "0"}, {"QVKV_STREAM_UNIT_COST": "40"},
+                                 {"QVKV_ATTN_STREAM": "0"}],
                          ids=lambda e: ",".join(f"{k}={v}" for k, v in e.items()))
 @pytest.mark.parametrize("dtype,H,G,D,lens", SWITCH_CASES)
 def test_attention_launch_switches_stay_within_tolerance(hip, dtype, H, G, D, lens, env,
