@@ -29,6 +29,16 @@ def _run(cmd, verbose):
     subprocess.run(cmd, check=True)
 
 
+def hip_command(src: str, mode: list, out: str) -> list:
+    """The hipcc command for one HIP source of the library (mode: ["-c", ...] for an object,
+    ["--cuda-device-only", "-S"] for the device assembly)."""
+    return ["hipcc", f"--offload-arch={ARCH}", *mode, "-O3", "-std=c++17", "-Wall",
+            "-Wno-unused-function", "-I", os.path.join(ROOT, "include"), "-I", CSRC,
+            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+            *HIP_FLAGS.get(src, []), *os.environ.get("QVKV_EXTRA_HIPFLAGS", "").split(),
+            os.path.join(CSRC, src), "-o", out]
+
+
 def build(verbose: bool = False, jobs: int = 4) -> str:
     os.makedirs(OUT_DIR, exist_ok=True)
     obj_dir = os.path.join(OUT_DIR, "obj")
@@ -39,10 +49,7 @@ def build(verbose: bool = False, jobs: int = 4) -> str:
     for src in HIP_SOURCES:
         obj = os.path.join(obj_dir, src + ".o")
         objs.append(obj)
-        cmd = ["hipcc", f"--offload-arch={ARCH}", "-c", *common, *inc,
-               "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-               *HIP_FLAGS.get(src, []), *os.environ.get("QVKV_EXTRA_HIPFLAGS", "").split(),
-               "-fno-gpu-rdc", os.path.join(CSRC, src), "-o", obj]
+        cmd = hip_command(src, ["-c", "-fPIC", "-fno-gpu-rdc"], obj)
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append(subprocess.Popen(cmd))

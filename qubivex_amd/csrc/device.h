@@ -218,9 +218,16 @@ __device__ __forceinline__ float mul_rn(float a, float b) {
 
 // a * b rounded once, with 0 * x = 0 for every x (NaN and inf included): v_mul_legacy_f32.
 // Opaque to the compiler, so never contracted into a later operation either.
+// The s_nop 0 is required: `a` is often a v_exp_f32 result, and on gfx950 a VALU
+// instruction that reads the result of a transcendental instruction (v_exp, v_log, v_rcp,
+// ...) issued just before it needs one wait state.  The compiler inserts that wait for its
+// own instructions but not for inline asm, and without it the multiply read the register's
+// old contents -- for v_exp_f32 vN, vN that is the exponent itself, so a masked row read
+// -inf instead of 0 and -inf * scale put NaN into P.V.  The 3-wave q8_0 builds had placed
+// the multiply right after the v_exp (the 4-wave builds had not).
 __device__ __forceinline__ float mul_legacy(float a, float b) {
     float y;
-    asm("v_mul_legacy_f32 %0, %1, %2" : "=v"(y) : "v"(a), "v"(b));
+    asm("s_nop 0\n\tv_mul_legacy_f32 %0, %1, %2" : "=v"(y) : "v"(a), "v"(b));
     return y;
 }
 
@@ -487,10 +494,24 @@ __device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<
         // int8 exactly as f16.  The rows' scales of group j/2 fold into the probabilities
         // (P' = p * scale in f32, then f16 high part + residual: exact to ~2^-22), so the
         // products the MFMA forms are exact.
-        // Rows at or past n_max (a partial tile only) have p = 0 exactly (score -inf).  Their
-        // int8 values are finite whatever the slot holds, so 0 * value = 0 in the MFMA; their
-        // scales may be any f16 bits (NaN, inf) and are folded in with v_mul_legacy_f32,
-        // whose 0 * x is 0 for every x.  No row needs masking.
+        // Rows at or past n_max (a partial tile only) may never have been written: their
+        // scales may be any f16 bits (NaN, inf).  Their p is 0 exactly (score -inf), and
+        // v_mul_legacy_f32's 0 * x is 0 for every x, but the tile does not rest on that: in
+        // a partial tile (wave-uniform, at most one per unit) those rows' scales and int8
+        // values are zeroed before use, as the f16 branch zeroes its value rows.
+        uint32_t vs[Tile<D, Q8>::SW];
+#pragma unroll
+        for (int x = 0; x < Tile<D, Q8>::SW; x++) vs[x] = t.vs[x];
+        if (partial) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (p0 + 4 * qg + i >= n_max) {
+#pragma unroll
+                    for (int x = 0; x < NG / 2; x++) vs[i * (NG / 2) + x] = 0u;
+#pragma unroll
+                    for (int x = 0; x < Tile<D, Q8>::VW; x++) vw[i][x] = 0u;
+                }
+        }
         const float neg_lo = hi_col ? 0.0f : -1.0f;
         // The A operand of scaled probabilities for group g (this lane's scale pick): the f16
         // high part u of x = p * scale, or the residual x - u.
@@ -519,7 +540,7 @@ __device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<
                 float sc[4];
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const uint32_t w = t.vs[(i * NG) / 2 + m] >> (16u * sigma);
+                    const uint32_t w = vs[(i * NG) / 2 + m] >> (16u * sigma);
                     sc[i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
                 }
                 const h4 pa = scaled(sc);
@@ -531,7 +552,7 @@ __device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<
             for (int gi = 0; gi < NG; gi++) {
                 float sc[4];
 #pragma unroll
-                for (int i = 0; i < 4; i++) sc[i] = half_at(t.vs, i * NG + gi);
+                for (int i = 0; i < 4; i++) sc[i] = half_at(vs, i * NG + gi);
                 pv_group(scaled(sc), gi);
             }
         }
