@@ -116,6 +116,22 @@ int qvkv_timing(const qvkv_dev *dev, uint64_t *gpu_ns);
  * as a whole.  Kernels address pools with 64-bit offsets, so this is the device memory. */
 int qvkv_max_arena(const qvkv_dev *dev, uint64_t *out);
 
+/* Launch-shape knobs.  No counterpart in the reference (its backends have no launch
+ * shapes to choose); for callers and benchmarks that measure alternative kernel builds and
+ * splits.  Process-wide (every device), read by each launch; the library reads no
+ * environment variable.  Every knob starts at its default, the measured best, and every
+ * value a knob may take gives results within the path's tolerance (the attention
+ * parity tests run each switch).  Names: append_u, append_grid_per_cu, append_nt,
+ * append_q8_fast, append_nts, gather_split, gather_q8_fast, gather_t, gather_uf, copy_u,
+ * copy_t, attn_full, attn_stream, attn_stream_wg, stream_unit_cost, attn_target, fused_q8,
+ * attn_waves4_f16, attn_waves3_q8, attn_pack, attn_ids_below, attn_xcd, prefill_v2,
+ * prefill_lds_pad, prefill_exact_p, prefill_dma, prefill_q8_fast, prelude_fast,
+ * prelude_wide, prelude_full_wg.  An unknown name is QVKV_E_SHAPE. */
+int qvkv_tune(const char *name, int value);
+int qvkv_tune_get(const char *name, int *value);
+/* Every knob back to its default. */
+void qvkv_tune_reset(void);
+
 /* DiscreteDevice::alloc (discrete.rs:500-508): `len` bytes, contents unspecified. */
 int qvkv_alloc(qvkv_dev *dev, size_t len, qvkv_buf **out);
 /* Drop of the last DeviceBuffer clone (discrete.rs:24-95). */

@@ -80,6 +80,13 @@ class PrefixStats(ctypes.Structure):
 
 
 def _load():
+    # torch's HIP runtime first: libqvkv.so then binds the libamdhip64 already in the
+    # process.  Loaded the other way round, the process holds two HIP runtimes and the
+    # library's sees no device.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     if not os.path.exists(LIB):
         raise ImportError(
             f"libqvkv.so is not built ({LIB}); run `python qubivex_amd/build.py` (or __graft_entry__.build()) first")
@@ -105,6 +112,9 @@ SIGNATURES = {
     "qvkv_stream": (_vp, [_vp]),
     "qvkv_timing": (_i32, [_vp, _P(_u64)]),
     "qvkv_max_arena": (_i32, [_vp, _P(_u64)]),
+    "qvkv_tune": (_i32, [ctypes.c_char_p, _i32]),
+    "qvkv_tune_get": (_i32, [ctypes.c_char_p, _P(_i32)]),
+    "qvkv_tune_reset": (None, []),
     "qvkv_alloc": (_i32, [_vp, _sz, _P(_vp)]),
     "qvkv_free": (None, [_vp]),
     "qvkv_buf_ptr": (_vp, [_vp]),

@@ -74,6 +74,10 @@ struct StreamState {
     void *ws = nullptr;    // attention workspace (partials of context chunks)
     uint64_t ws_bytes = 0;
     std::mutex check_mu;   // one check at a time per stream
+    // The attention launches of this stream, one at a time: the workspace is grown (which
+    // waits for this stream to drain) and handed to the launch under it.  Other streams'
+    // calls never wait for it.
+    std::mutex ws_mu;
 };
 
 struct qvkv_dev {
@@ -86,8 +90,8 @@ struct qvkv_dev {
     hipEvent_t order_ev = nullptr;  // orders pool copies after a caller's stream
     hipEvent_t t0 = nullptr, t1 = nullptr;  // GPU time of a synchronous call
     // host_mu: the host-memory entry points, one at a time (the staging buffer and the
-    // device stream's state are theirs); mu: the stream states and workspace growth (held
-    // briefly).  Order: host_mu before mu.
+    // device stream's state are theirs); mu: the list of stream states (held briefly, never
+    // across a wait).  Order: host_mu, then mu, then a stream's ws_mu.
     std::mutex host_mu, mu;
     std::atomic<uint64_t> used{0}, peak{0}, refused{0};
     std::atomic<uint64_t> uploads{0}, upload_bytes{0}, downloads{0}, download_bytes{0};
@@ -467,6 +471,10 @@ int qvkv_max_arena(const qvkv_dev *dev, uint64_t *out) {
     return QVKV_OK;
 }
 
+int qvkv_tune(const char *name, int value) { return qvkv::set_tune(name, value); }
+int qvkv_tune_get(const char *name, int *value) { return qvkv::get_tune(name, value); }
+void qvkv_tune_reset(void) { qvkv::reset_tune(); }
+
 int qvkv_transfers(const qvkv_dev *dev, qvkv_transfers_t *out) {
     if (!dev || !out) return fail(QVKV_E_SHAPE, "null argument");
     out->uploads = dev->uploads.load();
@@ -617,14 +625,15 @@ int qvkv_attention_async(qvkv_dev *dev, const qvkv_layout *layout, const void *p
     if (!pool || !q || !blocks || !table_at || !pos || !out)
         return fail(QVKV_E_SHAPE, "shape mismatch in attention: null pointer");
     if (int rc = set_device(dev)) return rc;
-    // The stream's workspace is grown and handed to the launch under the device lock, so
-    // no other thread frees it in between; launches on one stream use it in turn.  The
-    // device's own stream is also the host-memory entry points': take their lock too.
+    // The stream's workspace is grown and handed to the launch under that stream's own
+    // lock, so no other thread frees it in between; launches on one stream use it in turn,
+    // and a growth that waits for this stream to drain holds up no other stream's calls.
+    // The device's own stream is also the host-memory entry points': take their lock too.
     std::unique_lock<std::mutex> host_lk(dev->host_mu, std::defer_lock);
     if ((hipStream_t)stream == dev->stream) host_lk.lock();
-    std::lock_guard<std::mutex> lk(dev->mu);
     StreamState *st;
-    if (int rc = state_locked(dev, (hipStream_t)stream, &st)) return rc;
+    if (int rc = state_of(dev, stream, &st)) return rc;
+    std::lock_guard<std::mutex> wl(st->ws_mu);
     if (int rc = ensure_attention(dev, st, p)) return rc;
     return launched(dev, qvkv::launch_attention(g, p, pool, pool_blocks, q, blocks, n_table,
                                                 table_at, pos, n_items, heads, max_pos, out,
@@ -650,9 +659,9 @@ int qvkv_append_attention_async(qvkv_dev *dev, const qvkv_layout *layout, void *
     if (int rc = set_device(dev)) return rc;
     std::unique_lock<std::mutex> host_lk(dev->host_mu, std::defer_lock);
     if ((hipStream_t)stream == dev->stream) host_lk.lock();
-    std::lock_guard<std::mutex> lk(dev->mu);
     StreamState *st;
-    if (int rc = state_locked(dev, (hipStream_t)stream, &st)) return rc;
+    if (int rc = state_of(dev, stream, &st)) return rc;
+    std::lock_guard<std::mutex> wl(st->ws_mu);
     const bool fused = qvkv::fused_append_attention(g);
     // unfused: the items' slots after the attention workspace, then append + attention
     const uint64_t slots_at = (p.ws_bytes + 255) / 256 * 256;

@@ -31,7 +31,7 @@ struct Geo {  // kernel-side copy of Geometry
 
 inline Geo to_geo(const Geometry &g) {
     return Geo{g.dtype, g.G, g.D, g.B, (uint32_t)g.kv_out, g.block_bytes,
-               g.k_off, g.ks_off, g.v_off, g.vs_off, (uint32_t)tune("QVKV_ATTN_XCD", 1),
+               g.k_off, g.ks_off, g.v_off, g.vs_off, (uint32_t)tune(KNOB_ATTN_XCD),
                FastDiv((uint32_t)g.B)};
 }
 

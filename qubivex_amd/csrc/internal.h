@@ -72,8 +72,50 @@ struct AttnPlan {
 };
 int plan_attention(const Geometry &g, uint32_t n_items, uint32_t heads, uint32_t max_pos,
                    AttnPlan *p, const char **why);
-// Launch-shape knob: the default, or an environment variable of the same name (kernels.hip).
-int tune(const char *name, int def);
+// Launch-shape knobs: process-wide values that pick kernel builds and launch shapes.  Each
+// starts at its default (the measured best) and changes only through qvkv_tune(); the
+// library reads no environment variable.  X(id, name, default).
+#define QVKV_KNOBS(X)                                                                           \
+    X(APPEND_U, "append_u", 2)                  /* rows per append thread group */              \
+    X(APPEND_GRID_PER_CU, "append_grid_per_cu", 1 << 20)                                        \
+    X(APPEND_NT, "append_nt", -1)               /* non-temporal loads; -1: f16 yes, q8_0 no */   \
+    X(APPEND_Q8_FAST, "append_q8_fast", 1)      /* k_append_q8 at d = 64/128/256 */             \
+    X(APPEND_NTS, "append_nts", 1)              /* non-temporal q8_0 stores */                  \
+    X(GATHER_SPLIT, "gather_split", 1)                                                          \
+    X(GATHER_Q8_FAST, "gather_q8_fast", 1)                                                      \
+    X(GATHER_T, "gather_t", 64)                                                                 \
+    X(GATHER_UF, "gather_uf", 4)                                                                \
+    X(COPY_U, "copy_u", 1)                                                                      \
+    X(COPY_T, "copy_t", 64)                                                                     \
+    X(ATTN_FULL, "attn_full", 512)              /* units from which a launch runs unsplit */    \
+    X(ATTN_STREAM, "attn_stream", 1)            /* 1: split by work, 0: context chunks */       \
+    X(ATTN_STREAM_WG, "attn_stream_wg", 768)                                                    \
+    X(STREAM_UNIT_COST, "stream_unit_cost", 8)  /* a unit's set-up cost in tiles */             \
+    X(ATTN_TARGET, "attn_target", 1536)         /* context-chunk split: workgroups aimed at */  \
+    X(FUSED_Q8, "fused_q8", 1)                  /* fused append + attention for q8_0 */         \
+    X(ATTN_WAVES4_F16, "attn_waves4_f16", 0)                                                    \
+    X(ATTN_WAVES3_Q8, "attn_waves3_q8", 0)      /* q8_0 d = 128 at 3 waves/SIMD */              \
+    X(ATTN_PACK, "attn_pack", 1)                                                                \
+    X(ATTN_IDS_BELOW, "attn_ids_below", 2048)                                                   \
+    X(ATTN_XCD, "attn_xcd", 1)                                                                  \
+    X(PREFILL_V2, "prefill_v2", 1)                                                              \
+    X(PREFILL_LDS_PAD, "prefill_lds_pad", 0)                                                    \
+    X(PREFILL_EXACT_P, "prefill_exact_p", 0)                                                    \
+    X(PREFILL_DMA, "prefill_dma", 1)                                                            \
+    X(PREFILL_Q8_FAST, "prefill_q8_fast", 1)                                                    \
+    X(PRELUDE_FAST, "prelude_fast", 1)                                                          \
+    X(PRELUDE_WIDE, "prelude_wide", 1)                                                          \
+    X(PRELUDE_FULL_WG, "prelude_full_wg", 1)
+enum Knob : int {
+#define QVKV_KNOB_ID(id, name, def) KNOB_##id,
+    QVKV_KNOBS(QVKV_KNOB_ID)
+#undef QVKV_KNOB_ID
+    KNOB_COUNT
+};
+int tune(Knob k);                       // the knob's current value (kernels.hip)
+int set_tune(const char *name, int v);  // QVKV_OK, or QVKV_E_SHAPE for an unknown name
+int get_tune(const char *name, int *v);
+void reset_tune();
 
 // Paged prefill attention over segments of consecutive tokens (kernels.hip).
 int check_prefill(const Geometry &g, uint32_t n_seg, uint32_t heads, uint32_t max_tok,
@@ -86,7 +128,8 @@ hipError_t launch_prefill(const Geometry &g, const void *pool, uint64_t pool_blo
                           int *err, hipStream_t s, bool f16_values = true);
 // New key and value rows of a fused append + attention (n_items rows of kv_out floats
 // each, stored at each item's position pos[i] and attended there); null in a plain
-// attention launch.  The fused form runs for f16 pools at d = 64, 128, 256.
+// attention launch.  The fused form runs at d = 64, 128, 256 for f16 pools, and for q8_0
+// pools unless the knob fused_q8 is 0.
 struct NewRows {
     const float *k = nullptr, *v = nullptr;
 };

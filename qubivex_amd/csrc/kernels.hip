@@ -19,6 +19,9 @@
 // probabilities (again high part + residual) against the V tile.  Accumulation is f32.
 // The score tile produced by the first MFMA is, lane for lane, the A operand of the
 // second, so probabilities never leave registers.
+#include <atomic>
+#include <string.h>
+
 #include "device.h"
 
 namespace qvkv {
@@ -1343,7 +1346,9 @@ void k_attn_stream_nr(QV_STREAM_PARAMS) {
                                                   table_at, pos, n_items, H, max_pos, out, ws,
                                                   hc_n, ucost, geo, err, nr);
 }
-// (3 waves/SIMD at d = 128: at the plain stream kernel's 4 its registers spill)
+// (3 waves/SIMD at d = 128: at the plain stream kernel's 4 its registers spill.  Its q8_0
+// tile code is the 4-wave builds' source; the 3-wave builds' wrong outputs were the
+// v_exp_f32 -> inline-asm v_mul_legacy_f32 wait state, now in the asm itself.)
 template <int D, bool PK>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 3 : 1)))
 void k_attn_stream_q8nr(QV_STREAM_PARAMS) {
@@ -1527,11 +1532,49 @@ int make_geometry(const qvkv_layout *l, Geometry *g, const char **why) {
     return QVKV_OK;
 }
 
-// Launch-shape knobs (defaults are the measured best); an environment variable of the
-// same name overrides one for measurement.
-int tune(const char *name, int def) {
-    const char *s = getenv(name);
-    return s && *s ? atoi(s) : def;
+// Launch-shape knobs: relaxed atomics, so a qvkv_tune on one thread and launches on others
+// are race-free (a launch sees the old or the new value).
+static const char *const kKnobName[KNOB_COUNT] = {
+#define QVKV_KNOB_NAME(id, name, def) name,
+    QVKV_KNOBS(QVKV_KNOB_NAME)
+#undef QVKV_KNOB_NAME
+};
+static constexpr int kKnobDefault[KNOB_COUNT] = {
+#define QVKV_KNOB_DEF(id, name, def) def,
+    QVKV_KNOBS(QVKV_KNOB_DEF)
+#undef QVKV_KNOB_DEF
+};
+static std::atomic<int> g_knob[KNOB_COUNT] = {
+#define QVKV_KNOB_DEF(id, name, def) {def},
+    QVKV_KNOBS(QVKV_KNOB_DEF)
+#undef QVKV_KNOB_DEF
+};
+
+int tune(Knob k) { return g_knob[k].load(std::memory_order_relaxed); }
+
+static int knob_of(const char *name) {
+    if (name)
+        for (int i = 0; i < KNOB_COUNT; i++)
+            if (strcmp(name, kKnobName[i]) == 0) return i;
+    return -1;
+}
+
+int set_tune(const char *name, int v) {
+    const int i = knob_of(name);
+    if (i < 0) return set_error(QVKV_E_SHAPE, "unknown knob '%s'", name ? name : "(null)");
+    g_knob[i].store(v, std::memory_order_relaxed);
+    return QVKV_OK;
+}
+
+int get_tune(const char *name, int *v) {
+    const int i = knob_of(name);
+    if (i < 0) return set_error(QVKV_E_SHAPE, "unknown knob '%s'", name ? name : "(null)");
+    if (v) *v = g_knob[i].load(std::memory_order_relaxed);
+    return QVKV_OK;
+}
+
+void reset_tune() {
+    for (int i = 0; i < KNOB_COUNT; i++) g_knob[i].store(kKnobDefault[i], std::memory_order_relaxed);
 }
 
 // Workgroups for a grid-stride kernel over `threads` work items, at most per_cu per CU.
@@ -1549,11 +1592,12 @@ hipError_t launch_append(const Geometry &g, void *pool, uint64_t pool_blocks, co
                          hipStream_t s) {
     const Geo geo = to_geo(g);
     const uint64_t per_row = 2 * (g.kv_out / 8);
-    const int U = tune("QVKV_APPEND_U", 2);
-    const uint64_t per_cu = (uint64_t)tune("QVKV_APPEND_GRID_PER_CU", 1 << 20);
+    const int U = tune(KNOB_APPEND_U);
+    const uint64_t per_cu = (uint64_t)tune(KNOB_APPEND_GRID_PER_CU);
     // f16: non-temporal f32 loads and f16 stores (a pure stream); q8_0 is faster with
     // cached loads (measured at cfg3: 4.78 vs 4.40 TB/s).
-    const bool NT = tune("QVKV_APPEND_NT", g.dtype == QVKV_F16 ? 1 : 0) != 0;
+    const int nt = tune(KNOB_APPEND_NT);
+    const bool NT = nt < 0 ? g.dtype == QVKV_F16 : nt != 0;
     // keep the flat index inside 32 bits: launch in batches of whole 16-row tiles
     const uint32_t max_rows = (uint32_t)((0x7fffffffull / per_row)) & ~15u;
     const bool tiled = g.D == 64 || g.D == 128 || g.D == 256;
@@ -1582,11 +1626,11 @@ hipError_t launch_append(const Geometry &g, void *pool, uint64_t pool_blocks, co
     else if (g.D == 128) QV_APPEND_Q8(UU, NN, 128);                                            \
     else QV_APPEND_Q8(UU, NN, 256);
         const bool q8fast = (g.D == 64 || g.D == 128 || g.D == 256) &&
-                            tune("QVKV_APPEND_Q8_FAST", 1) != 0;
+                            tune(KNOB_APPEND_Q8_FAST) != 0;
         if (g.dtype == QVKV_Q8_0 && q8fast) {
             // cached loads, non-temporal stores (measured at cfg3: 5.50 / 5.57 TB/s with cached
             // / non-temporal stores, 5.3 with non-temporal loads; 2 chunks per thread ahead of 4)
-            const int mode = (NT ? 1 : 0) | (tune("QVKV_APPEND_NTS", 1) ? 2 : 0);
+            const int mode = (NT ? 1 : 0) | (tune(KNOB_APPEND_NTS) ? 2 : 0);
 #define QV_APPEND_Q8_M(UU)                                                                     \
     if (mode == 0) { QV_APPEND_Q8_D(UU, 0) } else if (mode == 1) { QV_APPEND_Q8_D(UU, 1) }     \
     else if (mode == 2) { QV_APPEND_Q8_D(UU, 2) } else { QV_APPEND_Q8_D(UU, 3) }
@@ -1623,7 +1667,7 @@ hipError_t launch_gather(const Geometry &g, const void *pool, uint64_t pool_bloc
     // flight per thread (the f16 -> f16 copy moves 8 values per load, f16 -> f32 4)
     const uint64_t per_batch = 256ull * 8 * (out_dtype == QVKV_F16 ? 8 : 4);
     const uint64_t vals = 2ull * g.G * 16 * g.D;
-    uint32_t parts = tune("QVKV_GATHER_SPLIT", 1) ? (uint32_t)((vals + per_batch - 1) / per_batch) : 1u;
+    uint32_t parts = tune(KNOB_GATHER_SPLIT) ? (uint32_t)((vals + per_batch - 1) / per_batch) : 1u;
     if (g.dtype != QVKV_F16 || grid * parts > 0x7fffffffull) parts = 1;
 #define QV_GATHER(DT, OT)                                                                      \
     hipLaunchKernelGGL((k_gather<DT, OT>), dim3((unsigned)(grid * parts)), dim3(256), 0, s, p,  \
@@ -1633,15 +1677,15 @@ hipError_t launch_gather(const Geometry &g, const void *pool, uint64_t pool_bloc
     hipLaunchKernelGGL((k_gather_q8<DD>), dim3((unsigned)grid), dim3(256), 0, s, p,            \
                        pool_blocks, blocks, n_table, table_at, lens, out_at, n_items, tiles,   \
                        out_positions, (float *)out_k, (float *)out_v, geo, err)
-    const bool q8fast = tune("QVKV_GATHER_Q8_FAST", 1) != 0;
+    const bool q8fast = tune(KNOB_GATHER_Q8_FAST) != 0;
     if (g.dtype == QVKV_Q8_0 && q8fast && g.D == 64) QV_GATHER_Q8(64);
     else if (g.dtype == QVKV_Q8_0 && q8fast && g.D == 128) QV_GATHER_Q8(128);
     else if (g.dtype == QVKV_Q8_0 && q8fast && g.D == 256) QV_GATHER_Q8(256);
-    else if (g.dtype == QVKV_F16 && out_dtype == QVKV_F16 && tune("QVKV_GATHER_T", 64) == 64) {
+    else if (g.dtype == QVKV_F16 && out_dtype == QVKV_F16 && tune(KNOB_GATHER_T) == 64) {
         // f16 -> f16: one-wave workgroups of 4 loads per lane (4 KiB of a tile each), as for
         // the block copy.  Measured (4 runs each): cfg2 6.25-6.59 against 5.77-6.30 TB/s
         // for 256 threads x 8, cfg5 5.96-6.41 against 5.74-6.39; 1, 2 or 8 per lane slower.
-        const int uf = tune("QVKV_GATHER_UF", 4);
+        const int uf = tune(KNOB_GATHER_UF);
         const uint32_t UFv = uf >= 8 ? 8 : uf >= 4 ? 4 : uf >= 2 ? 2 : 1;
         const uint32_t parts64 = (uint32_t)((vals + 64ull * UFv * 8 - 1) / (64ull * UFv * 8));
 #define QV_G64(UU)                                                                              \
@@ -1669,9 +1713,9 @@ hipError_t launch_block_copy(const Geometry &g, void *pool, uint64_t pool_blocks
     // workgroups keep the most copies in flight.  Measured against 256 threads x 4 (16 KiB):
     // 32 KiB blocks 6.34-6.39 vs 5.61-5.66 TB/s, cfg4 compaction (64 KiB blocks) 5.43-5.53
     // vs 5.00-5.05; 2 or 4 per lane, 128 or 256 threads, and 8 per lane were slower.
-    const int ut = tune("QVKV_COPY_U", 1);
+    const int ut = tune(KNOB_COPY_U);
     const int U = ut >= 8 ? 8 : ut >= 4 ? 4 : ut >= 2 ? 2 : 1;
-    const int tt = tune("QVKV_COPY_T", 64);
+    const int tt = tune(KNOB_COPY_T);
     const int T = tt >= 256 ? 256 : tt >= 128 ? 128 : 64;
     const uint32_t per = (uint32_t)((g.block_bytes / 16 + (uint64_t)T * U - 1) / ((uint64_t)T * U));
     const uint64_t grid = (uint64_t)per * n;
@@ -1723,10 +1767,10 @@ int plan_attention(const Geometry &g, uint32_t n_items, uint32_t heads, uint32_t
     // the best context-chunk split and 3.98 / 3.48 with 512 / 1024 workgroups.  Launches of
     // 512 units and more (a layer of 128 x 8k, or of cfg3) run best unsplit: 6.0 and 4.8
     // TB/s, against 5.7 and 3.3-4.3 split by work.
-    const uint64_t full = (uint64_t)tune("QVKV_ATTN_FULL", 512);
-    if (tune("QVKV_ATTN_STREAM", 1) != 0 && units < full && n_items <= STREAM_MAX_ITEMS) {
+    const uint64_t full = (uint64_t)tune(KNOB_ATTN_FULL);
+    if (tune(KNOB_ATTN_STREAM) != 0 && units < full && n_items <= STREAM_MAX_ITEMS) {
         const uint64_t work = units * max_tiles;  // bound: the actual work is known on the device
-        uint64_t wgs = (uint64_t)tune("QVKV_ATTN_STREAM_WG", 768);
+        uint64_t wgs = (uint64_t)tune(KNOB_ATTN_STREAM_WG);
         if (wgs > (work + 3) / 4) wgs = (work + 3) / 4;  // at least a tile per wave
         if (wgs < 1) wgs = 1;
         p->kind = 2;
@@ -1735,13 +1779,13 @@ int plan_attention(const Geometry &g, uint32_t n_items, uint32_t heads, uint32_t
         // LDS merge and output) worth about 8 tiles: counting it in the shares evens out
         // workgroups that start several short units (cfg2-like layer of 32 ragged items:
         // 64.2 -> 60.1 us; contexts / 8: 31.7 -> 22.0 us; 4-24 within 2 % of 8).
-        p->ucost = (uint32_t)tune("QVKV_STREAM_UNIT_COST", 8);
+        p->ucost = (uint32_t)tune(KNOB_STREAM_UNIT_COST);
         p->ws_bytes = stream_rec_at(wgs, g.D, n_items) +
                       (uint64_t)n_items * g.G * p->hc * sizeof(StreamRec);
         return QVKV_OK;
     }
     // Else (QVKV_ATTN_STREAM=0) into context chunks, aiming at about 6 workgroups per CU.
-    const uint64_t target = (uint64_t)tune("QVKV_ATTN_TARGET", 1536);
+    const uint64_t target = (uint64_t)tune(KNOB_ATTN_TARGET);
     uint64_t nch = units >= full ? 1 : (target + units - 1) / units;
     const uint64_t cap = (max_tiles + 3) / 4;  // at least one tile per wave
     if (nch > cap) nch = cap;
@@ -1756,7 +1800,7 @@ int plan_attention(const Geometry &g, uint32_t n_items, uint32_t heads, uint32_t
 }
 
 bool fused_append_attention(const Geometry &g) {
-    return (g.dtype == QVKV_F16 || tune("QVKV_FUSED_Q8", 1) != 0) &&
+    return (g.dtype == QVKV_F16 || tune(KNOB_FUSED_Q8) != 0) &&
            (g.D == 64 || g.D == 128 || g.D == 256);
 }
 
@@ -1806,14 +1850,13 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
     }
     float *wsf = (float *)ws;
     const bool q8 = g.dtype == QVKV_Q8_0;
-    // q8_0 at d = 128 always runs its 4-wave builds (k_attn_mfma_w / k_attn_stream_w, MFMA
-    // accumulators in VGPRs): the same source built for 3 waves/SIMD (accumulators in AGPRs)
-    // returned wrong outputs in the oracle tests (both the unsplit and the split-by-work
-    // form), so those builds are not launched.  f16 selects its 4-wave build by
-    // QVKV_ATTN_WAVES4_F16 (measured slower, oracle tests green).
-    const bool w4 = q8 || tune("QVKV_ATTN_WAVES4_F16", 0) != 0;
+    // q8_0 at d = 128 runs its 4-wave builds (k_attn_mfma_w / k_attn_stream_w): its dequant
+    // VALU work needs the extra wave (4.82 vs 4.14 TB/s at cfg3).  The 3-wave builds
+    // (knob attn_waves3_q8) are kept for measurement and tested like the others.  f16
+    // selects its 4-wave build by the knob attn_waves4_f16 (measured slower).
+    const bool w4 = q8 ? tune(KNOB_ATTN_WAVES3_Q8) == 0 : tune(KNOB_ATTN_WAVES4_F16) != 0;
     // q8_0 with <= 4 query heads per KV head: two groups' probabilities per A operand
-    const bool pk = q8 && heads / (uint32_t)g.G <= 4 && tune("QVKV_ATTN_PACK", 1) != 0;
+    const bool pk = q8 && heads / (uint32_t)g.G <= 4 && tune(KNOB_ATTN_PACK) != 0;
     if (p.kind == 2) {
         const unsigned P = p.n_chunks;
 #define QV_AS(DD, QQ, PK)                                                                       \
@@ -1846,8 +1889,8 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
                 else if (w4) QV_AS_W4(128, false, false);
                 else QV_AS(128, false, false);
             }
-            else if (pk) QV_AS_W4(128, true, true);
-            else QV_AS_W4(128, true, false);
+            else if (pk) { if (w4) QV_AS_W4(128, true, true); else QV_AS(128, true, true); }
+            else { if (w4) QV_AS_W4(128, true, false); else QV_AS(128, true, false); }
         } else {
             if (!q8) { if (nr.k) QV_AS_NR(256); else QV_AS(256, false, false); }
             else if (pk) QV_AS(256, true, true);
@@ -1868,7 +1911,7 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
     // f16, d = 128, launches of one layer's items (cfg5: 512 workgroups): the table entries
     // fetched ahead of the tiles (per layer cfg5 16.7-17.2 -> 16.2 ms per step; the batched
     // launch of every layer lost 2-4 % with it)
-    const bool per_layer = grid < (uint64_t)tune("QVKV_ATTN_IDS_BELOW", 2048);
+    const bool per_layer = grid < (uint64_t)tune(KNOB_ATTN_IDS_BELOW);
     // K/V tiles are streamed with non-temporal loads (read once).
     // Occupancy: `mode` 0 is the compiler's register choice (3 waves/SIMD at d=128), 4
     // holds the kernel to 4 waves per SIMD (125 VGPRs, no spill).  Measured (cfg5 f16,
@@ -1911,8 +1954,8 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
             else if (per_layer) QV_ATTN_IDS(128);
             else QV_ATTN(128, false, false);
         }
-        else if (pk) QV_ATTN_W4(128, true, true);
-        else QV_ATTN_W4(128, true, false);
+        else if (pk) { if (w4) QV_ATTN_W4(128, true, true); else QV_ATTN(128, true, true); }
+        else { if (w4) QV_ATTN_W4(128, true, false); else QV_ATTN(128, true, false); }
     } else {
         if (!q8) { if (nr.k) QV_ATTN_NR(256); else QV_ATTN(256, false, false); }
         else if (pk) QV_ATTN(256, true, true);

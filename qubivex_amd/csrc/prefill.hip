@@ -1145,18 +1145,18 @@ hipError_t launch_prefill(const Geometry &g, const void *pool, uint64_t pool_blo
         return hipGetLastError();
     }
     const uint32_t GS = heads / (uint32_t)g.G;
-    if (!q8 && (g.D == 64 || g.D == 128) && tune("QVKV_PREFILL_V2", 1)) {
+    if (!q8 && (g.D == 64 || g.D == 128) && tune(KNOB_PREFILL_V2)) {
         const uint32_t n_qb = (uint32_t)(((uint64_t)max_tok * GS + 63) / 64);
         const unsigned grid2 = (unsigned)((uint64_t)n_seg * g.G * n_qb);
-        const unsigned pad = (unsigned)tune("QVKV_PREFILL_LDS_PAD", 0);
+        const unsigned pad = (unsigned)tune(KNOB_PREFILL_LDS_PAD);
 #define QV_PF2(DD, DMA, PS)                                                                    \
     hipLaunchKernelGGL((k_prefill_f16<DD, DMA, PS>), dim3(grid2), dim3(256), pad, s, pp,         \
                        pool_blocks, q, blocks, n_table, table_at, pos0, q_at, n_tok, n_seg,     \
                        heads, max_pos, max_tok, q_rows, n_qb, out, geo, err)
         // P as one f16 (the default) or as high part + residual (QVKV_PREFILL_EXACT_P=1)
-        const bool ps = tune("QVKV_PREFILL_EXACT_P", 0) != 0;
+        const bool ps = tune(KNOB_PREFILL_EXACT_P) != 0;
         if (g.D == 64) { if (ps) QV_PF2(64, false, true); else QV_PF2(64, false, false); }
-        else if (tune("QVKV_PREFILL_DMA", 1)) {
+        else if (tune(KNOB_PREFILL_DMA)) {
             if (ps) QV_PF2(128, true, true); else QV_PF2(128, true, false);
         } else {
             if (ps) QV_PF2(128, false, true); else QV_PF2(128, false, false);
@@ -1165,7 +1165,7 @@ hipError_t launch_prefill(const Geometry &g, const void *pool, uint64_t pool_blo
         return hipGetLastError();
     }
     // f16_values: the q8_0 MFMA-throughput form, which holds dequantised values in f16
-    if (q8 && g.D == 128 && f16_values && tune("QVKV_PREFILL_Q8_FAST", 1)) {
+    if (q8 && g.D == 128 && f16_values && tune(KNOB_PREFILL_Q8_FAST)) {
         const uint32_t n_qb = (uint32_t)(((uint64_t)max_tok * GS + 63) / 64);
         const unsigned grid3 = (unsigned)((uint64_t)n_seg * g.G * n_qb);
         hipLaunchKernelGGL((k_prefill_q8<128>), dim3(grid3), dim3(256), 0, s, pp, pool_blocks, q,

@@ -505,12 +505,12 @@ hipError_t launch_prelude(float *q, float *k, float *v, uint32_t s, uint32_t hea
     if (s == 0) return hipSuccess;
     const bool full = a.norm == QVKV_NORM_FULL;
     if ((d == 64 || d == 128 || d == 256) && (!full || (heads * d <= 4096 && kvh * d <= 4096)) &&
-        tune("QVKV_PRELUDE_FAST", 1) != 0) {
+        tune(KNOB_PRELUDE_FAST) != 0) {
         // per-head norms at d = 128: 2048 values per wave (one vector rms serves 16 heads;
         // +2 % at 32 query heads; 5 % slower at d = 256, equal at d = 64)
         const bool wide = !full && a.norm == QVKV_NORM_PER_HEAD && d == 128 &&
-                          tune("QVKV_PRELUDE_WIDE", 1) != 0;
-        if (full && tune("QVKV_PRELUDE_FULL_WG", 1) != 0) {
+                          tune(KNOB_PRELUDE_WIDE) != 0;
+        if (full && tune(KNOB_PRELUDE_FULL_WG) != 0) {
             // q rows, then k and v rows: waves per row by the row's length (16 values per
             // lane per wave)
             for (int kv = 0; kv < 2; kv++) {

@@ -18,6 +18,37 @@ from ._lib import F16, F32, Q8_0, check, lib
 _DTYPES = {"f16": F16, "q8_0": Q8_0}
 
 
+def tune(name: str, value: int) -> None:
+    """Sets a launch-shape knob (process-wide; see qvkv_tune)."""
+    check(lib.qvkv_tune(name.encode(), int(value)))
+
+
+def tune_get(name: str) -> int:
+    v = ctypes.c_int()
+    check(lib.qvkv_tune_get(name.encode(), ctypes.byref(v)))
+    return v.value
+
+
+def tune_reset() -> None:
+    lib.qvkv_tune_reset()
+
+
+class tuned:
+    """Context manager: knobs set for the block, every knob back to its default after."""
+
+    def __init__(self, knobs: dict):
+        self.knobs = dict(knobs)
+
+    def __enter__(self):
+        for k, v in self.knobs.items():
+            tune(k, v)
+        return self
+
+    def __exit__(self, *exc):
+        tune_reset()
+        return False
+
+
 @dataclass(frozen=True)
 class KvLayout:
     """Storage layout of a pool: dtype ("f16" or "q8_0"), kv_heads, head_dim, block."""

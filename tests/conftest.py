@@ -26,3 +26,14 @@ def hip():
     print(f"device: {dev.describe()}", flush=True)
     yield dev
     dev.close()
+
+
+@pytest.fixture
+def knobs():
+    """Sets launch-shape knobs through the library's qvkv_tune (knobs(name, value)); every
+    knob is back at its default after the test."""
+    from qubivex_amd import kv
+
+    kv.tune_reset()
+    yield kv.tune
+    kv.tune_reset()

@@ -159,3 +159,25 @@ def test_build_rejects_a_library_with_an_undefined_launch_stub(tmp_path):
     with pytest.raises(RuntimeError, match="undefined kernel launch stubs"):
         build._check_stubs(str(bad_c.with_suffix(".so")))
     assert not bad_c.with_suffix(".so").exists()
+
+
+def test_launch_knobs_are_set_through_the_api_only(monkeypatch):
+    """qvkv_tune sets a knob process-wide, qvkv_tune_reset restores every default, unknown
+    names are refused, and the environment has no say (the library reads none)."""
+    from qubivex_amd import kv, ShapeError
+
+    kv.tune_reset()
+    assert kv.tune_get("attn_full") == 512
+    assert kv.tune_get("attn_waves3_q8") == 0
+    monkeypatch.setenv("QVKV_ATTN_FULL", "7")
+    monkeypatch.setenv("attn_full", "7")
+    assert kv.tune_get("attn_full") == 512
+    kv.tune("attn_full", 9)
+    assert kv.tune_get("attn_full") == 9
+    with kv.tuned({"attn_stream": 0, "stream_unit_cost": 40}):
+        assert kv.tune_get("attn_stream") == 0 and kv.tune_get("stream_unit_cost") == 40
+    assert kv.tune_get("attn_full") == 512 and kv.tune_get("attn_stream") == 1
+    with pytest.raises(ShapeError):
+        kv.tune("no_such_knob", 1)
+    with pytest.raises(ShapeError):
+        kv.tune_get("QVKV_ATTN_FULL")

@@ -9,6 +9,7 @@ and require that no kernel places an asm instruction closer to its producers or 
 than gfx950 allows (tests/asm_hazards.py lists the rules).  CPU only: hipcc
 cross-compiles.
 """
+import importlib.util
 import os
 import shutil
 import subprocess
@@ -18,7 +19,14 @@ from concurrent.futures import ThreadPoolExecutor
 import pytest
 
 import asm_hazards as H
-from qubivex_amd import build as B
+
+# qubivex_amd/build.py by path: importing the package would load libqvkv.so at collection,
+# before torch has set up the HIP runtime that the library must share with it.
+_spec = importlib.util.spec_from_file_location(
+    "qvkv_build", os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                               "qubivex_amd", "build.py"))
+B = importlib.util.module_from_spec(_spec)
+_spec.loader.exec_module(B)
 
 pytestmark = pytest.mark.skipif(shutil.which("hipcc") is None, reason="hipcc not installed")
 

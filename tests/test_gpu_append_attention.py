@@ -5,7 +5,7 @@ the outputs and the pool bytes of qvkv_append_async at the same slots followed b
 qvkv_attention_async (whose parity with the oracle the attention tests pin), on every
 launch form (one workgroup per unit, the split by work, the context-chunk split), for f16
 and q8_0 pools (q8_0: the new rows quantised as the append stores them), and on the unfused
-paths (head dims without an MFMA kernel, or QVKV_FUSED_Q8=0)."""
+paths (head dims without an MFMA kernel, or the knob fused_q8 = 0)."""
 import numpy as np
 import pytest
 
@@ -16,46 +16,46 @@ CASES = [
     # dtype, kv heads, query heads, d, block, sequence lengths before the step, env
     ("f16", 8, 32, 128, 16, [300, 17, 4096, 1000, 64, 1], {}),             # split by work
     ("f16", 4, 32, 128, 16, [2049, 15, 16, 31, 33] * 26, {}),              # one per unit
-    ("f16", 8, 32, 128, 16, [3000, 700, 129], {"QVKV_ATTN_STREAM": "0"}),  # context chunks
+    ("f16", 8, 32, 128, 16, [3000, 700, 129], {"attn_stream": "0"}),  # context chunks
     ("f16", 2, 32, 128, 32, [95, 96, 97, 500], {}),                        # 2 head chunks
     ("f16", 8, 16, 64, 16, [200, 47, 1], {}),
     ("f16", 4, 8, 256, 256, [600, 255, 256], {}),
     ("q8_0", 8, 32, 128, 16, [300, 1000, 31], {}),                         # split by work
     ("q8_0", 4, 32, 128, 16, [2049, 15, 16, 31, 33] * 26, {}),             # one per unit
     ("q8_0", 8, 32, 128, 16, [1000, 17, 64, 4095] * 32, {}),               # one per unit, packed
-    ("q8_0", 8, 32, 128, 16, [3000, 700, 129], {"QVKV_ATTN_STREAM": "0"}),  # context chunks
+    ("q8_0", 8, 32, 128, 16, [3000, 700, 129], {"attn_stream": "0"}),  # context chunks
     ("q8_0", 2, 32, 128, 32, [95, 96, 97, 500], {}),                       # 2 head chunks
     ("q8_0", 8, 16, 64, 16, [200, 47, 1], {}),
     ("q8_0", 4, 8, 256, 256, [600, 255, 256], {}),
-    ("q8_0", 8, 32, 128, 16, [300, 31], {"QVKV_FUSED_Q8": "0"}),           # unfused
+    ("q8_0", 8, 32, 128, 16, [300, 31], {"fused_q8": "0"}),           # unfused
     ("f16", 4, 8, 96, 16, [100, 33], {}),                                  # unfused (generic)
 ]
 
 
 @pytest.mark.parametrize("dtype,G,H,D,B,lens,env", CASES)
 def test_append_attention_equals_append_then_attention(hip, dtype, G, H, D, B, lens, env,
-                                                       monkeypatch):
-    run_case(hip, dtype, G, H, D, B, lens, env, monkeypatch)
+                                                       knobs):
+    run_case(hip, dtype, G, H, D, B, lens, env, knobs)
 
 
 @pytest.mark.parametrize("dtype,lens,env", [
     ("f16", [300, 17, 64], {}), ("f16", [2049, 15] * 130, {}),
     ("q8_0", [300, 17, 64], {}), ("q8_0", [2049, 15] * 130, {}),
 ])
-def test_append_attention_with_special_values_in_the_new_rows(hip, dtype, lens, env, monkeypatch):
+def test_append_attention_with_special_values_in_the_new_rows(hip, dtype, lens, env, knobs):
     """NaN, infinities, values past the f16 range, f32 subnormals and an all-zero q8_0 group
     in the step's new rows: the fused launch narrows or quantises them exactly as the append
     (compared bit for bit, NaN outputs included)."""
-    run_case(hip, dtype, 8, 32, 128, 16, lens, env, monkeypatch, special=True)
+    run_case(hip, dtype, 8, 32, 128, 16, lens, env, knobs, special=True)
 
 
-def run_case(hip, dtype, G, H, D, B, lens, env, monkeypatch, special=False):
+def run_case(hip, dtype, G, H, D, B, lens, env, knobs, special=False):
     from qubivex_amd import KvLayout, KvPool
 
     print(f"append+attention {dtype} G={G} H={H} D={D} B={B} items={len(lens)} env={env} "
           f"special={special}", flush=True)
     for k, v in env.items():
-        monkeypatch.setenv(k, v)
+        knobs(k, int(v))
     L = KvLayout(dtype, G, D, B)
     S = len(lens)
     N = sum(n // B + 2 for n in lens) + 8

@@ -520,3 +520,69 @@ def test_graph_replays_of_append_and_attention_match_eager(hip):
         hip.check(s)
         assert torch.equal(out, ref), ("fused", rep)
     pool.close()
+
+
+def test_workspace_growth_on_one_stream_does_not_stall_another(hip):
+    """Thread A's attention must grow its stream's workspace, which waits for stream A to
+    drain, behind ~0.4 s of queued work.  Meanwhile thread B appends on stream B: its call
+    returns while A is still waiting (the wait holds only stream A's lock), and both
+    results match the oracle."""
+    import time
+
+    import torch
+
+    from qubivex_amd import KvLayout
+
+    L = KvLayout("f16", 4, 128, 16)
+    H = 32
+    r = np.random.default_rng(77)
+    n = 3000
+    N = n // 16 + 9
+    blocks, table_at = random_tables(r, [n], 16, N)
+    k = r.standard_normal((n, L.kv_out)).astype(np.float32)
+    v = r.standard_normal((n, L.kv_out)).astype(np.float32)
+    q = r.standard_normal((1, H, 128)).astype(np.float32)
+    slots = slots_of(blocks, table_at, 0, np.arange(n), 16)
+    t32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.uint32).view(np.int32)).cuda()  # noqa: E731
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    pool_a = torch.zeros(N * L.block_bytes, dtype=torch.uint8, device="cuda")
+    pool_b = torch.zeros(N * L.block_bytes, dtype=torch.uint8, device="cuda")
+    dk, dv, dq = (torch.from_numpy(x).cuda() for x in (k, v, q))
+    ds, db, dt, dp = t32(slots), t32(blocks), t32(table_at), t32([n - 1])
+    out = torch.full((1, H, 128), float("nan"), device="cuda")
+    a_mat = torch.randn(8192, 8192, device="cuda")
+    torch.cuda.synchronize()
+    # each stream's state exists before the timed part (its first use allocates)
+    hip.append(L, pool_a, N, dk, dv, ds, stream=sa)
+    hip.append(L, pool_b, N, dk[:1], dv[:1], ds[:1], stream=sb)
+    hip.check(sa)
+    hip.check(sb)
+    with torch.cuda.stream(sa):
+        for _ in range(40):  # ~0.4 s of work queued on stream A
+            a_mat = a_mat @ a_mat * (1.0 / 8192)
+    a_done = threading.Event()
+
+    def thread_a():
+        hip.attention(L, pool_a, N, dq, db, dt, dp, H, n - 1, out, stream=sa)
+        a_done.set()
+
+    ta = threading.Thread(target=thread_a)
+    ta.start()
+    time.sleep(0.05)
+    assert not sa.query(), "stream A drained before the measurement (work too short)"
+    t0 = time.perf_counter()
+    hip.append(L, pool_b, N, dk, dv, ds, stream=sb)
+    dt_b = time.perf_counter() - t0
+    a_waiting = not a_done.is_set() and not sa.query()
+    ta.join()
+    hip.check(sa)
+    hip.check(sb)
+    print(f"  append on stream B returned in {dt_b * 1e3:.2f} ms; A still waiting: {a_waiting}",
+          flush=True)
+    assert a_waiting, "stream B's append waited for stream A's workspace growth"
+    sim = oracle.SimPool(N, 4, 128, 16, oracle.F16)
+    sim.store(k, v, slots)
+    want = sim.attention(q, H, blocks, table_at, np.array([n - 1], np.uint32))
+    e = attn_errors(out.cpu().numpy(), want)
+    assert e[0] <= MAX_ABS and e[1] <= REL_L2, e
+    assert torch.equal(pool_a, pool_b)  # B's append stored the same rows

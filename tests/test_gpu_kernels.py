@@ -3,7 +3,6 @@
 Append, gather and block copy are checked bit for bit; attention within max-abs 2e-3
 and relative L2 1e-3 of the oracle's `attend` (f32, the reference's sequential order).
 """
-import os
 
 import numpy as np
 import pytest
@@ -250,21 +249,22 @@ def test_attention_within_tolerance(hip, dtype, H, G, D, lens):
     assert max_abs <= MAX_ABS and rel <= REL_L2, (max_abs, rel)
 
 
-# Launch switches a caller may set (QVKV_* environment variables read at each launch) and
-# a few shapes each, from ATTN_CASES: every selectable build must meet the same tolerance.
+# Launch switches a caller may set (qvkv_tune knobs, read at each launch) and a few shapes
+# each, from ATTN_CASES: every selectable build must meet the same tolerance.
 SWITCH_CASES = [ATTN_CASES[i] for i in (0, 1, 8, 9)] + ATTN_CASES[-4:]
 
 
-@pytest.mark.parametrize("env", [{"QVKV_ATTN_WAVES4_F16": "1"}, {"QVKV_ATTN_PACK": "0"},
-                                 {"QVKV_ATTN_XCD": "0"}, {"QVKV_ATTN_IDS_BELOW": "0"},
-                                 {"QVKV_STREAM_UNIT_COST": "0"}, {"QVKV_STREAM_UNIT_COST": "40"},
-                                 {"QVKV_ATTN_STREAM": "0"}],
+@pytest.mark.parametrize("env", [{"attn_waves4_f16": "1"}, {"attn_waves3_q8": "1"},
+                                 {"attn_pack": "0"},
+                                 {"attn_xcd": "0"}, {"attn_ids_below": "0"},
+                                 {"stream_unit_cost": "0"}, {"stream_unit_cost": "40"},
+                                 {"attn_stream": "0"}],
                          ids=lambda e: ",".join(f"{k}={v}" for k, v in e.items()))
 @pytest.mark.parametrize("dtype,H,G,D,lens", SWITCH_CASES)
 def test_attention_launch_switches_stay_within_tolerance(hip, dtype, H, G, D, lens, env,
-                                                         monkeypatch):
+                                                         knobs):
     for k, v in env.items():
-        monkeypatch.setenv(k, v)
+        knobs(k, int(v))
     test_attention_within_tolerance(hip, dtype, H, G, D, lens)
 
 
@@ -308,11 +308,11 @@ def test_attention_ignores_nan_in_unwritten_slots(hip, dtype):
 
 
 @pytest.mark.parametrize("split", ["work", "chunks"])
-def test_attention_split_context_8k(hip, split, monkeypatch):
+def test_attention_split_context_8k(hip, split, knobs):
     """One long item alone: the launch splits the context (by work, the default, or into
     context chunks) and merges the partials."""
     if split == "chunks":
-        monkeypatch.setenv("QVKV_ATTN_STREAM", "0")
+        knobs("attn_stream", 0)
     r = rng(7)
     L = layout(F16, 4, 128)
     lens = [8192]
@@ -333,12 +333,12 @@ def test_attention_split_context_8k(hip, split, monkeypatch):
 
 @pytest.mark.parametrize("dtype", [F16, Q8_0])
 @pytest.mark.parametrize("split", ["work", "chunks"])
-def test_attention_split_ragged_batch(hip, dtype, split, monkeypatch):
+def test_attention_split_ragged_batch(hip, dtype, split, knobs):
     """A small ragged batch (one layer of a decode step in model order: 24 items of 1 to
     3000 positions, 8 KV heads, so 192 units): split by work, units are cut across
     workgroup ranges at arbitrary tiles and merged; both split forms against the oracle."""
     if split == "chunks":
-        monkeypatch.setenv("QVKV_ATTN_STREAM", "0")
+        knobs("attn_stream", 0)
     r = rng(71 + (dtype == Q8_0))
     L = layout(dtype, 8, 128)
     lens = [int(x) for x in r.integers(1, 3000, 24)]
@@ -573,11 +573,9 @@ def test_attention_propagates_nan_and_inf_like_the_reference(hip, dtype, H, G, D
         from qubivex_amd import UnsupportedError
         with pytest.raises(UnsupportedError):
             prefill()
-        os.environ["QVKV_PREFILL_Q8_FAST"] = "0"
-        try:
+        from qubivex_amd import kv
+        with kv.tuned({"prefill_q8_fast": 0}):
             prefill()
-        finally:
-            del os.environ["QVKV_PREFILL_Q8_FAST"]
     else:
         prefill()
     gotp = outp.cpu().numpy().reshape(T, H, D)

@@ -124,13 +124,13 @@ def test_prefill_reads_no_table_entry_past_a_segment(hip, dtype, D):
 
 
 @pytest.mark.parametrize("exact_p", [True, False])
-def test_prefill_equals_decode_kernel_per_token(hip, exact_p, monkeypatch):
+def test_prefill_equals_decode_kernel_per_token(hip, exact_p, knobs):
     """The prefill kernel and the decode kernel (one item per token) agree to float
     rounding on the same pool: the same tiles, scores and softmax, another order (with
     the prefill's P as high part + residual); with P as one f16 (the default prefill)
     to its rounding, 2^-11 relative per probability."""
     if exact_p:
-        monkeypatch.setenv("QVKV_PREFILL_EXACT_P", "1")
+        knobs("prefill_exact_p", 1)
     r = rng(31)
     L = layout(F16, 8, 128)
     H = 32
@@ -241,17 +241,17 @@ def _f64_attention(k16, v16, q, g_of, npos):
 
 
 @pytest.mark.parametrize("kind", ["prefill", "prefill_exact_p", "decode"])
-def test_f16_paths_track_float64_closely(hip, kind, monkeypatch):
+def test_f16_paths_track_float64_closely(hip, kind, knobs):
     """With f16 K/V the products q.k and p.v are exact in the MFMAs when q and p are
     carried as f16 high part + residual (decode, and the prefill with
-    QVKV_PREFILL_EXACT_P=1): those paths sit within ~1e-6 of float64.  Pins the split: a
+    knob prefill_exact_p = 1): those paths sit within ~1e-6 of float64.  Pins the split: a
     high part and residual taken from two different roundings of the same product (a
     contraction into v_fma_mix for one of them) leaves one-ulp errors that show up here
     as ~1e-5.  The default prefill carries P as one f16 (relative error 2^-11 per
     probability, normalised by the sum of the rounded values): about 2e-5 here, held
     under 2e-4, ten times inside the reference tolerance of 2e-3."""
     if kind == "prefill_exact_p":
-        monkeypatch.setenv("QVKV_PREFILL_EXACT_P", "1")
+        knobs("prefill_exact_p", 1)
     r = rng(77)
     G, D, H = 4, 128, 32
     L = layout(F16, G, D)

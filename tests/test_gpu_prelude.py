@@ -47,11 +47,11 @@ CASES = [
 
 @pytest.mark.parametrize("fast", [1, 0], ids=["default", "lds_kernel"])
 @pytest.mark.parametrize("heads,kvh,d,norm,clip,bias,scale", CASES)
-def test_prelude_bit_exact(hip, monkeypatch, heads, kvh, d, norm, clip, bias, scale, fast):
+def test_prelude_bit_exact(hip, knobs, heads, kvh, d, norm, clip, bias, scale, fast):
     from qubivex_amd import KvLayout
 
-    # QVKV_PRELUDE_FAST=0 forces the LDS kernel, the form for every other shape
-    monkeypatch.setenv("QVKV_PRELUDE_FAST", str(fast))
+    # the knob prelude_fast = 0 forces the LDS kernel, the form for every other shape
+    knobs("prelude_fast", int(fast))
     print(f"prelude heads={heads} kvh={kvh} d={d} norm={norm} clip={clip} bias={bias} "
           f"fast={fast}", flush=True)
     r = np.random.default_rng(heads * d + kvh)

@@ -29,9 +29,9 @@ torch = pytest.importorskip("torch")
 # launch forms of a decode attention launch, chosen by the library's tuning variables
 FORMS = {
     "default": {},
-    "unsplit": {"QVKV_ATTN_FULL": "1"},                                   # one workgroup per unit
-    "work": {"QVKV_ATTN_FULL": "1000000000", "QVKV_ATTN_STREAM": "1"},    # split by work
-    "chunks": {"QVKV_ATTN_FULL": "1000000000", "QVKV_ATTN_STREAM": "0"},  # context chunks
+    "unsplit": {"attn_full": "1"},                                   # one workgroup per unit
+    "work": {"attn_full": "1000000000", "attn_stream": "1"},    # split by work
+    "chunks": {"attn_full": "1000000000", "attn_stream": "0"},  # context chunks
 }
 
 
@@ -58,11 +58,11 @@ SEEDS = list(range(7000, 7100))
 
 
 @pytest.mark.parametrize("seed", SEEDS)
-def test_random_shapes_match_the_oracle(hip, seed, monkeypatch):
+def test_random_shapes_match_the_oracle(hip, seed, knobs):
     dtype, D, G, H, B, lens, form = draw(seed)
     print(f"sweep seed={seed} {dtype} D={D} G={G} H={H} B={B} form={form} lens={lens}", flush=True)
     for k, v in FORMS[form].items():
-        monkeypatch.setenv(k, v)
+        knobs(k, int(v))
     r = rng(seed)
     L = layout(dtype, G, D, B)
     N = sum((x + B - 1) // B for x in lens) + 3
@@ -110,11 +110,11 @@ def test_random_shapes_match_the_oracle(hip, seed, monkeypatch):
 
 
 @pytest.mark.parametrize("seed", SEEDS[::2])
-def test_random_shapes_fused_append_attention(hip, seed, monkeypatch):
+def test_random_shapes_fused_append_attention(hip, seed, knobs):
     from test_gpu_append_attention import run_case
 
     dtype, D, G, H, B, lens, form = draw(seed)
-    run_case(hip, "f16" if dtype == F16 else "q8_0", G, H, D, B, lens, FORMS[form], monkeypatch)
+    run_case(hip, "f16" if dtype == F16 else "q8_0", G, H, D, B, lens, FORMS[form], knobs)
 
 
 @pytest.mark.parametrize("seed", SEEDS[1::2])

@@ -62,13 +62,13 @@ def test_noalloc_attention_equals_the_allocating_form(hip, dtype):
         assert torch.equal(got, want), (n_items, float((got - want).abs().max()))
 
 
-def test_noalloc_attention_refuses_a_launch_past_its_scratch(hip, monkeypatch):
+def test_noalloc_attention_refuses_a_launch_past_its_scratch(hip, knobs):
     from qubivex_amd import KvLayout, ShapeError, _lib
 
     # a tiny launch over a long context split by work over as many workgroups as it has
     # 4-tile shares (8192 here): 2 partial slots x 8 heads x 258 floats per workgroup need
     # more than the scratch array holds
-    monkeypatch.setenv("QVKV_ATTN_STREAM_WG", "100000")
+    knobs("attn_stream_wg", 100000)
     L = KvLayout("f16", 1, 256, 16)
     q = torch.zeros((8, 8, 256), device="cuda")
     out = torch.zeros_like(q)
