@@ -75,12 +75,23 @@ typedef struct qvkv_usage_t {
 } qvkv_usage_t;
 
 /* Copies so far: TransferStats (crates/qubivex-compute/src/discrete.rs:376-427).
- * timed / gpu_ns: the synchronous calls whose GPU time was measured and that time summed
- * (TransferStats::timed, gpu_ns); stream_waits: pool copies that waited for a caller's
- * stream. */
+ *  uploads / upload_bytes: host-to-device copies (qvkv_write and the host-memory entry
+ *    points' staged inputs); downloads / download_bytes: device-to-host copies;
+ *  submissions: kernel launches made (every entry point);
+ *  wait_ns / fence_waits: host time blocked waiting for the device, and the waits;
+ *  timed / gpu_ns: the synchronous calls whose GPU time was measured, and that time summed;
+ *  stream_waits: pool copies that waited for a caller's stream (no counterpart);
+ *  activations_in / activations_out: bytes the host-memory entry points staged in and
+ *    copied back;
+ *  transfer_ns: GPU time of those calls' copies (events around them) plus the wall time of
+ *    qvkv_write / qvkv_read;
+ *  submit_ns: host time inside the library's calls, less their waits;
+ *  gpu_busy_ns: union of the timed calls' GPU intervals; they run one at a time on the
+ *    device's own stream, so it equals gpu_ns. */
 typedef struct qvkv_transfers_t {
     uint64_t uploads, upload_bytes, downloads, download_bytes, submissions, wait_ns;
     uint64_t timed, gpu_ns, stream_waits;
+    uint64_t activations_in, activations_out, transfer_ns, fence_waits, submit_ns, gpu_busy_ns;
 } qvkv_transfers_t;
 
 /* Detail of the calling thread's last failure (ComputeError's Display). Returns the
@@ -216,7 +227,8 @@ int qvkv_append_attention_async(qvkv_dev *dev, const qvkv_layout *layout, void *
  * call on one GPU shares that array (the last call's contents stay in it): calls that
  * overlap on one GPU, on any streams or device handles, race.  Index errors its kernels
  * latch go to a device-wide flag in the same array, reported (and cleared) by the next
- * qvkv_check on any stream of the device. */
+ * check on any stream of the device: a qvkv_check, or the host-memory entry points' own
+ * check, which then returns QVKV_E_SHAPE for it. */
 #define QVKV_NOALLOC_SCRATCH_BYTES (32ull << 20)
 int qvkv_attention_noalloc_async(qvkv_dev *dev, const qvkv_layout *layout, const void *pool,
                                  uint64_t pool_blocks, const float *q, const uint32_t *blocks,
@@ -339,10 +351,12 @@ int qvkv_prelude_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *p
 typedef struct qvkv_pool qvkv_pool;
 
 /* Counters: KvPoolStats (crates/qubivex-runtime/src/discrete.rs:92-108) plus the
- * sharing and compaction counters this path adds. */
+ * sharing and compaction counters this path adds.  allocated: 1 when the pool holds device
+ * memory (a device pool allocates it whole at qvkv_pool_create), 0 for a host-only pool. */
 typedef struct qvkv_pool_stats_t {
     uint64_t bytes, blocks, free, layers, synced_rows, full;
     uint64_t shared_blocks, cow_copies, evicted_blocks, moved_blocks;
+    uint64_t allocated;
 } qvkv_pool_stats_t;
 
 /* A pool of n_blocks blocks (OnDevice::new pool sizing, discrete.rs:429-455; the free

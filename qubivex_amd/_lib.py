@@ -53,13 +53,16 @@ class Usage(ctypes.Structure):
 class Transfers(ctypes.Structure):
     _fields_ = [(n, ctypes.c_uint64) for n in ("uploads", "upload_bytes", "downloads",
                                                 "download_bytes", "submissions", "wait_ns",
-                                                "timed", "gpu_ns", "stream_waits")]
+                                                "timed", "gpu_ns", "stream_waits",
+                                                "activations_in", "activations_out",
+                                                "transfer_ns", "fence_waits", "submit_ns",
+                                                "gpu_busy_ns")]
 
 
 class PoolStats(ctypes.Structure):
     _fields_ = [(n, ctypes.c_uint64) for n in ("bytes", "blocks", "free", "layers", "synced_rows",
                                                 "full", "shared_blocks", "cow_copies",
-                                                "evicted_blocks", "moved_blocks")]
+                                                "evicted_blocks", "moved_blocks", "allocated")]
 
 
 NORM_NONE, NORM_FULL, NORM_PER_HEAD = 0, 1, 2

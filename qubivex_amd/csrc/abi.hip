@@ -97,6 +97,13 @@ struct qvkv_dev {
     std::atomic<uint64_t> uploads{0}, upload_bytes{0}, downloads{0}, download_bytes{0};
     std::atomic<uint64_t> submissions{0}, wait_ns{0}, timed{0}, gpu_ns{0}, last_gpu_ns{0};
     std::atomic<uint64_t> stream_waits{0};
+    // TransferStats' remaining fields: activations_in / _out (bytes the host-memory entry
+    // points stage in and copy back), transfer_ns (their copies' GPU time from events, plus
+    // the synchronous write / read calls), fence_waits (host waits for completion),
+    // submit_ns (host time in the library's calls outside those waits).
+    std::atomic<uint64_t> act_in{0}, act_out{0}, transfer_ns{0}, fence_waits{0}, submit_ns{0};
+    hipEvent_t c0 = nullptr, c1 = nullptr, d0 = nullptr, d1 = nullptr;  // copy intervals
+    bool up_open = false, down_open = false;  // under host_mu: this call's copies recorded
     uint8_t *scratch = nullptr;  // this device's copy of `scratch` (allocation-free entry)
     int *scratch_err = nullptr;  // its error flag (the first 256 bytes)
     char name[256] = {0};
@@ -114,6 +121,8 @@ void release(qvkv_dev *dev) {
     if (dev->refs.fetch_sub(1) != 1) return;
     (void)hipSetDevice(dev->device);
     if (dev->order_ev) (void)hipEventDestroy(dev->order_ev);
+    for (hipEvent_t ev : {dev->c0, dev->c1, dev->d0, dev->d1})
+        if (ev) (void)hipEventDestroy(ev);
     if (dev->t0) (void)hipEventDestroy(dev->t0);
     if (dev->t1) (void)hipEventDestroy(dev->t1);
     if (dev->stream) (void)hipStreamDestroy(dev->stream);
@@ -248,6 +257,7 @@ struct Stager {
     int upload(qvkv_dev *dev) {
         int rc = ensure(dev, dev->stream, &dev->stage, &dev->stage_bytes, total);
         if (rc) return rc;
+        (void)hipEventRecord(dev->c0, dev->stream);
         for (auto &p : pieces) {
             if (!p.src || !p.len) continue;
             hipError_t e = hipMemcpyAsync((char *)dev->stage + p.off, p.src, p.len,
@@ -255,7 +265,10 @@ struct Stager {
             if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync (upload)");
             dev->uploads.fetch_add(1);
             dev->upload_bytes.fetch_add(p.len);
+            dev->act_in.fetch_add(p.len);
         }
+        (void)hipEventRecord(dev->c1, dev->stream);
+        dev->up_open = true;
         return QVKV_OK;
     }
     template <class T>
@@ -264,23 +277,73 @@ struct Stager {
     }
 };
 
-int download(qvkv_dev *dev, void *host, const void *devp, uint64_t len) {
+// A copy back on the device's stream (caller holds host_mu); the call's copies back are
+// timed from before the first to after the last.
+int download(qvkv_dev *dev, void *host, const void *devp, uint64_t len, bool output = true) {
     if (!len) return QVKV_OK;
+    if (output) dev->act_out.fetch_add(len);
+    if (!dev->down_open) (void)hipEventRecord(dev->d0, dev->stream);
     hipError_t e = hipMemcpyAsync(host, devp, len, hipMemcpyDeviceToHost, dev->stream);
     if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync (download)");
+    (void)hipEventRecord(dev->d1, dev->stream);
+    dev->down_open = true;
     dev->downloads.fetch_add(1);
     dev->download_bytes.fetch_add(len);
     return QVKV_OK;
 }
 
-// Takes latched error bits: one thread exchanges each flag with 0 (so bits a kernel
-// latches meanwhile are never lost) and keeps what it held in flag[1].  `other` is the
-// device-wide flag of the allocation-free entry point (may be null).
-__global__ void k_take_error(int *flag, int *other) {
-    if (threadIdx.x == 0) {
-        flag[1] = atomicExch(&flag[0], 0);
-        if (other) other[1] = atomicExch(&other[0], 0);
+// After the device's stream has drained: the GPU time of this call's copies into
+// transfer_ns (caller holds host_mu).
+void take_copy_time(qvkv_dev *dev) {
+    float ms = 0.f;
+    if (dev->up_open && hipEventElapsedTime(&ms, dev->c0, dev->c1) == hipSuccess)
+        dev->transfer_ns.fetch_add((uint64_t)((double)ms * 1e6));
+    if (dev->down_open && hipEventElapsedTime(&ms, dev->d0, dev->d1) == hipSuccess)
+        dev->transfer_ns.fetch_add((uint64_t)((double)ms * 1e6));
+    (void)hipGetLastError();
+    dev->up_open = dev->down_open = false;
+}
+
+// Host time waiting for the device on this thread (finish, write, read): a call's
+// submit time is its host time less this.
+thread_local uint64_t t_wait_ns = 0;
+
+uint64_t now_ns() {
+    return (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
+               std::chrono::steady_clock::now().time_since_epoch())
+        .count();
+}
+
+// Adds the host time of one library call, less its waits, to submit_ns.
+struct SubmitTimer {
+    qvkv_dev *dev;
+    uint64_t t0, w0;
+    explicit SubmitTimer(qvkv_dev *d) : dev(d), t0(now_ns()), w0(t_wait_ns) {}
+    ~SubmitTimer() {
+        if (!dev) return;
+        const uint64_t spent = now_ns() - t0, waited = t_wait_ns - w0;
+        dev->submit_ns.fetch_add(spent > waited ? spent - waited : 0);
     }
+};
+
+// A host wait for the device: counted in fence_waits and wait_ns.
+hipError_t fence_wait(qvkv_dev *dev, hipStream_t s) {
+    const uint64_t t0 = now_ns();
+    hipError_t e = hipStreamSynchronize(s);
+    const uint64_t dt = now_ns() - t0;
+    t_wait_ns += dt;
+    dev->wait_ns.fetch_add(dt);
+    dev->fence_waits.fetch_add(1);
+    return e;
+}
+
+// Takes latched error bits: one thread exchanges each flag with 0 (so bits a kernel
+// latches meanwhile are never lost) and leaves what they held in the calling stream's own
+// flag[1].  `other` is the device-wide flag of the allocation-free entry point (may be
+// null): what it held goes to this stream's slot too, never to a slot another stream's
+// check also writes.
+__global__ void k_take_error(int *flag, int *other) {
+    if (threadIdx.x == 0) flag[1] = atomicExch(&flag[0], 0) | (other ? atomicExch(&other[0], 0) : 0);
 }
 
 // The status a set of latched bits stands for.
@@ -303,22 +366,16 @@ int status_of(int bits) {
 // QVKV_E_SHAPE (clearing them).
 int finish(qvkv_dev *dev, StreamState *st) {
     std::lock_guard<std::mutex> lk(st->check_mu);
-    auto t0 = std::chrono::steady_clock::now();
     int *other = dev->scratch_err;
     hipLaunchKernelGGL(k_take_error, dim3(1), dim3(64), 0, st->stream, st->d_err, other);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "error flag launch");
-    int bits = 0, more = 0;
+    int bits = 0;
     e = hipMemcpyAsync(&bits, st->d_err + 1, sizeof bits, hipMemcpyDeviceToHost, st->stream);
-    if (e == hipSuccess && other)
-        e = hipMemcpyAsync(&more, other + 1, sizeof more, hipMemcpyDeviceToHost, st->stream);
     if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync (error flag)");
-    e = hipStreamSynchronize(st->stream);
-    dev->wait_ns.fetch_add((uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
-                               std::chrono::steady_clock::now() - t0)
-                               .count());
+    e = fence_wait(dev, st->stream);
     if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
-    return status_of(bits | more);
+    return status_of(bits);
 }
 
 int launched(qvkv_dev *dev, hipError_t e, const char *what) {
@@ -337,6 +394,7 @@ void time_take(qvkv_dev *dev);
 int finish_timed(qvkv_dev *dev) {
     const int rc = finish(dev, dev->own);
     if (rc == QVKV_OK) time_take(dev);
+    take_copy_time(dev);
     return rc;
 }
 
@@ -394,7 +452,9 @@ int qvkv_open(int device, qvkv_dev **out) {
         return hip_fail(e, "hipStreamCreate");
     }
     if ((e = hipEventCreateWithFlags(&d->order_ev, hipEventDisableTiming)) != hipSuccess ||
-        (e = hipEventCreate(&d->t0)) != hipSuccess || (e = hipEventCreate(&d->t1)) != hipSuccess) {
+        (e = hipEventCreate(&d->t0)) != hipSuccess || (e = hipEventCreate(&d->t1)) != hipSuccess ||
+        (e = hipEventCreate(&d->c0)) != hipSuccess || (e = hipEventCreate(&d->c1)) != hipSuccess ||
+        (e = hipEventCreate(&d->d0)) != hipSuccess || (e = hipEventCreate(&d->d1)) != hipSuccess) {
         qvkv_close(d);
         return hip_fail(e, "hipEventCreate");
     }
@@ -486,6 +546,14 @@ int qvkv_transfers(const qvkv_dev *dev, qvkv_transfers_t *out) {
     out->timed = dev->timed.load();
     out->gpu_ns = dev->gpu_ns.load();
     out->stream_waits = dev->stream_waits.load();
+    out->activations_in = dev->act_in.load();
+    out->activations_out = dev->act_out.load();
+    out->transfer_ns = dev->transfer_ns.load();
+    out->fence_waits = dev->fence_waits.load();
+    out->submit_ns = dev->submit_ns.load();
+    // the timed calls run one at a time on the device's own stream (host_mu): their GPU
+    // intervals never overlap, so their union is their sum
+    out->gpu_busy_ns = dev->gpu_ns.load();
     return QVKV_OK;
 }
 
@@ -528,14 +596,17 @@ int qvkv_write(qvkv_dev *dev, qvkv_buf *buf, size_t offset, const void *host, si
     if (offset > buf->len || len > buf->len - offset)
         return fail(QVKV_E_DEVICE, "hip device error: write of %zu bytes at %zu past a %zu-byte buffer",
                     len, offset, buf->len);
+    SubmitTimer timer(dev);
     std::lock_guard<std::mutex> lk(dev->host_mu);
     if (int rc = set_device(dev)) return rc;
+    const uint64_t t0 = now_ns();
     hipError_t e = hipMemcpyAsync((char *)buf->ptr + offset, host, len, hipMemcpyHostToDevice,
                                   dev->stream);
     if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync (write)");
     dev->uploads.fetch_add(1);
     dev->upload_bytes.fetch_add(len);
-    e = hipStreamSynchronize(dev->stream);
+    e = fence_wait(dev, dev->stream);
+    dev->transfer_ns.fetch_add(now_ns() - t0);
     return e == hipSuccess ? QVKV_OK : hip_fail(e, "hipStreamSynchronize");
 }
 
@@ -545,10 +616,12 @@ int qvkv_read(qvkv_dev *dev, const qvkv_buf *buf, size_t offset, void *host, siz
     if (offset > buf->len || len > buf->len - offset)
         return fail(QVKV_E_DEVICE, "hip device error: read of %zu bytes at %zu past a %zu-byte buffer",
                     len, offset, buf->len);
+    SubmitTimer timer(dev);
     std::lock_guard<std::mutex> lk(dev->host_mu);
     if (int rc = set_device(dev)) return rc;
-    if (int rc = download(dev, host, (const char *)buf->ptr + offset, len)) return rc;
-    hipError_t e = hipStreamSynchronize(dev->stream);
+    if (int rc = download(dev, host, (const char *)buf->ptr + offset, len, false)) return rc;
+    hipError_t e = fence_wait(dev, dev->stream);
+    take_copy_time(dev);
     return e == hipSuccess ? QVKV_OK : hip_fail(e, "hipStreamSynchronize");
 }
 
@@ -575,6 +648,7 @@ int qvkv_append_async(qvkv_dev *dev, const qvkv_layout *layout, void *pool,
                       uint64_t pool_blocks, const float *k, const float *v,
                       const uint32_t *slots, uint32_t n, void *stream) {
     if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    SubmitTimer timer(dev);
     Geometry g;
     if (int rc = geometry(layout, &g)) return rc;
     if (n == 0) return QVKV_OK;
@@ -593,6 +667,7 @@ int qvkv_gather_async(qvkv_dev *dev, const qvkv_layout *layout, const void *pool
                       uint32_t n_items, uint32_t max_len, uint32_t out_dtype,
                       uint64_t out_positions, void *out_k, void *out_v, void *stream) {
     if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    SubmitTimer timer(dev);
     Geometry g;
     if (int rc = geometry(layout, &g)) return rc;
     if (out_dtype != QVKV_F32 && !(out_dtype == QVKV_F16 && g.dtype == QVKV_F16))
@@ -615,6 +690,7 @@ int qvkv_attention_async(qvkv_dev *dev, const qvkv_layout *layout, const void *p
                          uint32_t n_items, uint32_t heads, uint32_t max_pos, float *out,
                          void *stream) {
     if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    SubmitTimer timer(dev);
     Geometry g;
     if (int rc = geometry(layout, &g)) return rc;
     qvkv::AttnPlan p;
@@ -647,6 +723,7 @@ int qvkv_append_attention_async(qvkv_dev *dev, const qvkv_layout *layout, void *
                                 const uint32_t *table_at, const uint32_t *pos, uint32_t n_items,
                                 uint32_t heads, uint32_t max_pos, float *out, void *stream) {
     if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    SubmitTimer timer(dev);
     Geometry g;
     if (int rc = geometry(layout, &g)) return rc;
     qvkv::AttnPlan p;
@@ -695,6 +772,7 @@ int qvkv_attention_noalloc_async(qvkv_dev *dev, const qvkv_layout *layout, const
                                  uint32_t n_items, uint32_t heads, uint32_t max_pos, float *out,
                                  void *stream) {
     if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    SubmitTimer timer(dev);
     Geometry g;
     if (int rc = geometry(layout, &g)) return rc;
     qvkv::AttnPlan p;
@@ -727,6 +805,7 @@ int qvkv_prefill_attention_async(qvkv_dev *dev, const qvkv_layout *layout, const
                                  uint32_t heads, uint32_t max_pos, uint32_t max_tok, float *out,
                                  void *stream) {
     if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    SubmitTimer timer(dev);
     Geometry g;
     if (int rc = geometry(layout, &g)) return rc;
     const char *why = "";
@@ -748,6 +827,7 @@ int qvkv_block_copy_async(qvkv_dev *dev, const qvkv_layout *layout, void *pool,
                           uint64_t pool_blocks, const uint32_t *src, const uint32_t *dst,
                           uint32_t n, void *stream) {
     if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    SubmitTimer timer(dev);
     Geometry g;
     if (int rc = geometry(layout, &g)) return rc;
     if (n == 0) return QVKV_OK;
@@ -774,6 +854,7 @@ static int pool_of(const qvkv_dev *dev, const qvkv_buf *pool, const Geometry &g,
 int qvkv_append(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *pool, const float *k,
                 const float *v, const uint32_t *slots, uint32_t n) {
     if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    SubmitTimer timer(dev);
     Geometry g;
     if (int rc = geometry(layout, &g)) return rc;
     uint64_t held;
@@ -806,6 +887,7 @@ int qvkv_gather(qvkv_dev *dev, const qvkv_layout *layout, const qvkv_buf *pool,
                 const uint32_t *lens, const uint64_t *out_at, uint32_t n_items,
                 uint32_t out_dtype, uint64_t out_positions, void *out_k, void *out_v) {
     if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    SubmitTimer timer(dev);
     Geometry g;
     if (int rc = geometry(layout, &g)) return rc;
     uint64_t held;
@@ -855,6 +937,7 @@ int qvkv_gather(qvkv_dev *dev, const qvkv_layout *layout, const qvkv_buf *pool,
 
 int qvkv_block_copy(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *pool,
                     const uint32_t *src, const uint32_t *dst, uint32_t n) {
+    SubmitTimer timer(dev);
     return qvkv::block_copy_after(dev, layout, pool, src, dst, n, false, nullptr);
 }
 
@@ -927,6 +1010,7 @@ int qvkv_decode_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *po
                           const float *sync, const uint32_t *sync_to, uint32_t n_sync,
                           const float *k_new, const float *v_new, float *out) {
     if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    SubmitTimer timer(dev);
     Geometry g;
     if (int rc = geometry(layout, &g)) return rc;
     uint64_t held;
@@ -1036,6 +1120,7 @@ static qvkv::PreludeArgs prelude_args(const qvkv_prelude_t *p) {
 int qvkv_prelude_async(qvkv_dev *dev, const qvkv_layout *layout, const qvkv_prelude_t *p,
                        float *q, float *k, float *v, uint32_t s, void *stream) {
     if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    SubmitTimer timer(dev);
     Geometry g;
     if (int rc = geometry(layout, &g)) return rc;
     if (int rc = prelude_shape(g, p)) return rc;
@@ -1054,6 +1139,7 @@ int qvkv_prelude_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *p
                            const float *sync, const uint32_t *sync_to, uint32_t n_sync,
                            float *out, float *k_new, float *v_new) {
     if (!dev) return fail(QVKV_E_SHAPE, "null device");
+    SubmitTimer timer(dev);
     Geometry g;
     if (int rc = geometry(layout, &g)) return rc;
     if (int rc = prelude_shape(g, p)) return rc;

@@ -200,6 +200,7 @@ int qvkv_pool_stats(const qvkv_pool *p, qvkv_pool_stats_t *out) {
     out->cow_copies = p->cow;
     out->evicted_blocks = p->evicted;
     out->moved_blocks = p->moved;
+    out->allocated = p->buf != nullptr;
     return QVKV_OK;
 }
 

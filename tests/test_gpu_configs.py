@@ -281,6 +281,7 @@ def test_cfg4_prefix_sharing_cow_eviction_compaction(hip):
     kids = [pool.fork(parent, PREFIX) for _ in range(S)]
     st = pool.stats()
     assert st["shared_blocks"] == L * (PREFIX // B + 1)
+    assert st["allocated"] == 1  # a device pool holds its memory from creation
     own = [append(kids, [DIV] * S, l) for l in range(L)]
     hip.check()
     st = pool.stats()

@@ -586,3 +586,35 @@ def test_workspace_growth_on_one_stream_does_not_stall_another(hip):
     e = attn_errors(out.cpu().numpy(), want)
     assert e[0] <= MAX_ABS and e[1] <= REL_L2, e
     assert torch.equal(pool_a, pool_b)  # B's append stored the same rows
+
+
+def test_transfer_stats_cover_the_reference_fields(hip):
+    """TransferStats (crates/qubivex-compute/src/discrete.rs:376-405) through qvkv_transfers:
+    a host-memory call stages its inputs (activations_in), copies its output back
+    (activations_out), waits once (fence_waits), and its copies and host time are timed."""
+    from qubivex_amd import KvLayout
+
+    r = np.random.default_rng(8)
+    L = KvLayout("f16", 2, 64, 16)
+    N = 8
+    buf = hip.alloc(N * L.block_bytes)
+    blocks, table_at = random_tables(r, [40], 16, N)
+    k = r.standard_normal((40, L.kv_out)).astype(np.float32)
+    v = r.standard_normal((40, L.kv_out)).astype(np.float32)
+    slots = slots_of(blocks, table_at, 0, np.arange(40), 16)
+    t0 = hip.transfers()
+    hip.append_host(L, buf, k, v, slots)
+    t1 = hip.transfers()
+    assert t1["activations_in"] - t0["activations_in"] >= k.nbytes + v.nbytes + slots.nbytes
+    assert t1["fence_waits"] == t0["fence_waits"] + 1
+    assert t1["transfer_ns"] > t0["transfer_ns"] and t1["submit_ns"] > t0["submit_ns"]
+    out_at = np.zeros(1, np.uint64)
+    hip.gather_host(L, buf, blocks, table_at, [40], out_at, 40)
+    t2 = hip.transfers()
+    assert t2["activations_out"] - t1["activations_out"] == 2 * 40 * L.kv_out * 4
+    assert t2["gpu_busy_ns"] == t2["gpu_ns"] and t2["gpu_ns"] > t1["gpu_ns"]
+    hip.write(buf, 0, b"\0" * 64)
+    t3 = hip.transfers()
+    assert t3["activations_in"] == t2["activations_in"]  # a write is not an activation
+    assert t3["uploads"] == t2["uploads"] + 1 and t3["fence_waits"] == t2["fence_waits"] + 1
+    buf.close()

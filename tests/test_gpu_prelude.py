@@ -83,6 +83,50 @@ def test_prelude_bit_exact(hip, knobs, heads, kvh, d, norm, clip, bias, scale, f
         assert bad.size == 0, f"{name}: {bad.size} of {g.size} differ, first {bad[:3]}: {g[bad[:3]]} vs {w[bad[:3]]}"
 
 
+@pytest.mark.parametrize("fast", [1, 0], ids=["default", "lds_kernel"])
+@pytest.mark.parametrize("norm,heads,kvh,d", [("per_head", 32, 4, 128), ("full", 16, 2, 128),
+                                              ("per_head", 16, 4, 64)])
+def test_prelude_norms_follow_the_reduction_tree(hip, knobs, norm, heads, kvh, d, fast):
+    """Rows whose sum of squares depends on the order of the additions: each head is
+    4096 in one place and +-1 elsewhere, so 2^24 + 1 ties back to 2^24 in a sequential sum
+    while reduce.rs's lane tree keeps the ones together (reduce.rs:14-50, pinned by hand in
+    test_oracle.py).  The kernel's q and k must equal the oracle's bit for bit, and the
+    positive control shows a sequential sum would give a different norm."""
+    from qubivex_amd import KvLayout
+
+    knobs("prelude_fast", int(fast))
+    r = np.random.default_rng(3)
+    L = KvLayout("f16", kvh, d, 16)
+    s = 9
+
+    def crafted(n_heads):
+        x = np.where(r.random((s, n_heads, d)) < 0.5, -1.0, 1.0).astype(np.float32)
+        x[:, :, r.integers(0, d)] = 4096.0
+        return x.reshape(s, n_heads * d)
+
+    q, k = crafted(heads), crafted(kvh)
+    v = r.standard_normal((s, kvh * d)).astype(np.float32)
+    rope = rope_rows(r.integers(0, 9000, s), d)
+    nq = d if norm == "per_head" else heads * d
+    nk = d if norm == "per_head" else kvh * d
+    qn, kn = np.ones(nq, np.float32), np.ones(nk, np.float32)
+    code = {"full": 1, "per_head": 2}[norm]
+    wq, wk, wv = oracle.prelude(q, k, v, heads, kvh, d, rope, None, None, None, None, code, qn,
+                                kn, 1e-6)
+    seg = q[0, :nq]
+    seq = np.float32(0)
+    for x in seg:
+        seq = np.float32(np.float32(x * x) + seq)
+    assert oracle.reduce_dot(seg, seg) != float(seq)  # the input tells the orders apart
+    dq, dk, dv = (torch.from_numpy(x.copy()).cuda() for x in (q, k, v))
+    hip.prelude(L, heads, dq, dk, dv, torch.from_numpy(rope).cuda(), norm=norm, eps=1e-6,
+                q_norm=torch.from_numpy(qn).cuda(), k_norm=torch.from_numpy(kn).cuda())
+    hip.check()
+    for name, got, want in (("q", dq, wq), ("k", dk, wk)):
+        g = got.cpu().numpy().reshape(-1)
+        assert np.array_equal(g.view(np.uint32), want.reshape(-1).view(np.uint32)), name
+
+
 def test_prelude_attention_end_to_end(hip):
     """qvkv_prelude_attention: projection outputs in; post-prelude rows stored after the
     sync rows; attention of the post-prelude q; k_new / v_new back bit for bit."""

@@ -311,6 +311,89 @@ def test_reduce_dot_matches_f64_and_handles_tails():
         assert abs(got - want) <= 1e-5 * max(abs(want), 1.0), (n, got, want)
 
 
+def _lanes(vals, n=64):
+    """A 64-element vector with the given {lane: value}; dot with ones puts each value in
+    its accumulator lane exactly (fma(v, 1, 0) = v)."""
+    w = np.zeros(n, np.float32)
+    for lane, v in vals.items():
+        w[lane] = v
+    return w
+
+
+# Hand-computed pins of reduce.rs:14-50's tree (a[i] += a[i + w] for w = 32, 16, 8, 4, then
+# (a0 + a1) + (a2 + a3)), all in f32 where 1e8 + 1 rounds back to 1e8 (ulp 8) and
+# 2^24 + 1 ties to 2^24.  Each expected value was worked out by hand from that tree; the
+# comment gives what another pairing or order gives instead.
+REDUCE_PINS = [
+    # final stage: (1e8 + 1) + (-1e8 + 1) = 1e8 - 1e8 = 0; sequential 1, (a0+a2)+(a1+a3) 2
+    (_lanes({0: 1e8, 1: 1, 2: -1e8, 3: 1}), 0.0),
+    # stage w pairs lane 0 with w and 1 with w + 1: a0 = 0, a1 = 2, so 2; adjacent pairs
+    # (0 with 1) absorb the ones into +-1e8 and give 0, a sequential sum 1
+    (_lanes({0: 1e8, 1: 1, 32: -1e8, 33: 1}), 2.0),
+    (_lanes({0: 1e8, 1: 1, 16: -1e8, 17: 1}), 2.0),
+    (_lanes({0: 1e8, 1: 1, 8: -1e8, 9: 1}), 2.0),
+    (_lanes({0: 1e8, 1: 1, 4: -1e8, 5: 1}), 2.0),
+    # stage order: w = 32 first adds lane 32 into 0 and 48 into 16, absorbing both ones:
+    # (1e8 + 1) + (-1e8 + 1) = 0; w = 16 first (or a sequential sum) gives 2
+    (_lanes({0: 1e8, 16: -1e8, 32: 1, 48: 1}), 0.0),
+    # all positive (a sum of squares, as in rms_norm): (2^24 + 1) + (1 + 1) = 2^24 + 2;
+    # sequential 2^24 (each 1 ties back to 2^24)
+    (_lanes({0: 2.0 ** 24, 1: 1, 2: 1, 3: 1}), 2.0 ** 24 + 2),
+    # tail of a 65-element vector: element 64 goes to lane 0 (lanes 0..rem): lane 0 =
+    # 1e8 + 1 = 1e8, so (1e8 - 1e8) + (1 + 0) = 1; tail in lane 2 gives 2, sequential 2
+    (np.concatenate([_lanes({0: 1e8, 1: -1e8, 2: 1}), np.float32([1])]), 1.0),
+]
+
+
+@pytest.mark.parametrize("w,want", REDUCE_PINS, ids=range(len(REDUCE_PINS)))
+def test_reduce_dot_tree_order_pinned_by_hand(w, want):
+    got = oracle.reduce_dot(w, np.ones_like(w))
+    assert got == want, (got, want)
+    # the same values split between w and x (w * x, exact products) give the same bits
+    assert oracle.reduce_dot(w * 2, np.full_like(w, 0.5)) == want
+
+
+def test_reduce_dot_pins_reject_other_trees():
+    """Positive control: each plausible wrong reduction (sequential, adjacent pairs,
+    stages in increasing width) misses at least one pin above."""
+    def tree(a, widths, final):
+        a = a.astype(np.float32).copy()
+        for wd in widths:
+            for i in range(wd):
+                a[i] = np.float32(a[i] + a[i + wd])
+        return float(final(a))
+
+    def lanes_of(w):
+        acc = np.zeros(64, np.float32)
+        for i, v in enumerate(w):
+            acc[i % 64] = np.float32(acc[i % 64] + v)
+        return acc
+
+    def seq(w):
+        s = np.float32(0)
+        for v in w:
+            s = np.float32(s + v)
+        return float(s)
+
+    ref_final = lambda a: np.float32(np.float32(a[0] + a[1]) + np.float32(a[2] + a[3]))  # noqa: E731
+    wrong = {
+        "sequential": seq,
+        "increasing widths": lambda w: tree(lanes_of(w), [4, 8, 16, 32], ref_final),
+        "final (a0+a2)+(a1+a3)": lambda w: tree(
+            lanes_of(w), [32, 16, 8, 4],
+            lambda a: np.float32(np.float32(a[0] + a[2]) + np.float32(a[1] + a[3]))),
+        "final sequential": lambda w: tree(
+            lanes_of(w), [32, 16, 8, 4],
+            lambda a: np.float32(np.float32(np.float32(a[0] + a[1]) + a[2]) + a[3])),
+        "down to 1 lane": lambda w: tree(lanes_of(w), [32, 16, 8, 4, 2, 1], lambda a: a[0]),
+    }
+    right = lambda w: tree(lanes_of(w), [32, 16, 8, 4], ref_final)  # noqa: E731
+    for w, want in REDUCE_PINS:
+        assert right(w) == want  # the hand values are the tree's
+    for name, f in wrong.items():
+        assert any(f(w) != want for w, want in REDUCE_PINS), name
+
+
 def test_reduce_dot_shape_is_observable():
     """Positive control: a plain sequential sum gives other bits on some inputs, so a
     kernel that matches the shape bit for bit does follow it."""

@@ -171,6 +171,7 @@ def test_plan_attention_declines_the_layer_a_short_pool_cannot_hold():
     st = p.stats()
     assert (ran, st["full"]) == (steps * (L - 1), steps)
     assert st["synced_rows"] == prompt * (L - 1)  # the prompt, once per layer that ran
+    assert st["allocated"] == 0  # a host-only pool holds no device memory (KvPoolStats)
     p.release(s)
     assert p.stats()["free"] == p.stats()["blocks"]
 

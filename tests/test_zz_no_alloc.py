@@ -55,9 +55,16 @@ def test_noalloc_attention_equals_the_allocating_form(hip, dtype):
         _lib.check(_call(_lib.lib.qvkv_attention_async, hip, L, pool, N, q, t32(blocks),
                          t32(table_at), t32(pos), H, max_pos, want))
         hip.check()
-        _lib.check(_call(_lib.lib.qvkv_attention_noalloc_async, hip, L, pool, N, q, t32(blocks),
-                         t32(table_at), t32(pos), H, max_pos, got))
+        tb, tt, tp = t32(blocks), t32(table_at), t32(pos)
+        torch.cuda.synchronize()
+        u0, (f0, _) = hip.usage(), torch.cuda.mem_get_info()
+        _lib.check(_call(_lib.lib.qvkv_attention_noalloc_async, hip, L, pool, N, q, tb, tt, tp,
+                         H, max_pos, got))
         hip.check()
+        u1, (f1, _) = hip.usage(), torch.cuda.mem_get_info()
+        # nothing allocated: the library's own accounting and the device's free memory
+        assert (u1["used"], u1["peak"]) == (u0["used"], u0["peak"]), (u0, u1)
+        assert f1 == f0, (f0, f1)
         assert torch.isfinite(want).all()
         assert torch.equal(got, want), (n_items, float((got - want).abs().max()))
 
