@@ -702,41 +702,46 @@ def run_cfg1(args, dev):
     kn = torch.randn((NL, G * D), generator=gen, device="cuda")
     ok = torch.empty(NL * (P + T) * G * D, dtype=torch.float16, device="cuda")
     ov = torch.empty_like(ok)
+    # each layer's gathered rows at a fixed stride of P + T positions
+    out_at = torch.arange(NL, dtype=torch.int64, device="cuda") * (P + T)
+    # the step's tables stay on the device: each sync sends only the ids added at block
+    # edges and the positions (one copy, one small kernel)
+    tables = pool.device_tables([s], 0, NL, (P + T) // B + 2)
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(T)]
     t0 = time.perf_counter()
     for step in range(T):
-        # host planning (the runtime's part): every layer's new slot, then the tables
+        # host planning (the runtime's part): every layer's new slot in one call, then the
+        # device tables brought up to date
         sl = pool.plan_append_layers([s], [1], 0, NL)
-        tabs = [pool.tables([s], l) for l in range(NL)]
-        blocks = np.concatenate([t[0] for t in tabs])
-        tat = np.cumsum([0] + [t[0].size for t in tabs[:-1]]).astype(np.uint32)
-        pos = np.concatenate([t[2] for t in tabs]).astype(np.uint32)
-        n = int(pos[0]) + 1
-        d_b, d_t, d_p, d_s, d_l = c32(blocks), c32(tat), c32(pos), c32(sl), c32(pos + 1)
-        out_at = torch.from_numpy((np.arange(NL, dtype=np.int64) * n)).cuda()
+        mp = tables.sync(stream)
         # the device path of one decode step: append, gather and attention of every layer
         # (odd steps: the append inside the attention launch, qvkv_append_attention_async)
         evs[step][0].record(stream)
         if step % 2 == 0:
-            dev.append(L, mem, N, kn, kn, d_s)
-            dev.gather(L, mem, N, d_b, d_t, d_l, out_at, n, ok, ov, "f16")
-            dev.attention(L, mem, N, q, d_b, d_t, d_p, H, int(pos.max()), out)
+            dev.append(L, mem, N, kn, kn, c32(sl))
+            dev.gather(L, mem, N, tables.blocks, tables.table_at, tables.lens, out_at, mp + 1,
+                       ok, ov, "f16")
+            dev.attention(L, mem, N, q, tables.blocks, tables.table_at, tables.pos, H, mp, out)
         else:
-            dev.append_attention(L, mem, N, q, kn, kn, d_b, d_t, d_p, H, int(pos.max()), out)
-            dev.gather(L, mem, N, d_b, d_t, d_l, out_at, n, ok, ov, "f16")
+            dev.append_attention(L, mem, N, q, kn, kn, tables.blocks, tables.table_at,
+                                 tables.pos, H, mp, out)
+            dev.gather(L, mem, N, tables.blocks, tables.table_at, tables.lens, out_at, mp + 1,
+                       ok, ov, "f16")
         evs[step][1].record(stream)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3
     gpu = float(np.mean([a.elapsed_time(b) for a, b in evs[0::2]]))
     gpu_f = float(np.mean([a.elapsed_time(b) for a, b in evs[1::2]]))
     dev.check()
+    tables.close()
     pool.close()
     res = {"prefill_append_ms": prefill_ms, "decode_steps": T, "decode_total_ms": wall,
            "decode_step_us": wall / T * 1e3, "decode_step_device_us": gpu * 1e3,
            "decode_step_fused_device_us": gpu_f * 1e3,
            "note": "latency-bound: per step 16 layers x (append 1 + gather + attention); "
-                   "decode_step_us includes the Python host planning; decode_step_device_us is "
+                   "decode_step_us includes the Python host planning (one all-layer plan call "
+                   "and a sync of device-resident tables per step); decode_step_device_us is "
                    "the three launches from the first to the last (HIP events, even steps), "
                    "decode_step_fused_device_us the two launches with the append inside the "
                    "attention (odd steps); no roofline claim"}

@@ -442,6 +442,34 @@ int qvkv_pool_plan_attention(qvkv_pool *pool, const uint32_t *seqs, const uint32
 int qvkv_pool_tables(const qvkv_pool *pool, const uint32_t *seqs, uint32_t n_seqs,
                      uint32_t layer, uint32_t *blocks_out, uint64_t blocks_cap,
                      uint64_t *n_table_out, uint32_t *table_at_out, uint32_t *pos_out);
+/* qvkv_pool_tables for layers layer0 .. layer0+n_layers-1 in one call: item
+ * (l - layer0) * n_seqs + i is seqs[i] on layer l (the attention_plan of every layer of a
+ * decode step, discrete.rs:951-1009, as one batch). */
+int qvkv_pool_tables_layers(const qvkv_pool *pool, const uint32_t *seqs, uint32_t n_seqs,
+                            uint32_t layer0, uint32_t n_layers, uint32_t *blocks_out,
+                            uint64_t blocks_cap, uint64_t *n_table_out, uint32_t *table_at_out,
+                            uint32_t *pos_out);
+
+/* Device-resident block tables of a fixed batch (no reference counterpart: the reference
+ * rebuilds and uploads its tables every submission, discrete.rs:951-1009).  Items are
+ * (sequence, layer) pairs as in qvkv_pool_tables_layers; item t's table sits at
+ * t * max_blocks of the device `blocks` array (table_at is fixed).  qvkv_tables_sync
+ * brings the device copy up to the pool: only the ids added since the last sync travel (a
+ * table changed in place -- copy-on-write, compaction, release, an epoch restart -- goes
+ * whole), with every item's pos, as one copy and one small kernel on `stream`.  The
+ * device arrays are valid for launches queued on `stream` after the sync.  Not
+ * thread-safe per object; the pool's own calls may run between syncs. */
+typedef struct qvkv_tables qvkv_tables;
+int qvkv_tables_create(qvkv_pool *pool, const uint32_t *seqs, uint32_t n_seqs, uint32_t layer0,
+                       uint32_t n_layers, uint32_t max_blocks, qvkv_tables **out);
+/* *max_pos_out (may be NULL) receives the largest pos: the launches' max_pos. */
+int qvkv_tables_sync(qvkv_tables *tables, void *stream, uint32_t *max_pos_out);
+/* The device arrays: blocks [n_items * max_blocks] (*n_table), table_at, pos and lens
+ * (= pos + 1, the gather's lengths) [n_items]; n_items = n_seqs * n_layers. */
+int qvkv_tables_device(const qvkv_tables *tables, const uint32_t **blocks, uint64_t *n_table,
+                       const uint32_t **table_at, const uint32_t **pos, const uint32_t **lens,
+                       uint32_t *n_items);
+void qvkv_tables_destroy(qvkv_tables *tables);
 /* Releases least-recently-used sequences (PrefixCache::evict_oldest,
  * crates/qubivex-kv-cache/src/lib.rs:197-213; ties: the lower handle) until at least
  * `target_blocks` blocks have returned to the free list or none is left; writes the

@@ -163,6 +163,11 @@ SIGNATURES = {
     "qvkv_pool_tables": (_i32, [_vp, _vp, _u32, _u32, _vp, _u64, _P(_u64), _vp, _vp]),
     "qvkv_pool_plan_attention": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _vp, _u64, _P(_u64), _vp,
                                         _vp, _vp, _vp, _vp, _u64, _P(_u64), _vp]),
+    "qvkv_pool_tables_layers": (_i32, [_vp, _vp, _u32, _u32, _u32, _vp, _u64, _P(_u64), _vp, _vp]),
+    "qvkv_tables_create": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _P(_vp)]),
+    "qvkv_tables_sync": (_i32, [_vp, _vp, _P(_u32)]),
+    "qvkv_tables_device": (_i32, [_vp, _P(_vp), _P(_u64), _P(_vp), _P(_vp), _P(_vp), _P(_u32)]),
+    "qvkv_tables_destroy": (None, [_vp]),
     "qvkv_pool_evict_lru": (_i32, [_vp, _u64, _vp, _u32, _P(_u32)]),
     "qvkv_pool_compact": (_i32, [_vp, _u32, _u64, _P(_u64), _vp]),
     "qvkv_pool_refcount": (_i32, [_vp, _u32, _P(_u32)]),

@@ -232,6 +232,12 @@ int state_of(qvkv_dev *dev, void *stream, StreamState **out) {
     return state_locked(dev, (hipStream_t)stream, out);
 }
 
+}  // namespace
+
+int qvkv::use_device(qvkv_dev *dev) { return set_device(dev); }
+
+namespace {
+
 int geometry(const qvkv_layout *l, Geometry *g) {
     const char *why = "";
     int rc = qvkv::make_geometry(l, g, &why);

@@ -36,6 +36,9 @@ int block_copy_after(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *pool,
                      const uint32_t *src, const uint32_t *dst, uint32_t n, bool ordered,
                      void *after);
 
+// Makes the device of `dev` current on the calling thread (QVKV_OK or QVKV_E_DEVICE).
+int use_device(qvkv_dev *dev);
+
 // Validates a layout and fills the geometry; returns a QVKV_* status and a message.
 int make_geometry(const qvkv_layout *l, Geometry *g, const char **why);
 
@@ -144,5 +147,10 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
 hipError_t launch_slots_at(const Geometry &g, const uint32_t *blocks, uint64_t n_table,
                            const uint32_t *table_at, const uint32_t *pos, uint32_t n_items,
                            uint32_t max_pos, uint32_t *slots, int *err, hipStream_t s);
+
+// Applies a device-tables sync (pool.cpp): pos[i] = staged[i] and lens[i] = staged[i] + 1
+// for i < n_pos, then blocks[staged[n_pos + 2k]] = staged[n_pos + 2k + 1] for k < n_pairs.
+hipError_t launch_table_scatter(const uint32_t *staged, uint32_t n_pos, uint64_t n_pairs,
+                                uint32_t *pos, uint32_t *lens, uint32_t *blocks, hipStream_t s);
 
 }  // namespace qvkv

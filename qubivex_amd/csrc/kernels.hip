@@ -1820,6 +1820,28 @@ __global__ __launch_bounds__(256) void k_slots_at(const uint32_t *__restrict__ b
     slots[i] = slot;
 }
 
+__global__ __launch_bounds__(256) void k_table_scatter(const uint32_t *__restrict__ staged,
+                                                      uint32_t n_pos, uint64_t n_pairs,
+                                                      uint32_t *__restrict__ pos,
+                                                      uint32_t *__restrict__ lens,
+                                                      uint32_t *__restrict__ blocks) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    if (i < n_pos) {
+        pos[i] = staged[i];
+        lens[i] = staged[i] + 1;
+    }
+    if (i < n_pairs) blocks[staged[n_pos + 2 * i]] = staged[n_pos + 2 * i + 1];
+}
+
+hipError_t launch_table_scatter(const uint32_t *staged, uint32_t n_pos, uint64_t n_pairs,
+                                uint32_t *pos, uint32_t *lens, uint32_t *blocks, hipStream_t s) {
+    const uint64_t n = n_pos > n_pairs ? n_pos : n_pairs;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_table_scatter, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, staged,
+                       n_pos, n_pairs, pos, lens, blocks);
+    return hipGetLastError();
+}
+
 hipError_t launch_slots_at(const Geometry &g, const uint32_t *blocks, uint64_t n_table,
                            const uint32_t *table_at, const uint32_t *pos, uint32_t n_items,
                            uint32_t max_pos, uint32_t *slots, int *err, hipStream_t s) {

@@ -47,6 +47,10 @@ struct qvkv_pool {
     std::vector<uint32_t> log_src, log_dst;  // host-only pools: copies issued, in order
     uint64_t clock = 0;
     uint64_t layers = 0, rows = 0, full = 0, cow = 0, evicted = 0, moved = 0;
+    // Bumped by every change to a table other than ids appended at its end (copy-on-write,
+    // release, a new or reused handle, an epoch restart, compaction): device-resident
+    // tables re-send whole tables when it moved (qvkv_tables_sync).
+    uint64_t tab_gen = 0;
     mutable std::mutex mu;
 };
 
@@ -80,6 +84,7 @@ uint32_t new_handle(qvkv_pool *p) {
         p->seqs.emplace_back();
     }
     Seq &s = p->seqs[h];
+    p->tab_gen++;
     s.live = true;
     s.used = ++p->clock;
     s.blocks.assign(p->n_layers, {});
@@ -96,6 +101,7 @@ void unref(qvkv_pool *p, uint32_t b, uint64_t *returned) {
 
 uint64_t release(qvkv_pool *p, uint32_t h) {
     Seq &s = p->seqs[h];
+    p->tab_gen++;
     uint64_t returned = 0;
     for (auto &l : s.blocks) {
         for (uint32_t b : l) unref(p, b, &returned);
@@ -309,6 +315,7 @@ int qvkv_pool_plan_append_layers(qvkv_pool *p, const uint32_t *seqs, const uint3
                 p->refs[nb] = 1;
                 p->refs[old]--;
                 tab[len / B] = nb;
+                p->tab_gen++;
                 src.push_back(old);
                 dst.push_back(nb);
                 p->cow++;
@@ -365,6 +372,7 @@ int qvkv_pool_plan_attention(qvkv_pool *p, const uint32_t *seqs, const uint32_t 
         // A mirror of another epoch (the host cache was cleared or restored) starts again
         // (discrete.rs:975-978): every block back, in table order.
         if (s.epoch != epochs[i]) {
+            p->tab_gen++;
             for (uint32_t l = 0; l < p->n_layers; l++) {
                 for (uint32_t b : s.blocks[l]) unref(p, b, nullptr);
                 s.blocks[l].clear();
@@ -389,6 +397,7 @@ int qvkv_pool_plan_attention(qvkv_pool *p, const uint32_t *seqs, const uint32_t 
                 p->refs[nb] = 1;
                 p->refs[old]--;
                 tab[bi] = nb;
+                p->tab_gen++;
                 src.push_back(old);
                 dst.push_back(nb);
                 p->cow++;
@@ -449,6 +458,32 @@ int qvkv_pool_tables(const qvkv_pool *p, const uint32_t *seqs, uint32_t n_seqs, 
         pos_out[i] = len - 1;
         if (blocks_out) std::copy(s->blocks[layer].begin(), s->blocks[layer].begin() + nb, blocks_out + at);
         at += nb;
+    }
+    *n_table_out = at;
+    return QVKV_OK;
+}
+
+int qvkv_pool_tables_layers(const qvkv_pool *p, const uint32_t *seqs, uint32_t n_seqs,
+                            uint32_t layer0, uint32_t n_layers, uint32_t *blocks_out,
+                            uint64_t blocks_cap, uint64_t *n_table_out, uint32_t *table_at_out,
+                            uint32_t *pos_out) {
+    if (!p || !n_table_out || (n_seqs && n_layers && (!seqs || !table_at_out || !pos_out)))
+        return err(QVKV_E_SHAPE, "shape mismatch in pool: null argument");
+    if (layer0 >= p->n_layers || n_layers > p->n_layers - layer0)
+        return err(QVKV_E_SHAPE, "shape mismatch in pool: no such layer");
+    uint64_t at = 0;
+    for (uint32_t l = 0; l < n_layers; l++) {
+        uint64_t n = 0;
+        if (int rc = qvkv_pool_tables(p, seqs, n_seqs, layer0 + l, blocks_out ? blocks_out + at : nullptr,
+                                      blocks_cap - at, &n, table_at_out + (uint64_t)l * n_seqs,
+                                      pos_out + (uint64_t)l * n_seqs))
+            return rc;
+        for (uint32_t i = 0; i < n_seqs; i++) {
+            const uint64_t t = (uint64_t)table_at_out[(uint64_t)l * n_seqs + i] + at;
+            if (t > 0xffffffffull) return err(QVKV_E_SHAPE, "shape mismatch in pool: table too long");
+            table_at_out[(uint64_t)l * n_seqs + i] = (uint32_t)t;
+        }
+        at += n;
     }
     *n_table_out = at;
     return QVKV_OK;
@@ -574,6 +609,7 @@ int qvkv_pool_compact(qvkv_pool *p, uint32_t mode, uint64_t seed, uint64_t *move
         pending.swap(rest);
     }
     // Tables, reference counts and the free list under the new ids.
+    p->tab_gen++;
     for (auto &s : p->seqs) {
         if (!s.live) continue;
         for (auto &l : s.blocks)
@@ -595,6 +631,176 @@ int qvkv_pool_refcount(const qvkv_pool *p, uint32_t block, uint32_t *out) {
     if (block >= p->n_blocks) return err(QVKV_E_SHAPE, "shape mismatch in pool: no such block");
     *out = p->refs[block];
     return QVKV_OK;
+}
+
+}  // extern "C"
+
+// ---- device-resident block tables (qvkv_tables_*) ----
+
+struct qvkv_tables {
+    qvkv_pool *pool = nullptr;
+    std::vector<uint32_t> seqs;
+    uint32_t layer0 = 0, n_layers = 0, max_blocks = 0, n_items = 0;
+    qvkv_buf *dev_mem = nullptr;  // blocks [n_items * max_blocks] | table_at | pos | lens | staging x2
+    uint32_t *d_blocks = nullptr, *d_table_at = nullptr, *d_pos = nullptr, *d_lens = nullptr;
+    uint32_t *d_stage[2] = {nullptr, nullptr};
+    uint32_t *h_stage[2] = {nullptr, nullptr};  // pinned
+    hipEvent_t done[2] = {nullptr, nullptr};    // after the scatter that read stage k
+    int next = 0;
+    uint64_t stage_words = 0;
+    uint64_t gen = ~0ull;          // the pool's tab_gen at the last sync
+    std::vector<uint32_t> have;    // ids on the device per item
+};
+
+namespace {
+void tables_free(qvkv_tables *t) {
+    for (int k = 0; k < 2; k++) {
+        if (t->done[k]) {
+            (void)hipEventSynchronize(t->done[k]);
+            (void)hipEventDestroy(t->done[k]);
+        }
+        if (t->h_stage[k]) (void)hipHostFree(t->h_stage[k]);
+    }
+    if (t->dev_mem) qvkv_free(t->dev_mem);
+    delete t;
+}
+}  // namespace
+
+extern "C" {
+
+int qvkv_tables_create(qvkv_pool *p, const uint32_t *seqs, uint32_t n_seqs, uint32_t layer0,
+                       uint32_t n_layers, uint32_t max_blocks, qvkv_tables **out) {
+    if (!p || !out || !seqs || !n_seqs || !n_layers || !max_blocks)
+        return err(QVKV_E_SHAPE, "shape mismatch in tables: null argument or empty batch");
+    if (!p->dev) return err(QVKV_E_UNSUPPORTED, "device tables need a device pool");
+    if (layer0 >= p->n_layers || n_layers > p->n_layers - layer0)
+        return err(QVKV_E_SHAPE, "shape mismatch in tables: no such layer");
+    const uint64_t n_items = (uint64_t)n_seqs * n_layers;
+    if (n_items * max_blocks > 0xffffffffull)
+        return err(QVKV_E_SHAPE, "shape mismatch in tables: n_items * max_blocks past 2^32");
+    if (int rc = qvkv::use_device(p->dev)) return rc;
+    auto *t = new qvkv_tables();
+    t->pool = p;
+    t->seqs.assign(seqs, seqs + n_seqs);
+    t->layer0 = layer0;
+    t->n_layers = n_layers;
+    t->max_blocks = max_blocks;
+    t->n_items = (uint32_t)n_items;
+    t->have.assign(n_items, 0);
+    // staging: every pos, then (index, id) pairs -- at most every id of every table
+    t->stage_words = n_items + 2 * n_items * max_blocks;
+    const uint64_t words = n_items * max_blocks + 3 * n_items + 2 * t->stage_words;
+    if (int rc = qvkv_alloc(p->dev, words * 4, &t->dev_mem)) {
+        delete t;
+        return rc;
+    }
+    uint32_t *base = (uint32_t *)qvkv_buf_ptr(t->dev_mem);
+    t->d_blocks = base;
+    t->d_table_at = base + n_items * max_blocks;
+    t->d_pos = t->d_table_at + n_items;
+    t->d_lens = t->d_pos + n_items;
+    t->d_stage[0] = t->d_lens + n_items;
+    t->d_stage[1] = t->d_stage[0] + t->stage_words;
+    for (int k = 0; k < 2; k++) {
+        if (hipHostMalloc((void **)&t->h_stage[k], t->stage_words * 4, hipHostMallocDefault) != hipSuccess ||
+            hipEventCreateWithFlags(&t->done[k], hipEventDisableTiming) != hipSuccess) {
+            (void)hipGetLastError();
+            tables_free(t);
+            return err(QVKV_E_DEVICE, "hip device error: pinned staging for device tables");
+        }
+    }
+    // table_at is fixed: item t at t * max_blocks
+    std::vector<uint32_t> tat(n_items);
+    for (uint64_t i = 0; i < n_items; i++) tat[i] = (uint32_t)(i * max_blocks);
+    if (hipMemcpy(t->d_table_at, tat.data(), n_items * 4, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipGetLastError();
+        tables_free(t);
+        return err(QVKV_E_DEVICE, "hip device error: table_at upload");
+    }
+    *out = t;
+    return QVKV_OK;
+}
+
+int qvkv_tables_sync(qvkv_tables *t, void *stream, uint32_t *max_pos_out) {
+    if (!t) return err(QVKV_E_SHAPE, "shape mismatch in tables: null argument");
+    qvkv_pool *p = t->pool;
+    if (int rc = qvkv::use_device(p->dev)) return rc;
+    const int k = t->next;
+    // the staging pair k was last read by the scatter two syncs ago
+    if (hipEventSynchronize(t->done[k]) != hipSuccess) {
+        (void)hipGetLastError();
+        return err(QVKV_E_DEVICE, "hip device error: device tables staging wait");
+    }
+    uint32_t *h = t->h_stage[k];
+    const uint32_t n_items = t->n_items, B = p->layout.block;
+    uint64_t pairs = 0;
+    uint32_t max_pos = 0;
+    {
+        std::lock_guard<std::mutex> lk(p->mu);
+        const bool whole = t->gen != p->tab_gen;
+        uint32_t *pr = h + n_items;
+        for (uint32_t l = 0; l < t->n_layers; l++)
+            for (uint32_t i = 0; i < (uint32_t)t->seqs.size(); i++) {
+                const uint32_t item = l * (uint32_t)t->seqs.size() + i;
+                const Seq *s = seq_of(p, t->seqs[i]);
+                if (!s) {
+                    t->gen = ~0ull;  // partly walked: resend everything next time
+                    return err(QVKV_E_SHAPE, "shape mismatch in tables: no such sequence");
+                }
+                const uint32_t layer = t->layer0 + l, len = s->len[layer];
+                if (len == 0) {
+                    t->gen = ~0ull;  // partly walked: resend everything next time
+                    return err(QVKV_E_SHAPE, "shape mismatch in tables: a sequence with no positions");
+                }
+                const uint32_t nb = (len + B - 1) / B;
+                if (nb > t->max_blocks) {
+                    t->gen = ~0ull;  // partly walked: resend everything next time
+                    return err(QVKV_E_SHAPE, "shape mismatch in tables: a table past max_blocks");
+                }
+                const uint32_t from = whole ? 0u : std::min(t->have[item], nb);
+                const std::vector<uint32_t> &tab = s->blocks[layer];
+                for (uint32_t b = from; b < nb; b++) {
+                    pr[2 * pairs] = item * t->max_blocks + b;
+                    pr[2 * pairs + 1] = tab[b];
+                    pairs++;
+                }
+                t->have[item] = nb;
+                h[item] = len - 1;
+                max_pos = std::max(max_pos, len - 1);
+            }
+        t->gen = p->tab_gen;
+    }
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = hipMemcpyAsync(t->d_stage[k], h, (n_items + 2 * pairs) * 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess)
+        e = qvkv::launch_table_scatter(t->d_stage[k], n_items, pairs, t->d_pos, t->d_lens,
+                                       t->d_blocks, s);
+    if (e == hipSuccess) e = hipEventRecord(t->done[k], s);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        t->gen = ~0ull;  // resend everything next time
+        return err(QVKV_E_DEVICE, "hip device error: device tables upload");
+    }
+    t->next = 1 - k;
+    if (max_pos_out) *max_pos_out = max_pos;
+    return QVKV_OK;
+}
+
+int qvkv_tables_device(const qvkv_tables *t, const uint32_t **blocks, uint64_t *n_table,
+                       const uint32_t **table_at, const uint32_t **pos, const uint32_t **lens,
+                       uint32_t *n_items) {
+    if (!t) return err(QVKV_E_SHAPE, "shape mismatch in tables: null argument");
+    if (blocks) *blocks = t->d_blocks;
+    if (n_table) *n_table = (uint64_t)t->n_items * t->max_blocks;
+    if (table_at) *table_at = t->d_table_at;
+    if (pos) *pos = t->d_pos;
+    if (lens) *lens = t->d_lens;
+    if (n_items) *n_items = t->n_items;
+    return QVKV_OK;
+}
+
+void qvkv_tables_destroy(qvkv_tables *t) {
+    if (t) tables_free(t);
 }
 
 }  // extern "C"

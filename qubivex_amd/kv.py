@@ -78,13 +78,18 @@ class KvLayout:
 
 
 class DevicePtr:
-    """A raw device address in the shape the bindings take (what `data_ptr()` returns)."""
+    """A raw device address in the shape the bindings take (what `data_ptr()` returns);
+    `n`: its element count, for the entry points that take one (numel())."""
 
-    def __init__(self, address: int):
+    def __init__(self, address: int, n: int = 0):
         self.address = int(address)
+        self.n = int(n)
 
     def data_ptr(self):
         return self.address
+
+    def numel(self):
+        return self.n
 
 
 def _ptr(x):
@@ -557,6 +562,24 @@ class KvPool:
                                    pos.ctypes.data_as(ctypes.c_void_p)))
         return blocks[:n.value], table_at, pos
 
+    def tables_layers(self, seqs, layer0, n_layers):
+        """Every layer's tables in one call: item (l - layer0) * len(seqs) + i."""
+        s, sp = _np(seqs, np.uint32)
+        cap = sum((self.length(int(x), l) + self.layout.block - 1) // self.layout.block
+                  for l in range(layer0, layer0 + n_layers) for x in s)
+        blocks = np.zeros(max(cap, 1), np.uint32)
+        table_at = np.zeros(s.size * n_layers, np.uint32)
+        pos = np.zeros(s.size * n_layers, np.uint32)
+        n = ctypes.c_uint64()
+        check(lib.qvkv_pool_tables_layers(self.handle, sp, s.size, layer0, n_layers,
+                                          blocks.ctypes.data_as(ctypes.c_void_p), blocks.size,
+                                          ctypes.byref(n), table_at.ctypes.data_as(ctypes.c_void_p),
+                                          pos.ctypes.data_as(ctypes.c_void_p)))
+        return blocks[:n.value], table_at, pos
+
+    def device_tables(self, seqs, layer0, n_layers, max_blocks):
+        return DeviceTables(self, seqs, layer0, n_layers, max_blocks)
+
     def evict_lru(self, target_blocks):
         cap = 1 << 16
         out = np.zeros(cap, np.uint32)
@@ -605,6 +628,46 @@ class KvPool:
     def close(self):
         if self.handle:
             lib.qvkv_pool_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        self.close()
+
+
+class DeviceTables:
+    """Device-resident block tables of a fixed batch (qvkv_tables_*): sync() sends only the
+    ids added since the last sync, and the positions; blocks / table_at / pos are device
+    arrays for the kernel entry points (item (l - layer0) * len(seqs) + i)."""
+
+    def __init__(self, pool: KvPool, seqs, layer0, n_layers, max_blocks):
+        self.pool = pool
+        self.handle = None
+        s, sp = _np(seqs, np.uint32)
+        h = ctypes.c_void_p()
+        check(lib.qvkv_tables_create(pool.handle, sp, s.size, layer0, n_layers, max_blocks,
+                                     ctypes.byref(h)))
+        self.handle = h
+        b, t, p, ln = (ctypes.c_void_p() for _ in range(4))
+        nt, ni = ctypes.c_uint64(), ctypes.c_uint32()
+        check(lib.qvkv_tables_device(h, ctypes.byref(b), ctypes.byref(nt), ctypes.byref(t),
+                                     ctypes.byref(p), ctypes.byref(ln), ctypes.byref(ni)))
+        self.n_table, self.n_items = nt.value, ni.value
+        self.blocks = DevicePtr(b.value, self.n_table)
+        self.table_at = DevicePtr(t.value, self.n_items)
+        self.pos = DevicePtr(p.value, self.n_items)
+        self.lens = DevicePtr(ln.value, self.n_items)
+        self.max_pos = 0
+
+    def sync(self, stream=None):
+        """Brings the device arrays up to the pool's tables on `stream`; returns max_pos."""
+        m = ctypes.c_uint32()
+        check(lib.qvkv_tables_sync(self.handle, _stream(stream), ctypes.byref(m)))
+        self.max_pos = m.value
+        return m.value
+
+    def close(self):
+        if self.handle:
+            lib.qvkv_tables_destroy(self.handle)
             self.handle = None
 
     def __del__(self):

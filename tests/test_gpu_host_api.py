@@ -618,3 +618,73 @@ def test_transfer_stats_cover_the_reference_fields(hip):
     assert t3["activations_in"] == t2["activations_in"]  # a write is not an activation
     assert t3["uploads"] == t2["uploads"] + 1 and t3["fence_waits"] == t2["fence_waits"] + 1
     buf.close()
+
+
+def test_device_tables_follow_the_pool(hip):
+    """qvkv_tables_*: after appends that cross block boundaries, a fork whose child's first
+    append copies the shared partial block (copy-on-write: an id changed in place), a
+    release and re-create, and a compaction (every id renamed), the device arrays hold
+    exactly the pool's tables (qvkv_pool_tables_layers) at item * max_blocks, its pos and
+    pos + 1."""
+    import torch
+
+    from qubivex_amd import KvLayout, KvPool
+
+    L = KvLayout("f16", 2, 64, 16)
+    NL, MB = 3, 40
+    pool = KvPool(hip, L, 2000, NL)
+    r = np.random.default_rng(4)
+    seqs = [pool.create() for _ in range(3)]
+    for layer in range(NL):
+        pool.plan_append(seqs, [37, 5, 16], layer)
+    tables = pool.device_tables(seqs, 0, NL, MB)
+    stream = torch.cuda.current_stream()
+
+    def check_mirror():
+        mp = tables.sync(stream)
+        torch.cuda.synchronize()
+        blocks, table_at, pos = pool.tables_layers(seqs, 0, NL)
+        n = tables.n_items
+        dev = np.frombuffer(hip_read(tables.blocks, tables.n_table), np.uint32)
+        dpos = np.frombuffer(hip_read(tables.pos, n), np.uint32)
+        dlen = np.frombuffer(hip_read(tables.lens, n), np.uint32)
+        dtat = np.frombuffer(hip_read(tables.table_at, n), np.uint32)
+        assert dtat.tolist() == [t * MB for t in range(n)]
+        assert dpos.tolist() == pos.tolist() and (dlen == pos + 1).all() and mp == int(pos.max())
+        ends = list(table_at[1:]) + [blocks.size]
+        for t in range(n):
+            mine = blocks[table_at[t]:ends[t]]
+            assert dev[t * MB:t * MB + mine.size].tolist() == mine.tolist(), t
+
+    def hip_read(ptr, n):
+        import ctypes
+
+        rt = ctypes.CDLL("libamdhip64.so.7")  # the HIP runtime already loaded (by soname)
+        host = np.zeros(n, np.uint32)
+        torch.cuda.synchronize()
+        rc = rt.hipMemcpy(ctypes.c_void_p(host.ctypes.data), ctypes.c_void_p(ptr.data_ptr()),
+                          ctypes.c_size_t(n * 4), 2)  # hipMemcpyDeviceToHost
+        assert rc == 0
+        return host.tobytes()
+
+    check_mirror()
+    for step in range(40):  # decode steps: one position per layer, blocks appended at edges
+        for layer in range(NL):
+            pool.plan_append(seqs, [1, 1, 1], layer)
+        check_mirror()
+    kid = pool.fork(seqs[0], int(pool.length(seqs[0], 0)))
+    pool.release(seqs[1])
+    seqs2 = [seqs[0], pool.create(), kid]
+    for layer in range(NL):
+        pool.plan_append(seqs2, [1, 20, 1], layer)  # the kid's append copies the partial block
+    tables.close()
+    tables = pool.device_tables(seqs2, 0, NL, MB)
+    seqs = seqs2
+    check_mirror()
+    for layer in range(NL):
+        pool.plan_append(seqs, [3, 3, 3], layer)
+    check_mirror()
+    pool.compact(mode="fill")
+    check_mirror()
+    tables.close()
+    pool.close()

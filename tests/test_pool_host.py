@@ -101,6 +101,17 @@ def test_tables_follow_attention_plan_restated():
             assert blocks.tolist() == plan["blocks"]
             assert table_at.tolist() == plan["table_at"]
             assert pos.tolist() == plan["pos"]
+        # every layer's tables in one call: the per-layer tables, layer after layer
+        ab, at, ap = p.tables_layers(handles, 0, n_layers)
+        off = 0
+        for layer in range(n_layers):
+            b1, t1, p1 = p.tables(handles, layer)
+            k = len(handles)
+            assert ab[off:off + b1.size].tolist() == b1.tolist()
+            assert (at[layer * k:(layer + 1) * k] - off).tolist() == t1.tolist()
+            assert ap[layer * k:(layer + 1) * k].tolist() == p1.tolist()
+            off += b1.size
+        assert ab.size == off
     assert p.stats()["free"] == len(ref.free)
 
 
