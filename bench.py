@@ -71,6 +71,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--legs", default="append,decode,layers,gather,copy,prefill,prelude")
+    ap.add_argument("--tune", action="append", default=[], metavar="KNOB=VALUE",
+                    help="set a launch-shape knob (qvkv_tune) before running, for A/B runs")
     return ap.parse_args()
 
 
@@ -812,6 +814,13 @@ def main():
     torch.cuda.init()
     dev = HipDevice(0)
     log(f"[bench] {dev.describe()}")
+    if args.tune:
+        from qubivex_amd import kv
+
+        for kvp in args.tune:
+            name, value = kvp.split("=")
+            kv.tune(name, int(value))
+            log(f"[bench] knob {name} = {value}")
     legs = set(args.legs.split(","))
     res, info = run_decode(args.config, args, dev, legs, args.steps, args.warmup,
                            cpu=not args.no_cpu)
