@@ -398,7 +398,7 @@ __device__ __forceinline__ uint32_t split_sel2(float x0, float x1, float c) {
 // n_col: positions this lane's query column sees (causal limit); n_max: the largest n_col
 // of the wave -- rows at or past it may never have been written and are zeroed.
 template <int D, bool Q8, bool PK>
-__device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<D> &st,
+__device__ __forceinline__ void compute_tile(Tile<D, Q8> &t, SoftmaxState<D> &st,
                                              const h4 *qf, uint32_t n_col, uint32_t n_max,
                                              uint32_t qg, bool hi_col, uint32_t sigma) {
     constexpr int NJ = D / 16;
@@ -499,9 +499,7 @@ __device__ __forceinline__ void compute_tile(const Tile<D, Q8> &t, SoftmaxState<
         // v_mul_legacy_f32's 0 * x is 0 for every x, but the tile does not rest on that: in
         // a partial tile (wave-uniform, at most one per unit) those rows' scales and int8
         // values are zeroed before use, as the f16 branch zeroes its value rows.
-        uint32_t vs[Tile<D, Q8>::SW];
-#pragma unroll
-        for (int x = 0; x < Tile<D, Q8>::SW; x++) vs[x] = t.vs[x];
+        uint32_t *vs = t.vs;  // masked in place (the caller's tile is not used again)
         if (partial) {
 #pragma unroll
             for (int i = 0; i < 4; i++)

@@ -1328,6 +1328,44 @@ __device__ __forceinline__ float stream_merge_value(const float *ws, const float
     return O / L;
 }
 
+// The in-kernel merge of a cut unit (k_attn_stream): called by every workgroup holding one
+// of its partials, right after storing it.  Its tiles are the slots [a, b) of the work
+// order (a0: its first set-up slot).  The contributors count their arrival on the unit's
+// counter; the last one merges every partial (in workgroup order, as the merge kernel
+// would) into the unit's nh output heads and sets the counter back to 0 for the next
+// launch.  Every contributor arrives exactly once per launch: no path skips it.
+__device__ __attribute__((noinline)) void stream_arrive(const float *ws, const float *ml,
+                                                        float *out, uint32_t *ctr, uint64_t T,
+                                                        uint32_t P, uint32_t D, uint64_t a0,
+                                                        uint64_t a, uint64_t b, uint32_t nh) {
+    auto owner = [&](uint64_t xx) { return (uint32_t)(((xx + 1) * P + T - 1) / T - 1); };
+    const uint32_t w0 = owner(a), w1 = owner(b - 1);
+    const uint32_t sw0 = (uint64_t)w0 * T / P < a0 ? 1u : 0u;
+    __shared__ uint32_t merge_here;
+    // this workgroup's partial stores (agent-scope atomics) complete before its arrival
+    // counts
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t nc = w1 - w0 + 1;
+        if (T < P) {  // workgroups with empty shares hold no partial
+            nc = 0;
+            for (uint32_t v = w0; v <= w1; v++) nc += (uint64_t)v * T / P != (uint64_t)(v + 1) * T / P;
+        }
+        const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        merge_here = old + 1 == nc;
+    }
+    __syncthreads();
+    if (merge_here) {
+        for (uint32_t idx = threadIdx.x; idx < nh * D; idx += 256u) {
+            const uint32_t hh = idx / D, d = idx - hh * D;
+            out[(uint64_t)hh * D + d] = stream_merge_value<true>(ws, ml, T, P, D, w0, w1, sw0, hh, d);
+        }
+        if (threadIdx.x == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();  // merge_here is read before the next unit's arrival
+}
+
 template <int D, bool Q8, bool NT, bool PK, bool NR>
 __device__ __forceinline__ void attn_stream_body(QV_STREAM_PARAMS) {
     __shared__ uint64_t cum[STREAM_MAX_ITEMS + 1];
@@ -1390,43 +1428,11 @@ __device__ __forceinline__ void attn_stream_body(QV_STREAM_PARAMS) {
                                      tab, t0, t1, ws + slot * 8 * D, D, ml + slot * 8 * 2, 2,
                                      nr);
             if (ctr) {
-                // In-kernel merge: the unit's contributors count their arrival on its
-                // counter; the last one merges every partial (in workgroup order, as the
-                // merge kernel would) and sets the counter back to 0 for the next launch.
-                // Every contributor arrives exactly once per launch: no path skips it.
+                // In-kernel merge of the cut unit (out of line: its registers stay out of the
+                // tile loop's budget)
                 const uint64_t a0 = c0 + (uint64_t)ul * per_unit;
-                auto owner = [&](uint64_t xx) { return (uint32_t)(((xx + 1) * P + T - 1) / T - 1); };
-                const uint32_t w0 = owner(tiles_at), w1 = owner(unit_end - 1);
-                const uint32_t sw0 = (uint64_t)w0 * T / P < a0 ? 1u : 0u;
-                const uint32_t u = item * upi + ul;
-                __shared__ uint32_t merge_here;
-                // this workgroup's partial stores (agent-scope atomics) complete before its
-                // arrival counts
-                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-                __syncthreads();
-                if (threadIdx.x == 0) {
-                    uint32_t nc = w1 - w0 + 1;
-                    if (T < P) {  // workgroups with empty shares hold no partial
-                        nc = 0;
-                        for (uint32_t v = w0; v <= w1; v++)
-                            nc += (uint64_t)v * T / P != (uint64_t)(v + 1) * T / P;
-                    }
-                    const uint32_t old =
-                        __hip_atomic_fetch_add(ctr + u, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    merge_here = old + 1 == nc;
-                }
-                __syncthreads();
-                if (merge_here) {
-                    const uint32_t nh = min(8u, GS - hc * 8);
-                    for (uint32_t idx = threadIdx.x; idx < nh * D; idx += 256u) {
-                        const uint32_t hh = idx / D, d = idx - hh * D;
-                        out[(oh0 + hh) * D + d] =
-                            stream_merge_value<true>(ws, ml, T, P, D, w0, w1, sw0, hh, d);
-                    }
-                    if (threadIdx.x == 0)
-                        __hip_atomic_store(ctr + u, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-                __syncthreads();  // merge_here is read before the next unit's arrival
+                stream_arrive(ws, ml, out + oh0 * D, ctr + item * upi + ul, T, P, D, a0,
+                              tiles_at, unit_end, min(8u, GS - hc * 8));
             }
         }
         first = false;
