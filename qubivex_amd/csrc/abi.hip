@@ -73,8 +73,6 @@ struct StreamState {
     int *d_err = nullptr;  // [0]: latched bits (ERR_*), [1]: taken by the last check
     void *ws = nullptr;    // attention workspace (partials of context chunks)
     uint64_t ws_bytes = 0;
-    uint32_t *ctr = nullptr;  // merge counters of split-by-work launches (0 between launches)
-    uint64_t ctr_units = 0;
     std::mutex check_mu;   // one check at a time per stream
     // The attention launches of this stream, one at a time: the workspace is grown (which
     // waits for this stream to drain) and handed to the launch under it.  Other streams'
@@ -142,10 +140,7 @@ struct qvkv_buf {
 // (the first 256 bytes) and the partial results of split-context launches.  Each GPU
 // holds its own copy for the life of the process; host code reaches it only through
 // the address hipGetSymbolAddress returns for the device (qvkv_dev::scratch).
-// Layout: error flag (256 bytes), the merge counters of split-by-work launches
-// (NOALLOC_CTR units, 0 between launches), then the partials (QVKV_NOALLOC_SCRATCH_BYTES).
-constexpr uint64_t NOALLOC_CTR = 65536;
-static __device__ __align__(256) uint8_t scratch[256 + NOALLOC_CTR * 4 + QVKV_NOALLOC_SCRATCH_BYTES];
+static __device__ __align__(256) uint8_t scratch[QVKV_NOALLOC_SCRATCH_BYTES + 256];
 
 namespace {
 
@@ -201,27 +196,10 @@ int ensure(qvkv_dev *dev, hipStream_t s, void **buf, uint64_t *have, uint64_t ne
     return QVKV_OK;
 }
 
-// The attention workspace of a stream grown for a plan (partials of context chunks), and
-// for a split-by-work plan its merge counters, zeroed when grown (a fill kernel queued
-// before the launch).
+// The attention workspace of a stream grown for a plan (partials of context chunks).
 int ensure_attention(qvkv_dev *dev, StreamState *st, const qvkv::AttnPlan &p) {
-    if (p.ws_bytes)
-        if (int rc = ensure(dev, st->stream, &st->ws, &st->ws_bytes, p.ws_bytes)) return rc;
-    if (p.kind == 2 && p.units > st->ctr_units) {
-        void *buf = st->ctr;
-        uint64_t have = st->ctr_units * 4;
-        if (int rc = ensure(dev, st->stream, &buf, &have, p.units * 4)) return rc;
-        st->ctr = (uint32_t *)buf;
-        st->ctr_units = have / 4;
-        hipError_t e = qvkv::launch_zero(st->ctr, have, st->stream);
-        if (e != hipSuccess) return hip_fail(e, "merge counter fill");
-    }
-    return QVKV_OK;
-}
-
-// The merge counters a launch of plan p passes (null: the separate merge kernel).
-uint32_t *merge_counters(const qvkv::AttnPlan &p, uint32_t *ctr) {
-    return p.kind == 2 && qvkv::tune(qvkv::KNOB_ATTN_STREAM_MERGE) != 0 ? ctr : nullptr;
+    if (!p.ws_bytes) return QVKV_OK;
+    return ensure(dev, st->stream, &st->ws, &st->ws_bytes, p.ws_bytes);
 }
 
 // The state of `stream`, created on first use.  Caller holds dev->mu.
@@ -507,11 +485,6 @@ int qvkv_open(int device, qvkv_dev **out) {
             return hip_fail(e, "hipMemcpy (scratch error flag)");
         }
         d->scratch_err = (int *)d->scratch;
-        // the merge counters start at 0 (each launch leaves them there)
-        if ((e = hipMemset(d->scratch + 256, 0, NOALLOC_CTR * 4)) != hipSuccess) {
-            qvkv_close(d);
-            return hip_fail(e, "hipMemset (scratch merge counters)");
-        }
     }
     *out = d;
     return QVKV_OK;
@@ -524,7 +497,6 @@ void qvkv_close(qvkv_dev *dev) {
     (void)hipDeviceSynchronize();
     for (StreamState *st : dev->streams) {
         dev_free(dev, st->ws, st->ws_bytes);
-        dev_free(dev, st->ctr, st->ctr_units * 4);
         dev_free(dev, st->d_err, 256);
         delete st;
     }
@@ -747,8 +719,7 @@ int qvkv_attention_async(qvkv_dev *dev, const qvkv_layout *layout, const void *p
     if (int rc = ensure_attention(dev, st, p)) return rc;
     return launched(dev, qvkv::launch_attention(g, p, pool, pool_blocks, q, blocks, n_table,
                                                 table_at, pos, n_items, heads, max_pos, out,
-                                                st->ws, st->d_err, st->stream, qvkv::NewRows{},
-                                                merge_counters(p, st->ctr)),
+                                                st->ws, st->d_err, st->stream),
                     "attention launch");
 }
 
@@ -786,8 +757,7 @@ int qvkv_append_attention_async(qvkv_dev *dev, const qvkv_layout *layout, void *
         nr.v = v_new;
         return launched(dev, qvkv::launch_attention(g, p, pool, pool_blocks, q, blocks, n_table,
                                                     table_at, pos, n_items, heads, max_pos, out,
-                                                    st->ws, st->d_err, st->stream, nr,
-                                                    merge_counters(p, st->ctr)),
+                                                    st->ws, st->d_err, st->stream, nr),
                         "append + attention launch");
     }
     uint32_t *slots = (uint32_t *)((uint8_t *)st->ws + slots_at);
@@ -798,8 +768,7 @@ int qvkv_append_attention_async(qvkv_dev *dev, const qvkv_layout *layout, void *
                                 st->stream);
     if (e == hipSuccess)
         e = qvkv::launch_attention(g, p, pool, pool_blocks, q, blocks, n_table, table_at, pos,
-                                   n_items, heads, max_pos, out, st->ws, st->d_err, st->stream,
-                                   qvkv::NewRows{}, merge_counters(p, st->ctr));
+                                   n_items, heads, max_pos, out, st->ws, st->d_err, st->stream);
     return launched(dev, e, "append + attention launch");
 }
 
@@ -829,12 +798,8 @@ int qvkv_attention_noalloc_async(qvkv_dev *dev, const qvkv_layout *layout, const
     if (int rc = set_device(dev)) return rc;
     return launched(dev, qvkv::launch_attention(g, p, pool, pool_blocks, q, blocks, n_table,
                                                 table_at, pos, n_items, heads, max_pos, out,
-                                                dev->scratch + 256 + NOALLOC_CTR * 4,
-                                                dev->scratch_err, (hipStream_t)stream,
-                                                qvkv::NewRows{},
-                                                p.units <= NOALLOC_CTR
-                                                    ? merge_counters(p, (uint32_t *)(dev->scratch + 256))
-                                                    : nullptr),
+                                                dev->scratch + 256, dev->scratch_err,
+                                                (hipStream_t)stream),
                     "attention launch");
 }
 
@@ -1038,8 +1003,7 @@ hipError_t attend_tokens(qvkv_dev *dev, const Geometry &g, const qvkv::AttnPlan 
                                     (uint32_t)sg.n_tok.size(), heads, max_pos, sg.max_tok, s,
                                     dout, dev->own->d_err, dev->stream, f16_values);
     return qvkv::launch_attention(g, plan, pool, held, dq, dblocks, n_table, dtable_at, dpos, s,
-                                  heads, max_pos, dout, dev->own->ws, dev->own->d_err, dev->stream,
-                                  qvkv::NewRows{}, merge_counters(plan, dev->own->ctr));
+                                  heads, max_pos, dout, dev->own->ws, dev->own->d_err, dev->stream);
 }
 
 }  // namespace

@@ -230,6 +230,16 @@ __device__ __forceinline__ float mul_legacy(float a, float b) {
     asm("s_nop 0\n\tv_mul_legacy_f32 %0, %1, %2" : "=v"(y) : "v"(a), "v"(b));
     return y;
 }
+// Four of them in one block behind one wait state.
+__device__ __forceinline__ void mul_legacy4(const float a[4], const float b[4], float y[4]) {
+    asm("s_nop 0\n\t"
+        "v_mul_legacy_f32 %0, %4, %8\n\t"
+        "v_mul_legacy_f32 %1, %5, %9\n\t"
+        "v_mul_legacy_f32 %2, %6, %10\n\t"
+        "v_mul_legacy_f32 %3, %7, %11"
+        : "=&v"(y[0]), "=&v"(y[1]), "=&v"(y[2]), "=&v"(y[3])
+        : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]));
+}
 
 __device__ __forceinline__ _Float16 split_part(float x, bool hi_part) {
     const _Float16 hi = (_Float16)x;
@@ -515,8 +525,7 @@ __device__ __forceinline__ void compute_tile(Tile<D, Q8> &t, SoftmaxState<D> &st
         // high part u of x = p * scale, or the residual x - u.
         auto scaled = [&](float sc_of_row[4]) {
             float x[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) x[i] = mul_legacy(pr[i], sc_of_row[i]);
+            mul_legacy4(pr, sc_of_row, x);
             const uint32_t a = split_sel2(x[0], x[1], neg_lo), b = split_sel2(x[2], x[3], neg_lo);
             return __builtin_bit_cast(h4, u2v{a, b});
         };

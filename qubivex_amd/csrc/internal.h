@@ -72,7 +72,6 @@ struct AttnPlan {
     uint32_t tpc;       // 16-position tiles per chunk
     uint64_t ws_bytes;  // workspace for partial results (0 when n_chunks == 1)
     uint32_t ucost;     // kind 2: a unit's set-up cost in tiles (its share of the split)
-    uint64_t units;     // kind 2: units of the launch (one merge counter each, in-kernel merge)
 };
 int plan_attention(const Geometry &g, uint32_t n_items, uint32_t heads, uint32_t max_pos,
                    AttnPlan *p, const char **why);
@@ -94,7 +93,6 @@ int plan_attention(const Geometry &g, uint32_t n_items, uint32_t heads, uint32_t
     X(ATTN_FULL, "attn_full", 512)              /* units from which a launch runs unsplit */    \
     X(ATTN_STREAM, "attn_stream", 1)            /* 1: split by work, 0: context chunks */       \
     X(ATTN_STREAM_WG, "attn_stream_wg", 768)                                                    \
-    X(ATTN_STREAM_MERGE, "attn_stream_merge", 1) /* 1: merge cut units in-kernel, 0: kernel */ \
     X(STREAM_UNIT_COST, "stream_unit_cost", 8)  /* a unit's set-up cost in tiles */             \
     X(ATTN_TARGET, "attn_target", 1536)         /* context-chunk split: workgroups aimed at */  \
     X(FUSED_Q8, "fused_q8", 1)                  /* fused append + attention for q8_0 */         \
@@ -143,11 +141,7 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
                             uint64_t pool_blocks, const float *q, const uint32_t *blocks,
                             uint64_t n_table, const uint32_t *table_at, const uint32_t *pos,
                             uint32_t n_items, uint32_t heads, uint32_t max_pos, float *out,
-                            void *ws, int *err, hipStream_t s, NewRows nr = NewRows{},
-                            uint32_t *ctr = nullptr);
-// Fills n bytes (a multiple of 4) of device memory with zeros on stream s (a kernel, so a
-// captured graph holds no memset node).
-hipError_t launch_zero(void *p, uint64_t n, hipStream_t s);
+                            void *ws, int *err, hipStream_t s, NewRows nr = NewRows{});
 // Each item's pool slot of position pos[i] (block * B + offset), for the append of the
 // unfused form; an item past max_pos or its table gets slot 0xffffffff (flagged).
 hipError_t launch_slots_at(const Geometry &g, const uint32_t *blocks, uint64_t n_table,

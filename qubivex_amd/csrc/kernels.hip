@@ -882,15 +882,6 @@ __global__ __launch_bounds__(T) void k_block_copy(uint8_t *__restrict__ pool,
     pool, pool_blocks, q, blocks, n_table, table_at, pos, n_items, H, max_pos, out, ws, hc_n,   \
         n_chunks, tpc, geo, err, nr
 
-// Agent-scope relaxed atomic store and load of one float: global_store / global_load with
-// sc1, coherent across XCDs per location without fences.
-__device__ __forceinline__ void st_agent(float *p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_agent(const float *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 template <int D, bool Q8, bool NT, bool PK, bool NR, bool IDS = false>
 __device__ __forceinline__ void attn_body(QV_ATTN_PARAMS);
 template <int D, bool Q8, bool NT, bool PK, bool NR, bool IDS = false>
@@ -1162,13 +1153,10 @@ __device__ __forceinline__ void attn_unit(const uint8_t *__restrict__ pool, uint
         if (!ml_base) {
             o_base[hh * o_stride + d] = O / L;
         } else {
-            // Partials are stored as agent-scope relaxed atomics (global_store ... sc1), each
-            // coherent across the XCDs' L2s by itself: a workgroup on another XCD may merge
-            // them in this launch (k_attn_stream's in-kernel merge) with no cache flush.
-            st_agent(o_base + hh * o_stride + d, O);
+            o_base[hh * o_stride + d] = O;
             if (d == 0) {
-                st_agent(ml_base + hh * ml_stride, M);
-                st_agent(ml_base + hh * ml_stride + 1, L);
+                ml_base[hh * ml_stride] = M;
+                ml_base[hh * ml_stride + 1] = L;
             }
         }
     }
@@ -1264,106 +1252,13 @@ __device__ __forceinline__ uint32_t stream_item(const uint64_t *cum, uint32_t n_
         const uint32_t *__restrict__ blocks, uint64_t n_table,                                  \
         const uint32_t *__restrict__ table_at, const uint32_t *__restrict__ pos,                \
         uint32_t n_items, uint32_t H, uint32_t max_pos, float *__restrict__ out,                \
-        float *__restrict__ ws, uint32_t hc_n, uint32_t ucost, Geo geo, int *err, NewRows nr,  \
-        uint32_t *__restrict__ ctr
+        float *__restrict__ ws, uint32_t hc_n, uint32_t ucost, Geo geo, int *err, NewRows nr
 
 // A value every lane holds alike, moved to scalar registers.
 __device__ __forceinline__ uint32_t uni(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
 __device__ __forceinline__ uint64_t uni(uint64_t v) {
     return (uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32)) << 32 |
            __builtin_amdgcn_readfirstlane((uint32_t)v);
-}
-
-// A cut unit's result from its partials: workgroups w0 .. w1 of P each left one in slot 0
-// (w0: slot s0) unless their share is empty; combined in workgroup order, so the bits do
-// not depend on which workgroup or kernel merges.  Head hh of the unit, value d.  AGENT:
-// read the partials with agent-scope loads (a merge inside the launch that wrote them).
-template <bool AGENT>
-__device__ __forceinline__ float stream_merge_value(const float *ws, const float *ml, uint64_t T,
-                                                    uint32_t P, uint32_t D, uint32_t w0,
-                                                    uint32_t w1, uint32_t s0, uint32_t hh,
-                                                    uint32_t d) {
-    auto ld = [](const float *p) { return AGENT ? ld_agent(p) : *p; };
-    // Workgroups with an empty range (only when there are fewer tiles than workgroups)
-    // hold no partial.
-    auto empty = [&](uint32_t w) {
-        return T < P && (uint64_t)w * T / P == (uint64_t)(w + 1) * T / P;
-    };
-    auto slot_of = [&](uint32_t w) { return 2ull * w + (w == w0 ? s0 : 0u); };
-    // The partials are read 4 workgroups at a time, every load of a group issued before
-    // any is used (one memory round trip per group instead of one per partial).
-    float M = -INFINITY;
-    for (uint32_t wb = w0; wb <= w1; wb += 4) {
-        float mc[4];
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const uint32_t w = wb + k;
-            mc[k] = w <= w1 && !empty(w) ? ld(ml + (slot_of(w) * 8 + hh) * 2) : -INFINITY;
-        }
-#pragma unroll
-        for (int k = 0; k < 4; k++) M = fmaxf(M, mc[k]);
-    }
-    const float Ms = M == -INFINITY ? 0.0f : M;
-    float L = 0.0f, O = 0.0f;
-    for (uint32_t wb = w0; wb <= w1; wb += 4) {
-        float mc[4], lc[4], oc[4];
-        bool live[4];
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const uint32_t w = wb + k;
-            live[k] = w <= w1 && !empty(w);
-            const uint64_t slot = live[k] ? slot_of(w) : 0u;
-            mc[k] = live[k] ? ld(ml + (slot * 8 + hh) * 2) : -INFINITY;
-            lc[k] = live[k] ? ld(ml + (slot * 8 + hh) * 2 + 1) : 0.0f;
-            oc[k] = live[k] ? ld(ws + (slot * 8 + hh) * D + d) : 0.0f;
-        }
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            if (!live[k]) continue;
-            const float f = mc[k] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mc[k] - Ms);
-            L = fmaf(lc[k], f, L);
-            O = fmaf(oc[k], f, O);
-        }
-    }
-    return O / L;
-}
-
-// The in-kernel merge of a cut unit (k_attn_stream): called by every workgroup holding one
-// of its partials, right after storing it.  Its tiles are the slots [a, b) of the work
-// order (a0: its first set-up slot).  The contributors count their arrival on the unit's
-// counter; the last one merges every partial (in workgroup order, as the merge kernel
-// would) into the unit's nh output heads and sets the counter back to 0 for the next
-// launch.  Every contributor arrives exactly once per launch: no path skips it.
-__device__ __attribute__((noinline)) void stream_arrive(const float *ws, const float *ml,
-                                                        float *out, uint32_t *ctr, uint64_t T,
-                                                        uint32_t P, uint32_t D, uint64_t a0,
-                                                        uint64_t a, uint64_t b, uint32_t nh) {
-    auto owner = [&](uint64_t xx) { return (uint32_t)(((xx + 1) * P + T - 1) / T - 1); };
-    const uint32_t w0 = owner(a), w1 = owner(b - 1);
-    const uint32_t sw0 = (uint64_t)w0 * T / P < a0 ? 1u : 0u;
-    __shared__ uint32_t merge_here;
-    // this workgroup's partial stores (agent-scope atomics) complete before its arrival
-    // counts
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t nc = w1 - w0 + 1;
-        if (T < P) {  // workgroups with empty shares hold no partial
-            nc = 0;
-            for (uint32_t v = w0; v <= w1; v++) nc += (uint64_t)v * T / P != (uint64_t)(v + 1) * T / P;
-        }
-        const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        merge_here = old + 1 == nc;
-    }
-    __syncthreads();
-    if (merge_here) {
-        for (uint32_t idx = threadIdx.x; idx < nh * D; idx += 256u) {
-            const uint32_t hh = idx / D, d = idx - hh * D;
-            out[(uint64_t)hh * D + d] = stream_merge_value<true>(ws, ml, T, P, D, w0, w1, sw0, hh, d);
-        }
-        if (threadIdx.x == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();  // merge_here is read before the next unit's arrival
 }
 
 template <int D, bool Q8, bool NT, bool PK, bool NR>
@@ -1377,7 +1272,7 @@ __device__ __forceinline__ void attn_stream_body(QV_STREAM_PARAMS) {
     const uint32_t P = gridDim.x, w = blockIdx.x;
     const uint64_t s0 = (uint64_t)w * T / P, s1 = (uint64_t)(w + 1) * T / P;
     float *ml = ws + (uint64_t)P * 2 * 8 * D;
-    if (w == 0 && !ctr) {  // the prefix sums and the units' records, for the merge kernel
+    if (w == 0) {  // the prefix sums and the units' records, for the merge
         uint64_t *wc = (uint64_t *)(ml + (uint64_t)P * 2 * 8 * 2);
         for (uint32_t i = threadIdx.x; i <= n_items; i += 256) wc[i] = cum[i];
         StreamRec *rec = (StreamRec *)((uint8_t *)ws + stream_rec_at(P, D, n_items));
@@ -1427,13 +1322,6 @@ __device__ __forceinline__ void attn_stream_body(QV_STREAM_PARAMS) {
             attn_unit<D, Q8, NT, PK, NR>(pool, pool_blocks, q, blocks, H, geo, err, item, g, hc, n,
                                      tab, t0, t1, ws + slot * 8 * D, D, ml + slot * 8 * 2, 2,
                                      nr);
-            if (ctr) {
-                // In-kernel merge of the cut unit (out of line: its registers stay out of the
-                // tile loop's budget)
-                const uint64_t a0 = c0 + (uint64_t)ul * per_unit;
-                stream_arrive(ws, ml, out + oh0 * D, ctr + item * upi + ul, T, P, D, a0,
-                              tiles_at, unit_end, min(8u, GS - hc * 8));
-            }
         }
         first = false;
         x = seg_end;
@@ -1443,20 +1331,20 @@ __device__ __forceinline__ void attn_stream_body(QV_STREAM_PARAMS) {
 template <int D, bool Q8, bool NT, bool PK>
 __global__ __launch_bounds__(256) void k_attn_stream(QV_STREAM_PARAMS) {
     attn_stream_body<D, Q8, NT, PK, false>(pool, pool_blocks, q, blocks, n_table, table_at, pos, n_items,
-                                    H, max_pos, out, ws, hc_n, ucost, geo, err, nr, ctr);
+                                    H, max_pos, out, ws, hc_n, ucost, geo, err, nr);
 }
 template <int D, bool Q8, bool NT, bool PK, int W>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W)))
 void k_attn_stream_w(QV_STREAM_PARAMS) {
     attn_stream_body<D, Q8, NT, PK, false>(pool, pool_blocks, q, blocks, n_table, table_at, pos, n_items,
-                                    H, max_pos, out, ws, hc_n, ucost, geo, err, nr, ctr);
+                                    H, max_pos, out, ws, hc_n, ucost, geo, err, nr);
 }
 template <int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 3)))
 void k_attn_stream_nr(QV_STREAM_PARAMS) {
     attn_stream_body<D, false, true, false, true>(pool, pool_blocks, q, blocks, n_table,
                                                   table_at, pos, n_items, H, max_pos, out, ws,
-                                                  hc_n, ucost, geo, err, nr, ctr);
+                                                  hc_n, ucost, geo, err, nr);
 }
 // (3 waves/SIMD at d = 128: at the plain stream kernel's 4 its registers spill.  Its q8_0
 // tile code is the 4-wave builds' source; the 3-wave builds' wrong outputs were the
@@ -1466,7 +1354,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 
 void k_attn_stream_q8nr(QV_STREAM_PARAMS) {
     attn_stream_body<D, true, true, PK, true>(pool, pool_blocks, q, blocks, n_table, table_at,
                                               pos, n_items, H, max_pos, out, ws, hc_n, ucost, geo,
-                                              err, nr, ctr);
+                                              err, nr);
 }
 
 // Merge for k_attn_stream: block = one (item, query head), D threads.  The unit's
@@ -1492,8 +1380,51 @@ __global__ __launch_bounds__(256) void k_attn_stream_merge(const float *__restri
     const uint64_t T = cum[n_items];  // (loaded beside the record, not after it)
     const uint32_t w0 = r.w0, w1 = r.w1;
     if (w0 == w1) return;
-    for (uint32_t d = threadIdx.x; d < D; d += blockDim.x)
-        out[(uint64_t)oh * D + d] = stream_merge_value<false>(ws, ml, T, P, D, w0, w1, r.s0, hh, d);
+    // Workgroups with an empty range (only when there are fewer tiles than workgroups)
+    // hold no partial.
+    auto empty = [&](uint32_t w) {
+        return T < P && (uint64_t)w * T / P == (uint64_t)(w + 1) * T / P;
+    };
+    // The unit's partials are read 4 workgroups at a time, every load of a group issued
+    // before any is used (one memory round trip per group instead of one per partial);
+    // they are combined in workgroup order.
+    auto slot_of = [&](uint32_t w) { return 2ull * w + (w == w0 ? r.s0 : 0u); };
+    float M = -INFINITY;
+    for (uint32_t wb = w0; wb <= w1; wb += 4) {
+        float mc[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t w = wb + k;
+            mc[k] = w <= w1 && !empty(w) ? ml[(slot_of(w) * 8 + hh) * 2] : -INFINITY;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) M = fmaxf(M, mc[k]);
+    }
+    const float Ms = M == -INFINITY ? 0.0f : M;
+    for (uint32_t d = threadIdx.x; d < D; d += blockDim.x) {
+        float L = 0.0f, O = 0.0f;
+        for (uint32_t wb = w0; wb <= w1; wb += 4) {
+            float mc[4], lc[4], oc[4];
+            bool live[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t w = wb + k;
+                live[k] = w <= w1 && !empty(w);
+                const uint64_t slot = live[k] ? slot_of(w) : 0u;
+                mc[k] = live[k] ? ml[(slot * 8 + hh) * 2] : -INFINITY;
+                lc[k] = live[k] ? ml[(slot * 8 + hh) * 2 + 1] : 0.0f;
+                oc[k] = live[k] ? ws[(slot * 8 + hh) * D + d] : 0.0f;
+            }
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                if (!live[k]) continue;
+                const float f = mc[k] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mc[k] - Ms);
+                L = fmaf(lc[k], f, L);
+                O = fmaf(oc[k], f, O);
+            }
+        }
+        out[(uint64_t)oh * D + d] = O / L;
+    }
 }
 
 // Merge of context-chunk partials: block = one (item, query head), D threads.
@@ -1822,7 +1753,6 @@ int plan_attention(const Geometry &g, uint32_t n_items, uint32_t heads, uint32_t
     p->tpc = 0;
     p->ws_bytes = 0;
     p->ucost = 0;
-    p->units = 0;
     if (!mfma) {
         if ((uint64_t)n_items * heads > 0x7fffffffull) { *why = "batch too large"; return QVKV_E_SHAPE; }
         return QVKV_OK;
@@ -1850,7 +1780,6 @@ int plan_attention(const Geometry &g, uint32_t n_items, uint32_t heads, uint32_t
         // workgroups that start several short units (cfg2-like layer of 32 ragged items:
         // 64.2 -> 60.1 us; contexts / 8: 31.7 -> 22.0 us; 4-24 within 2 % of 8).
         p->ucost = (uint32_t)tune(KNOB_STREAM_UNIT_COST);
-        p->units = units;
         p->ws_bytes = stream_rec_at(wgs, g.D, n_items) +
                       (uint64_t)n_items * g.G * p->hc * sizeof(StreamRec);
         return QVKV_OK;
@@ -1913,19 +1842,6 @@ hipError_t launch_table_scatter(const uint32_t *staged, uint32_t n_pos, uint64_t
     return hipGetLastError();
 }
 
-__global__ __launch_bounds__(256) void k_zero(uint32_t *__restrict__ p, uint64_t n) {
-    for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256u)
-        p[i] = 0u;
-}
-
-hipError_t launch_zero(void *p, uint64_t n, hipStream_t s) {
-    const uint64_t words = n / 4;
-    if (words == 0) return hipSuccess;
-    const uint64_t wgs = (words + 255) / 256 < 2048 ? (words + 255) / 256 : 2048;
-    hipLaunchKernelGGL(k_zero, dim3((unsigned)wgs), dim3(256), 0, s, (uint32_t *)p, words);
-    return hipGetLastError();
-}
-
 hipError_t launch_slots_at(const Geometry &g, const uint32_t *blocks, uint64_t n_table,
                            const uint32_t *table_at, const uint32_t *pos, uint32_t n_items,
                            uint32_t max_pos, uint32_t *slots, int *err, hipStream_t s) {
@@ -1939,7 +1855,7 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
                             uint64_t pool_blocks, const float *q, const uint32_t *blocks,
                             uint64_t n_table, const uint32_t *table_at, const uint32_t *pos,
                             uint32_t n_items, uint32_t heads, uint32_t max_pos, float *out,
-                            void *ws, int *err, hipStream_t s, NewRows nr, uint32_t *ctr) {
+                            void *ws, int *err, hipStream_t s, NewRows nr) {
     if (n_items == 0) return hipSuccess;
     const Geo geo = to_geo(g);
     const uint8_t *pp = (const uint8_t *)pool;
@@ -1968,19 +1884,19 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
 #define QV_AS(DD, QQ, PK)                                                                       \
     hipLaunchKernelGGL((k_attn_stream<DD, QQ, true, PK>), dim3(P), dim3(256), 0, s, pp,          \
                        pool_blocks, q, blocks, n_table, table_at, pos, n_items, heads, max_pos,  \
-                       out, wsf, p.hc, p.ucost, geo, err, nr, ctr)
+                       out, wsf, p.hc, p.ucost, geo, err, nr)
 #define QV_AS_NR(DD)                                                                            \
     hipLaunchKernelGGL((k_attn_stream_nr<DD>), dim3(P), dim3(256), 0, s,                        \
                        pp, pool_blocks, q, blocks, n_table, table_at, pos, n_items, heads,      \
-                       max_pos, out, wsf, p.hc, p.ucost, geo, err, nr, ctr)
+                       max_pos, out, wsf, p.hc, p.ucost, geo, err, nr)
 #define QV_AS_W4(DD, QQ, PK)                                                                    \
     hipLaunchKernelGGL((k_attn_stream_w<DD, QQ, true, PK, 4>), dim3(P), dim3(256), 0, s, pp,     \
                        pool_blocks, q, blocks, n_table, table_at, pos, n_items, heads, max_pos,  \
-                       out, wsf, p.hc, p.ucost, geo, err, nr, ctr)
+                       out, wsf, p.hc, p.ucost, geo, err, nr)
 #define QV_AS_Q8NR(DD, PK)                                                                      \
     hipLaunchKernelGGL((k_attn_stream_q8nr<DD, PK>), dim3(P), dim3(256), 0, s, pp, pool_blocks,  \
                        q, blocks, n_table, table_at, pos, n_items, heads, max_pos, out, wsf,    \
-                       p.hc, p.ucost, geo, err, nr, ctr)
+                       p.hc, p.ucost, geo, err, nr)
         if (q8 && nr.k) {
             if (g.D == 64) { if (pk) QV_AS_Q8NR(64, true); else QV_AS_Q8NR(64, false); }
             else if (g.D == 128) { if (pk) QV_AS_Q8NR(128, true); else QV_AS_Q8NR(128, false); }
@@ -2007,7 +1923,7 @@ hipError_t launch_attention(const Geometry &g, const AttnPlan &p, const void *po
 #undef QV_AS_W4
 #undef QV_AS
         hipError_t e = hipGetLastError();
-        if (e != hipSuccess || ctr) return e;  // ctr: merged inside the kernel
+        if (e != hipSuccess) return e;
         hipLaunchKernelGGL(k_attn_stream_merge, dim3(n_items * heads), dim3(g.D), 0, s,
                            (const float *)ws, n_items, heads, (uint32_t)g.G, p.hc, P,
                            (uint32_t)g.D, out);

@@ -5,8 +5,7 @@ each unit holds `cost` set-up slots (its per-unit overhead, no tiles) and then o
 tile; a unit whose tiles lie wholly inside one range is written out directly, a unit cut
 by range boundaries leaves one partial per workgroup whose range holds some of its tiles,
 in slot 0 (the workgroup's first unit with tiles) or 1 (its last); the merge finds them
-from the unit's range alone (or, merged in the kernel, the last of its contributors to
-count its arrival merges them).  Every unit's
+from the unit's range alone.  Every unit's
 tiles must be covered exactly once and the merge must read exactly the slots that were
 written (a partial read from a workgroup with an empty range would be garbage)."""
 import random
@@ -55,18 +54,6 @@ def merge_reads(cum, T, P, item, ul, upi, cost=0):
             for w in range(w0, w1 + 1) if w * T // P != (w + 1) * T // P}
 
 
-def arrivals(cum, T, P, item, ul, upi, cost=0):
-    """k_attn_stream's count of a cut unit's contributors: workgroups w0 .. w1 owning its
-    first and last tile, those with an empty range left out (only when T < P)."""
-    per = (cum[item + 1] - cum[item]) // upi
-    a0 = cum[item] + ul * per
-    owner = lambda x: ((x + 1) * P + T - 1) // T - 1  # noqa: E731
-    w0, w1 = owner(a0 + cost), owner(a0 + per - 1)
-    if T >= P:
-        return w1 - w0 + 1
-    return sum(v * T // P != (v + 1) * T // P for v in range(w0, w1 + 1))
-
-
 @pytest.mark.parametrize("cost", [0, 1, 6, 40])
 @pytest.mark.parametrize("seed", range(6))
 def test_every_tile_once_and_the_merge_reads_what_was_written(seed, cost):
@@ -88,11 +75,6 @@ def test_every_tile_once_and_the_merge_reads_what_was_written(seed, cost):
                 else:
                     assert all(k == "part" for k, *_ in got)
                     assert reads == {s for _, s, _, _ in got}
-                    # the in-kernel merge: the arrivals the last contributor waits for
-                    # (w1 - w0 + 1, less empty ranges) are exactly the partials written, one
-                    # per workgroup
-                    assert arrivals(cum, T, P, item, ul, upi, cost) == len(got)
-                    assert len({s // 2 for _, s, _, _ in got}) == len(got)
 
 
 def test_the_check_catches_reads_from_empty_workgroups():

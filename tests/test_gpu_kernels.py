@@ -258,7 +258,7 @@ SWITCH_CASES = [ATTN_CASES[i] for i in (0, 1, 8, 9)] + ATTN_CASES[-4:]
                                  {"attn_pack": "0"},
                                  {"attn_xcd": "0"}, {"attn_ids_below": "0"},
                                  {"stream_unit_cost": "0"}, {"stream_unit_cost": "40"},
-                                 {"attn_stream": "0"}, {"attn_stream_merge": "0"}],
+                                 {"attn_stream": "0"}],
                          ids=lambda e: ",".join(f"{k}={v}" for k, v in e.items()))
 @pytest.mark.parametrize("dtype,H,G,D,lens", SWITCH_CASES)
 def test_attention_launch_switches_stay_within_tolerance(hip, dtype, H, G, D, lens, env,
