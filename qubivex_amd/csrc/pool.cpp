@@ -512,6 +512,50 @@ int qvkv_pool_evict_lru(qvkv_pool *p, uint64_t target_blocks, uint32_t *released
     return QVKV_OK;
 }
 
+}  // extern "C"
+
+namespace {
+// Compaction mode FILL without a pass over the whole pool: K = the live count; the holes
+// are the free ids below K (ascending, then in the seeded order), the movers the live ids
+// at K or above (ascending); every destination is vacant, so the moves are one batch.
+// Work and memory are O(free ids + table entries), not O(pool).
+int compact_fill(qvkv_pool *p, uint64_t seed, uint64_t *moved, void *stream) {
+    const uint64_t N = p->n_blocks, K = N - p->free.size();
+    std::vector<uint32_t> holes, movers;
+    for (uint32_t b : p->free)
+        if (b < K) holes.push_back(b);
+    std::sort(holes.begin(), holes.end());
+    for (uint64_t b = K; b < N; b++)
+        if (p->refs[b]) movers.push_back((uint32_t)b);
+    if (seed) {
+        uint64_t st = seed;
+        for (uint64_t i = holes.size(); i > 1; i--) std::swap(holes[i - 1], holes[splitmix(st) % i]);
+    }
+    if (int rc = copy_blocks(p, movers, holes, stream)) return rc;
+    // Tables, reference counts and the free list under the new ids.
+    p->tab_gen++;
+    std::vector<uint32_t> to(N - K);
+    for (size_t j = 0; j < movers.size(); j++) to[movers[j] - K] = holes[j];
+    for (auto &s : p->seqs) {
+        if (!s.live) continue;
+        for (auto &l : s.blocks)
+            for (auto &b : l)
+                if (b >= K) b = to[b - K];
+    }
+    for (size_t j = 0; j < movers.size(); j++) {
+        p->refs[holes[j]] = p->refs[movers[j]];
+        p->refs[movers[j]] = 0;
+    }
+    p->free.clear();
+    for (uint64_t b = N; b > K; b--) p->free.push_back((uint32_t)(b - 1));
+    p->moved += movers.size();
+    if (moved) *moved = movers.size();
+    return QVKV_OK;
+}
+}  // namespace
+
+extern "C" {
+
 int qvkv_pool_compact(qvkv_pool *p, uint32_t mode, uint64_t seed, uint64_t *moved,
                       void *stream) {
     if (!p) return err(QVKV_E_SHAPE, "shape mismatch in pool: null argument");
@@ -519,6 +563,7 @@ int qvkv_pool_compact(qvkv_pool *p, uint32_t mode, uint64_t seed, uint64_t *move
         return err(QVKV_E_SHAPE, "shape mismatch in pool: no such compaction mode");
     std::lock_guard<std::mutex> lk(p->mu);
     const uint64_t N = p->n_blocks;
+    if (mode == QVKV_COMPACT_FILL) return compact_fill(p, seed, moved, stream);
     std::vector<uint32_t> live;
     for (uint64_t b = 0; b < N; b++)
         if (p->refs[b]) live.push_back((uint32_t)b);
