@@ -52,6 +52,7 @@ struct AppendItem {
     uint8_t *base;     // its block
     uint32_t rowidx;   // (head, position) row inside the K or V region
     uint32_t i;        // first value's index along d
+    uint32_t row, g;   // source row and KV head
     bool isv, ok;
 };
 
@@ -107,17 +108,27 @@ __device__ __forceinline__ AppendItem append_item(uint32_t w, uint32_t total, ui
         g = e / D;
         it.i = e - g * D;
     }
-    const uint32_t slot = slots[row];
-    const uint32_t blk = geo.fd_b.div(slot);
-    if (blk >= pool_blocks) {  // whole rows: every lane of a q8_0 group agrees
-        flag(err, ERR_BLOCK);
-        return it;
-    }
     it.src = (it.isv ? v : k) + (uint64_t)row * geo.kv_out + g * D + it.i;
-    it.base = pool + (uint64_t)blk * geo.bb;
-    it.rowidx = g * (uint32_t)geo.B + (slot - blk * (uint32_t)geo.B);
+    it.row = row;
+    it.g = g;
     it.ok = true;
     return it;
+}
+
+// The destination of an item whose source loads are in flight: the slot is loaded after
+// them (its latency overlaps theirs: the source address does not depend on it).  A block
+// id past the pool clears ok (whole rows: every lane of a q8_0 group agrees).
+__device__ __forceinline__ void append_dest(AppendItem &it, uint8_t *pool, uint64_t pool_blocks,
+                                            const uint32_t *slots, const Geo &geo, int *err) {
+    const uint32_t slot = slots[it.row];
+    const uint32_t blk = geo.fd_b.div(slot);
+    if (blk >= pool_blocks) {
+        flag(err, ERR_BLOCK);
+        it.ok = false;
+        return;
+    }
+    it.base = pool + (uint64_t)blk * geo.bb;
+    it.rowidx = it.g * (uint32_t)geo.B + (slot - blk * (uint32_t)geo.B);
 }
 
 // U chunks per thread per round, all loads issued before any store.  (64-thread workgroups,
@@ -143,6 +154,9 @@ __global__ __launch_bounds__(T) void k_append(uint8_t *__restrict__ pool, uint64
                 xb[u] = load_f4<NT>(its[u].src + 4);
             }
         }
+#pragma unroll
+        for (int u = 0; u < U; u++)
+            if (its[u].ok) append_dest(its[u], pool, pool_blocks, slots, geo, err);
 #pragma unroll
         for (int u = 0; u < U; u++) {
         if (!its[u].ok) continue;
@@ -389,7 +403,7 @@ __global__ __launch_bounds__(256) void k_append_q8(uint8_t *__restrict__ pool,
         uint8_t *rowk[U];   // the row's first byte in the K or V region
         uint8_t *rows[U];   // the row's first scale
         bool isv[U];
-        uint32_t mm[U];
+        uint32_t mm[U], rowi[U], gi[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
             rowk[u] = nullptr;
@@ -400,16 +414,9 @@ __global__ __launch_bounds__(256) void k_append_q8(uint8_t *__restrict__ pool,
             const uint32_t row = rc.row, g = rc.g, m = rc.m;
             isv[u] = rc.isv;
             mm[u] = m;
-            const uint32_t slot = slots[row];
-            const uint32_t blk = geo.fd_b.div(slot);
-            if (blk >= pool_blocks) {  // whole rows: every lane of a group agrees
-                flag(err, ERR_BLOCK);
-                continue;
-            }
-            const uint32_t rowidx = g * B + (slot - blk * B);
-            uint8_t *base = pool + (uint64_t)blk * geo.bb;
-            rowk[u] = base + (isv[u] ? geo.v_off : geo.k_off) + (uint64_t)rowidx * D;
-            rows[u] = base + (isv[u] ? geo.vs_off : geo.ks_off) + (uint64_t)rowidx * (D / 16);
+            rowk[u] = (uint8_t *)1;  // (placed below, once the source loads are issued)
+            rowi[u] = row;
+            gi[u] = g;
             const float *src = (isv[u] ? v : k) + (uint64_t)row * geo.kv_out + g * D;
             if (!isv[u]) {
                 const float4 a = load_f4<NT>(src + 8u * m), b = load_f4<NT>(src + 8u * m + 4);
@@ -425,6 +432,23 @@ __global__ __launch_bounds__(256) void k_append_q8(uint8_t *__restrict__ pool,
                     x[u][2 * j + 1] = p.y;
                 }
             }
+        }
+        // destinations: the slots load after the sources (the source address does not
+        // depend on them, so the two latencies overlap)
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (!rowk[u]) continue;
+            const uint32_t slot = slots[rowi[u]];
+            const uint32_t blk = geo.fd_b.div(slot);
+            if (blk >= pool_blocks) {  // whole rows: every lane of a group agrees
+                flag(err, ERR_BLOCK);
+                rowk[u] = nullptr;
+                continue;
+            }
+            const uint32_t rowidx = gi[u] * B + (slot - blk * B);
+            uint8_t *base = pool + (uint64_t)blk * geo.bb;
+            rowk[u] = base + (isv[u] ? geo.v_off : geo.k_off) + (uint64_t)rowidx * D;
+            rows[u] = base + (isv[u] ? geo.vs_off : geo.ks_off) + (uint64_t)rowidx * (D / 16);
         }
 #pragma unroll
         for (int u = 0; u < U; u++) {
