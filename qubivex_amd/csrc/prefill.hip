@@ -679,7 +679,6 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
         }
     }
     if (bad_id && lane == 0) flag(err, ERR_BLOCK);  // any wave: each resolves its own half
-    if constexpr (DMA) __syncthreads();  // every wave is past its last tile: slots reusable
     if (!wave_live) return;
     // ---- row totals; lane (col, grp) holds O rows 4 grp + i at d = 16 j + col
     l += __shfl_xor(l, 16);
@@ -687,31 +686,6 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
     float lr[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) lr[i] = __shfl(l, 4 * (int)grp + i);
-    if constexpr (DMA) {
-        // Through LDS, so that each store writes whole rows: the wave's 16 rows x 128
-        // values go into 8 KiB of a free slot (d XOR-swizzled by row & 3 against bank
-        // conflicts; float4 groups stay whole), then each half-wave stores one 512-byte row
-        // per instruction (whole 128-byte lines).
-        float *buf = (float *)(w < 2 ? (w == 0 ? s0.k : s0.v) : (w == 2 ? s1.k : s1.v));
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t r = 4 * grp + (uint32_t)i;
-            const float inv = 1.0f / lr[i];
-#pragma unroll
-            for (int j = 0; j < NDB; j++) buf[r * D + ((16u * j + col) ^ ((r & 3u) << 4))] = acc[j][i] * inv;
-        }
-        // (the same wave reads what it wrote: LDS operations of one wave complete in order)
-        const uint32_t half = lane >> 5, c4 = 4u * (lane & 31u);
-#pragma unroll
-        for (int it = 0; it < 8; it++) {
-            const uint32_t r = 2u * it + half, rr = rw0 + r;
-            if (rr >= nrows) continue;
-            const f4v x = *(const f4v *)(buf + r * D + (c4 ^ ((r & 3u) << 4)));
-            const uint32_t tr = rr / GS, hr = rr % GS;
-            *(f4v *)(out + ((uint64_t)(qa + tr) * H + (uint64_t)g * GS + hr) * D + c4) = x;
-        }
-        return;
-    }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const uint32_t rr = rw0 + 4 * grp + i;
