@@ -541,8 +541,12 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
             }
         };
         // pool offsets of the K and V parts of a block, as values (a per-lane choice
-        // between two kernel-argument fields would otherwise load through a vector address)
-        const uint32_t koff = (uint32_t)geo.k_off, voff = (uint32_t)geo.v_off;
+        // between two kernel-argument fields would otherwise load through a vector address).
+        // Chosen below as `koff + (isv ? kv_gap : 0)`: a per-lane choice between the two
+        // variables themselves became a choice between their addresses, and the compiler
+        // then kept both in scratch memory and read the chosen one back through a pointer
+        // on every tile of the register path.
+        const uint32_t koff = (uint32_t)geo.k_off, kv_gap = (uint32_t)(geo.v_off - geo.k_off);
         // Chunk u of this thread: wave w moves group 4 (w & 1) + u of its half's 8 groups of
         // 64 chunks (4 LDS rows each): groups 0-3 the K rows holding the half's positions
         // (LDS rows {0-3, 4-7, 16-19, 20-23} + 8 half), 4-7 its V rows (16 half + 4 (g - 4)
@@ -565,7 +569,7 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
                 uint32_t pos, piece;
                 bool isv;
                 chunk(c, pos, piece, isv);
-                c_off[u] = (isv ? voff : koff) + ((pos & 15u) * D + piece * 8) * 2u;
+                c_off[u] = (koff + (isv ? kv_gap : 0u)) + ((pos & 15u) * D + piece * 8) * 2u;
                 const uint32_t cc = isv ? c - CH : c;
                 c_lds[u] = __builtin_amdgcn_readfirstlane((cc - lane) * 8);
                 c_v[u] = __builtin_amdgcn_readfirstlane(isv ? 1u : 0u);
@@ -598,8 +602,10 @@ void k_prefill_f16(QV_PREFILL_PARAMS) {
                     uint32_t pos, piece;
                     bool isv;
                     chunk(c, pos, piece, isv);
-                    const uint32_t off = (isv ? voff : koff) + ((pos & 15u) * D + piece * 8) * 2u;
-                    _Float16 *dst = isv ? sl.v : sl.k;
+                    const uint32_t off = (koff + (isv ? kv_gap : 0u)) + ((pos & 15u) * D + piece * 8) * 2u;
+                    // (an offset, not a choice between two pointers: that choice per lane
+                    // had put both pointers in scratch memory, read back on every tile)
+                    _Float16 *dst = sl.k + (isv ? 32u * D : 0u);
                     const uint32_t cc = isv ? c - CH : c;
                     const u4v x = hb != nullptr && (pos & 15u) < valid ? *(const u4v *)(hb + off)
                                                                        : u4v{0u, 0u, 0u, 0u};
