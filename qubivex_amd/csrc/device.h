@@ -16,6 +16,19 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef float f4v __attribute__((ext_vector_type(4)));
+
+// Stores that name the global address space.  A store through a pointer the compiler
+// cannot place (one kept in an array, or chosen by a condition with nullptr) comes out as
+// a flat store, which also counts on the LDS counter: every later LDS wait then waits
+// for the store too.  st_g / st_g_nt (non-temporal) make it a global store.
+template <class T>
+__device__ __forceinline__ void st_g(T *p, T v) {
+    *(__attribute__((address_space(1))) T *)p = v;
+}
+template <class T>
+__device__ __forceinline__ void st_g_nt(T *p, T v) {
+    __builtin_nontemporal_store(v, (__attribute__((address_space(1))) T *)p);
+}
 typedef float f2v __attribute__((ext_vector_type(2)));
 typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 

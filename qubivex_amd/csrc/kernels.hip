@@ -291,8 +291,8 @@ __device__ __forceinline__ uint32_t pack_q4(int a, int b, int c, int d) {
 }
 template <bool NTS>
 __device__ __forceinline__ void st_u2(uint8_t *p, uint32_t a, uint32_t b) {
-    if constexpr (NTS) __builtin_nontemporal_store(u2v{a, b}, (u2v *)p);
-    else *(u2v *)p = u2v{a, b};
+    if constexpr (NTS) st_g_nt((u2v *)p, u2v{a, b});
+    else st_g((u2v *)p, u2v{a, b});
 }
 __device__ __forceinline__ void q8_scale(float amax, float &d, float &inv) {
     d = amax / 127.0f;
@@ -467,7 +467,7 @@ __global__ __launch_bounds__(256) void k_append_q8(uint8_t *__restrict__ pool,
                 for (int t = 0; t < 8; t++) qi[t] = quant_q8(x[u][t], inv);
                 st_u2<NTS>(rowk[u] + (m & 3u) * (D / 4) + (m >> 2) * 8u,
                            pack_q4(qi[0], qi[1], qi[2], qi[3]), pack_q4(qi[4], qi[5], qi[6], qi[7]));
-                if ((m & 3u) == 0) *(_Float16 *)(rows[u] + (m >> 2) * 2u) = (_Float16)d;
+                if ((m & 3u) == 0) st_g((_Float16 *)(rows[u] + (m >> 2) * 2u), (_Float16)d);
             } else {
                 float pm[4];
 #pragma unroll
@@ -529,7 +529,7 @@ __global__ __launch_bounds__(256) void k_append_q8(uint8_t *__restrict__ pool,
                 // D = 256: lane m < 8 holds group 4 (m % 2) + m / 2
                 if (m < D / 32) {
                     const uint32_t grp = D == 256 ? 4u * (m & 1u) + (m >> 1) : m;
-                    *(_Float16 *)(rows[u] + grp * 2u) = (_Float16)dsc;
+                    st_g((_Float16 *)(rows[u] + grp * 2u), (_Float16)dsc);
                 }
             }
         }
@@ -542,8 +542,8 @@ __global__ __launch_bounds__(256) void k_append_q8(uint8_t *__restrict__ pool,
 // Output rows are written with non-temporal stores (a pure stream the kernel never reads
 // back): 5.9-6.2 vs 5.6-5.7 TB/s with plain stores at cfg5.
 __device__ __forceinline__ void store_f8(float *dst, const float *y) {
-    __builtin_nontemporal_store(f4v{y[0], y[1], y[2], y[3]}, (f4v *)dst);
-    __builtin_nontemporal_store(f4v{y[4], y[5], y[6], y[7]}, (f4v *)(dst + 4));
+    st_g_nt((f4v *)dst, f4v{y[0], y[1], y[2], y[3]});
+    st_g_nt((f4v *)(dst + 4), f4v{y[4], y[5], y[6], y[7]});
 }
 
 // T threads per workgroup; UF: loads in flight per thread in the f16 -> f16 copy.
@@ -612,7 +612,7 @@ __global__ __launch_bounds__(T) void k_gather(const uint8_t *__restrict__ pool,
             }
 #pragma unroll
             for (int u = 0; u < U; u++)
-                if (dst[u]) __builtin_nontemporal_store(x[u], (u4v *)dst[u]);
+                if (dst[u]) st_g_nt((u4v *)dst[u], x[u]);
         }
         return;
     }
@@ -648,8 +648,7 @@ __global__ __launch_bounds__(T) void k_gather(const uint8_t *__restrict__ pool,
                 if (!dst[u]) continue;
                 const uint32_t w0 = x[u].x, w1 = x[u].y;
                 const h2 a = __builtin_bit_cast(h2, w0), b = __builtin_bit_cast(h2, w1);
-                __builtin_nontemporal_store(f4v{(float)a.x, (float)a.y, (float)b.x, (float)b.y},
-                                            (f4v *)dst[u]);
+                st_g_nt((f4v *)dst[u], f4v{(float)a.x, (float)a.y, (float)b.x, (float)b.y});
             }
         }
         return;
@@ -670,8 +669,7 @@ __global__ __launch_bounds__(T) void k_gather(const uint8_t *__restrict__ pool,
             const uint4 x = *(const uint4 *)(base + (isv ? geo.v_off : geo.k_off) +
                                               (rowidx * D + e) * 2u);
             if (OUT == QVKV_F16) {
-                __builtin_nontemporal_store(u4v{x.x, x.y, x.z, x.w},
-                                            (u4v *)((uint16_t *)(isv ? out_v : out_k) + o));
+                st_g_nt((u4v *)((uint16_t *)(isv ? out_v : out_k) + o), u4v{x.x, x.y, x.z, x.w});
             } else {
                 h2 a = __builtin_bit_cast(h2, x.x), b = __builtin_bit_cast(h2, x.y);
                 h2 c = __builtin_bit_cast(h2, x.z), d2 = __builtin_bit_cast(h2, x.w);
@@ -715,8 +713,8 @@ __global__ __launch_bounds__(T) void k_gather(const uint8_t *__restrict__ pool,
 template <int D>
 __device__ __forceinline__ void store_run(float *dst, const float *y, int n) {
     if (n == 8) store_f8(dst, y);
-    else if (n == 4) __builtin_nontemporal_store(f4v{y[0], y[1], y[2], y[3]}, (f4v *)dst);
-    else __builtin_nontemporal_store(f2v{y[0], y[1]}, (f2v *)dst);
+    else if (n == 4) st_g_nt((f4v *)dst, f4v{y[0], y[1], y[2], y[3]});
+    else st_g_nt((f2v *)dst, f2v{y[0], y[1]});
 }
 
 // A wave's LDS writes before its reads of other lanes' data, and those reads before the
@@ -824,8 +822,8 @@ __global__ __launch_bounds__(256) void k_gather_q8(const uint8_t *__restrict__ p
                     lds_order();
 #pragma unroll
                     for (uint32_t k = 0; k < 4; k++)
-                        __builtin_nontemporal_store(*(const f4v *)(rowbuf + 32u * k + 4u * j),
-                                                    (f4v *)(dst[u] + 32u * k + 4u * j));
+                        st_g_nt((f4v *)(dst[u] + 32u * k + 4u * j),
+                                *(const f4v *)(rowbuf + 32u * k + 4u * j));
                     lds_order();
                 } else {
 #pragma unroll

@@ -74,10 +74,14 @@ def _device_asm(src, out_dir):
         return f.read()
 
 
-def test_library_kernels_keep_inline_asm_wait_states():
+@pytest.fixture(scope="module")
+def texts():
     with tempfile.TemporaryDirectory() as d:
         with ThreadPoolExecutor(len(B.HIP_SOURCES)) as ex:
-            texts = dict(zip(B.HIP_SOURCES, ex.map(lambda s: _device_asm(s, d), B.HIP_SOURCES)))
+            return dict(zip(B.HIP_SOURCES, ex.map(lambda s: _device_asm(s, d), B.HIP_SOURCES)))
+
+
+def test_library_kernels_keep_inline_asm_wait_states(texts):
     n_kernels = 0
     bad = []
     for src, text in texts.items():
@@ -86,3 +90,17 @@ def test_library_kernels_keep_inline_asm_wait_states():
         bad += [(src,) + tuple(f) for f in H.check_asm(text)]
     assert n_kernels > 50  # every attention, prefill, prelude, append and gather build
     assert bad == [], "\n".join(map(str, bad[:20]))
+
+
+def test_no_kernel_uses_flat_memory_instructions(texts):
+    """Every global access names its address space.  A pointer the compiler cannot place
+    (kept in an array, or chosen by a condition) turns its accesses into flat ones, which
+    also count on the LDS counter, so LDS waits wait for them too; it once did for every
+    output store of the q8_0 gather and append."""
+    bad = []
+    for src, text in texts.items():
+        for name, lines in H.kernels(text).items():
+            n = sum(1 for ln in lines if ln.strip().startswith("flat_"))
+            if n:
+                bad.append((src, name, n))
+    assert bad == [], bad
