@@ -215,7 +215,7 @@ int state_locked(qvkv_dev *dev, hipStream_t stream, StreamState **out) {
         delete st;
         return rc;
     }
-    const int zero[2] = {0, 0};
+    const int zero[64] = {};
     hipError_t e = hipMemcpy(st->d_err, zero, sizeof zero, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
         dev_free(dev, st->d_err, 256);
@@ -358,7 +358,7 @@ int status_of(int bits) {
     if (bits == 16)
         return fail(QVKV_E_UNSUPPORTED,
                     "q8_0 prefill: a value scale above 512 (dequantised values past the f16 "
-                    "range of the MFMA prefill; QVKV_PREFILL_Q8_FAST=0 selects the form "
+                    "range of the MFMA prefill; the knob prefill_q8_fast=0 selects the form "
                     "without that limit)");
     return fail(QVKV_E_SHAPE, "shape mismatch in kv kernel: %s%s%s%s%s",
                 (bits & 1) ? "a block id past the pool; " : "",
@@ -479,7 +479,7 @@ int qvkv_open(int device, qvkv_dev **out) {
         return hip_fail(e, "hipGetSymbolAddress (scratch)");
     }
     {
-        const int zero[2] = {0, 0};
+        const int zero[64] = {};
         if ((e = hipMemcpy(d->scratch, zero, sizeof zero, hipMemcpyHostToDevice)) != hipSuccess) {
             qvkv_close(d);
             return hip_fail(e, "hipMemcpy (scratch error flag)");

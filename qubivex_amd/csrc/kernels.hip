@@ -1806,7 +1806,7 @@ int plan_attention(const Geometry &g, uint32_t n_items, uint32_t heads, uint32_t
                       (uint64_t)n_items * g.G * p->hc * sizeof(StreamRec);
         return QVKV_OK;
     }
-    // Else (QVKV_ATTN_STREAM=0) into context chunks, aiming at about 6 workgroups per CU.
+    // Else (knob attn_stream=0) into context chunks, aiming at about 6 workgroups per CU.
     const uint64_t target = (uint64_t)tune(KNOB_ATTN_TARGET);
     uint64_t nch = units >= full ? 1 : (target + units - 1) / units;
     const uint64_t cap = (max_tiles + 3) / 4;  // at least one tile per wave

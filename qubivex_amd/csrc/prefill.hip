@@ -1159,7 +1159,7 @@ hipError_t launch_prefill(const Geometry &g, const void *pool, uint64_t pool_blo
     hipLaunchKernelGGL((k_prefill_f16<DD, DMA, PS>), dim3(grid2), dim3(256), pad, s, pp,         \
                        pool_blocks, q, blocks, n_table, table_at, pos0, q_at, n_tok, n_seg,     \
                        heads, max_pos, max_tok, q_rows, n_qb, out, geo, err)
-        // P as one f16 (the default) or as high part + residual (QVKV_PREFILL_EXACT_P=1)
+        // P as one f16 (the default) or as high part + residual (knob prefill_exact_p=1)
         const bool ps = tune(KNOB_PREFILL_EXACT_P) != 0;
         if (g.D == 64) { if (ps) QV_PF2(64, false, true); else QV_PF2(64, false, false); }
         else if (tune(KNOB_PREFILL_DMA)) {
