@@ -662,7 +662,7 @@ def run_cfg4(args, dev):
         f"{res['cow_us']:.1f} us ({res['cow_gbs']:.0f} GB/s), repeated {bat_ms:.3f} ms = "
         f"{res['cow_batched_gbs']:.0f} GB/s; evicted {res['evicted_blocks']} blocks; compaction "
         f"(fill) {comp['fill']['moves']} moves in {comp['fill']['gpu_ms']:.3f} ms GPU = "
-        f"{comp['fill']['gbs']:.0f} GB/s ({comp['fill']['wall_ms']:.0f} ms wall); (permute) "
+        f"{comp['fill']['gbs']:.0f} GB/s ({comp['fill']['wall_ms']:.3f} ms wall, planning included); (permute) "
         f"{comp['permute']['moves']} moves in {comp['permute']['gpu_ms']:.3f} ms = "
         f"{comp['permute']['gbs']:.0f} GB/s")
     pool.close()

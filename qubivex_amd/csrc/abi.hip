@@ -1259,7 +1259,7 @@ int qvkv_prelude_attention(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *p
 // compaction copies, whose source rows the caller may have appended asynchronously).
 int qvkv::block_copy_after(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *pool,
                            const uint32_t *src, const uint32_t *dst, uint32_t n, bool ordered,
-                           void *after) {
+                           void *after, void (*overlap)(void *), void *ctx) {
     if (!dev) return fail(QVKV_E_SHAPE, "null device");
     Geometry g;
     if (int rc = geometry(layout, &g)) return rc;
@@ -1289,5 +1289,6 @@ int qvkv::block_copy_after(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *p
                           "block copy launch"))
         return rc;
     time_stop(dev);
+    if (overlap) overlap(ctx);
     return finish_timed(dev);
 }

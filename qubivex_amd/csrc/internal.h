@@ -31,10 +31,11 @@ void set_oom(uint64_t requested, uint64_t used, uint64_t capacity);
 OomDetail last_oom();
 
 // qvkv_block_copy; with `ordered`, the copy runs after the work queued on stream `after`
-// (a hipStream_t; 0 is the null stream) when the call was made.
+// (a hipStream_t; 0 is the null stream) when the call was made.  `overlap(ctx)`, when
+// given, runs on the host once the copy is launched, before the call waits for it.
 int block_copy_after(qvkv_dev *dev, const qvkv_layout *layout, qvkv_buf *pool,
                      const uint32_t *src, const uint32_t *dst, uint32_t n, bool ordered,
-                     void *after);
+                     void *after, void (*overlap)(void *) = nullptr, void *ctx = nullptr);
 
 // Makes the device of `dev` current on the calling thread (QVKV_OK or QVKV_E_DEVICE).
 int use_device(qvkv_dev *dev);
