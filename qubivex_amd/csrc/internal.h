@@ -80,7 +80,7 @@ int plan_attention(const Geometry &g, uint32_t n_items, uint32_t heads, uint32_t
 // starts at its default (the measured best) and changes only through qvkv_tune(); the
 // library reads no environment variable.  X(id, name, default).
 #define QVKV_KNOBS(X)                                                                           \
-    X(APPEND_U, "append_u", 2)                  /* rows per append thread group */              \
+    X(APPEND_U, "append_u", 2)                  /* rows per thread group: 2 (1, 2) or 4 */     \
     X(APPEND_GRID_PER_CU, "append_grid_per_cu", 1 << 20)                                        \
     X(APPEND_NT, "append_nt", -1)               /* non-temporal loads; -1: f16 yes, q8_0 no */   \
     X(APPEND_Q8_FAST, "append_q8_fast", 1)      /* k_append_q8 at d = 64/128/256 */             \

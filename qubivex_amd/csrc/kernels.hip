@@ -1614,7 +1614,12 @@ hipError_t launch_append(const Geometry &g, void *pool, uint64_t pool_blocks, co
                          hipStream_t s) {
     const Geo geo = to_geo(g);
     const uint64_t per_row = 2 * (g.kv_out / 8);
-    const int U = tune(KNOB_APPEND_U);
+    // rows per thread group: the builds are 2 and 4, and the grid follows the build that
+    // runs (3 rows per thread group measured no faster for q8_0 at cfg3: 5.41-5.43 against
+    // 5.38-5.50 TB/s)
+    const bool q8fast = g.dtype == QVKV_Q8_0 && (g.D == 64 || g.D == 128 || g.D == 256) &&
+                        tune(KNOB_APPEND_Q8_FAST) != 0;
+    const int U = tune(KNOB_APPEND_U) <= 2 ? 2 : 4;
     const uint64_t per_cu = (uint64_t)tune(KNOB_APPEND_GRID_PER_CU);
     // f16: non-temporal f32 loads and f16 stores (a pure stream); q8_0 is faster with
     // cached loads (measured at cfg3: 4.78 vs 4.40 TB/s).
@@ -1647,16 +1652,14 @@ hipError_t launch_append(const Geometry &g, void *pool, uint64_t pool_blocks, co
     if (g.D == 64) QV_APPEND_Q8(UU, NN, 64);                                                   \
     else if (g.D == 128) QV_APPEND_Q8(UU, NN, 128);                                            \
     else QV_APPEND_Q8(UU, NN, 256);
-        const bool q8fast = (g.D == 64 || g.D == 128 || g.D == 256) &&
-                            tune(KNOB_APPEND_Q8_FAST) != 0;
-        if (g.dtype == QVKV_Q8_0 && q8fast) {
+        if (q8fast) {
             // cached loads, non-temporal stores (measured at cfg3: 5.50 / 5.57 TB/s with cached
             // / non-temporal stores, 5.3 with non-temporal loads; 2 chunks per thread ahead of 4)
             const int mode = (NT ? 1 : 0) | (tune(KNOB_APPEND_NTS) ? 2 : 0);
 #define QV_APPEND_Q8_M(UU)                                                                     \
     if (mode == 0) { QV_APPEND_Q8_D(UU, 0) } else if (mode == 1) { QV_APPEND_Q8_D(UU, 1) }     \
     else if (mode == 2) { QV_APPEND_Q8_D(UU, 2) } else { QV_APPEND_Q8_D(UU, 3) }
-            if (U <= 2) { QV_APPEND_Q8_M(2) } else { QV_APPEND_Q8_M(4) }
+            if (U == 2) { QV_APPEND_Q8_M(2) } else { QV_APPEND_Q8_M(4) }
 #undef QV_APPEND_Q8_M
         } else if (g.dtype == QVKV_F16) {
             QV_APPEND_U(QVKV_F16)

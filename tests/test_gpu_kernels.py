@@ -131,6 +131,21 @@ def test_append_q8_0_bit_exact(hip, G, D):
             assert (got[name] == want_q).all(), f"row {i} {name} values"
 
 
+@pytest.mark.parametrize("knob", [("append_u", 1), ("append_u", 4), ("append_nt", 1),
+                                  ("append_nt", 0), ("append_nts", 0)],
+                         ids=lambda kv: f"{kv[0]}={kv[1]}")
+@pytest.mark.parametrize("dtype", [F16, Q8_0])
+def test_append_builds_are_bit_exact(hip, dtype, knob, knobs):
+    """Every append build a knob selects (rows per thread group, cached or non-temporal loads
+    and stores) stores the same bytes as the oracle, over 3 layouts each."""
+    knobs(*knob)
+    for G, D in [(8, 128), (4, 64), (3, 96)]:
+        if dtype == F16:
+            test_append_f16_bit_exact(hip, G, D)
+        else:
+            test_append_q8_0_bit_exact(hip, G, D)
+
+
 def fill_items(hip, L, pool, N, lens, r, outliers=0.0):
     """Appends every position of every item through its table; returns rows and tables."""
     blocks, table_at = random_tables(r, lens, L.block, N)
